@@ -1,0 +1,262 @@
+"""ctypes loader for the C oracle (test infrastructure only).
+
+Only the tests, ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` import this
+module. It is the checker that the HIP product path is compared against and never part of it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libpw_oracle.so")
+_lib = None
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_sz = ctypes.c_size_t
+
+
+class PwoExpert(ctypes.Structure):
+    _fields_ = [
+        ("gate_w", _u8p), ("gate_s", _f32p),
+        ("up_w", _u8p), ("up_s", _f32p),
+        ("down_w", _u8p), ("down_s", _f32p),
+    ]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        L.pwo_decode_e4m3fn.argtypes = [ctypes.c_uint8]
+        L.pwo_decode_e4m3fn.restype = ctypes.c_float
+        L.pwo_round_bf16.argtypes = [ctypes.c_float]
+        L.pwo_round_bf16.restype = ctypes.c_float
+        L.pwo_encode_e4m3fn.argtypes = [ctypes.c_float, _u8p]
+        L.pwo_encode_e4m3fn.restype = ctypes.c_int
+        L.pwo_sleef_expf_u10.argtypes = [ctypes.c_float]
+        L.pwo_sleef_expf_u10.restype = ctypes.c_float
+        L.pwo_sigmoid_f32.argtypes = [ctypes.c_float]
+        L.pwo_sigmoid_f32.restype = ctypes.c_float
+        L.pwo_dynamic_fp8.argtypes = [_f32p, _sz, _sz, _u8p, _f32p, _f32p]
+        L.pwo_gemm_mode_a.argtypes = [_u8p, _f32p, _sz, _sz, _f32p, _sz, _f32p]
+        L.pwo_gemm_mode_b_equation.argtypes = [_u8p, _f32p, _sz, _sz, _u8p, _f32p, _sz, _f32p]
+        L.pwo_fp8_linear_mode_b.argtypes = [_u8p, _f32p, _sz, _sz, _f32p, _sz, _f32p]
+        L.pwo_swiglu_f32.argtypes = [_f32p, _f32p, _f32p, _sz]
+        L.pwo_swiglu_f32.restype = None
+        L.pwo_swiglu_bf16_staged.argtypes = [_f32p, _f32p, _f32p, _sz]
+        L.pwo_swiglu_bf16_staged.restype = None
+        L.pwo_topk_unsorted.argtypes = [_f32p, _sz, _sz, _u32p]
+        L.pwo_noaux_routes.argtypes = [_f32p, _f32p, _sz, _sz, _u32p, _f32p, _u64p]
+        L.pwo_router_logits_lane64.argtypes = [_f32p, _sz, _f32p, _sz, _sz, _f32p]
+        L.pwo_router_logits_lane64.restype = None
+        L.pwo_route.argtypes = [_f32p, _sz, _f32p, _f32p, _sz, _sz, _f32p, _f32p, _u32p, _f32p, _u64p]
+        for name in ("pwo_moe_layer_mode_a", "pwo_moe_layer_mode_b"):
+            getattr(L, name).argtypes = [_f32p, _sz, _sz, _sz, ctypes.POINTER(PwoExpert), _sz,
+                                         _u32p, _f32p, _sz, _f32p]
+        L.pwo_expert_mode_a.argtypes = [_f32p, _sz, _sz, _sz, ctypes.POINTER(PwoExpert), _f32p, _f32p]
+        for name in ("pwo_full_qkv_source_row", "pwo_full_qkv_scale_row", "pwo_swa_qkv_source_row"):
+            getattr(L, name).argtypes = [ctypes.c_int64]
+            getattr(L, name).restype = ctypes.c_int64
+        _lib = L
+    return _lib
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def decode_e4m3fn(b: int) -> float:
+    return lib().pwo_decode_e4m3fn(b)
+
+
+def round_bf16(v: float) -> float:
+    return lib().pwo_round_bf16(v)
+
+
+def encode_e4m3fn(v: float):
+    out = ctypes.c_uint8(0)
+    rc = lib().pwo_encode_e4m3fn(v, ctypes.byref(out))
+    return None if rc != 0 else out.value
+
+
+def sleef_expf_u10(v: float) -> float:
+    return lib().pwo_sleef_expf_u10(v)
+
+
+def sigmoid_f32(v: float) -> float:
+    return lib().pwo_sigmoid_f32(v)
+
+
+def dynamic_fp8(x: np.ndarray):
+    x = _c(x, np.float32)
+    rows, cols = x.shape
+    codes = np.zeros((rows, cols), np.uint8)
+    scales = np.zeros((rows, cols // 128), np.float32)
+    deq = np.zeros((rows, cols), np.float32)
+    rc = lib().pwo_dynamic_fp8(_p(x, _f32p), rows, cols, _p(codes, _u8p), _p(scales, _f32p), _p(deq, _f32p))
+    if rc != 0:
+        raise ValueError(f"dynamic_fp8 failed: {rc}")
+    return codes, scales, deq
+
+
+def gemm_mode_a(w: np.ndarray, s: np.ndarray, x: np.ndarray) -> np.ndarray:
+    w = _c(w, np.uint8); s = _c(s, np.float32); x = _c(np.atleast_2d(x), np.float32)
+    n, k = w.shape
+    y = np.zeros((x.shape[0], n), np.float32)
+    rc = lib().pwo_gemm_mode_a(_p(w, _u8p), _p(s, _f32p), n, k, _p(x, _f32p), x.shape[0], _p(y, _f32p))
+    if rc != 0:
+        raise ValueError(f"gemm_mode_a failed: {rc}")
+    return y
+
+
+def gemm_mode_b_equation(w, s, q, a) -> np.ndarray:
+    w = _c(w, np.uint8); s = _c(s, np.float32); q = _c(q, np.uint8); a = _c(a, np.float32)
+    n, k = w.shape
+    y = np.zeros((q.shape[0], n), np.float32)
+    rc = lib().pwo_gemm_mode_b_equation(_p(w, _u8p), _p(s, _f32p), n, k, _p(q, _u8p), _p(a, _f32p),
+                                        q.shape[0], _p(y, _f32p))
+    if rc != 0:
+        raise ValueError(f"gemm_mode_b_equation failed: {rc}")
+    return y
+
+
+def fp8_linear_mode_b(w, s, x) -> np.ndarray:
+    w = _c(w, np.uint8); s = _c(s, np.float32); x = _c(np.atleast_2d(x), np.float32)
+    n, k = w.shape
+    y = np.zeros((x.shape[0], n), np.float32)
+    rc = lib().pwo_fp8_linear_mode_b(_p(w, _u8p), _p(s, _f32p), n, k, _p(x, _f32p), x.shape[0], _p(y, _f32p))
+    if rc != 0:
+        raise ValueError(f"fp8_linear_mode_b failed: {rc}")
+    return y
+
+
+def swiglu_f32(g, u):
+    g = _c(g, np.float32); u = _c(u, np.float32)
+    out = np.zeros_like(g)
+    lib().pwo_swiglu_f32(_p(g, _f32p), _p(u, _f32p), _p(out, _f32p), g.size)
+    return out
+
+
+def swiglu_bf16_staged(g, u):
+    g = _c(g, np.float32); u = _c(u, np.float32)
+    out = np.zeros_like(g)
+    lib().pwo_swiglu_bf16_staged(_p(g, _f32p), _p(u, _f32p), _p(out, _f32p), g.size)
+    return out
+
+
+def topk_unsorted(values, k=8):
+    v = _c(values, np.float32)
+    sel = np.zeros(k, np.uint32)
+    rc = lib().pwo_topk_unsorted(_p(v, _f32p), v.size, k, _p(sel, _u32p))
+    if rc != 0:
+        raise ValueError(f"topk failed: {rc}")
+    return sel
+
+
+def noaux_routes(scores, bias):
+    scores = _c(np.atleast_2d(scores), np.float32); bias = _c(bias, np.float32)
+    rows, experts = scores.shape
+    sel = np.zeros((rows, 8), np.uint32)
+    w = np.zeros((rows, 8), np.float32)
+    ties = ctypes.c_uint64(0)
+    rc = lib().pwo_noaux_routes(_p(scores, _f32p), _p(bias, _f32p), rows, experts, _p(sel, _u32p),
+                                _p(w, _f32p), ctypes.byref(ties))
+    if rc != 0:
+        raise ValueError(f"noaux routes failed: {rc}")
+    return sel, w, ties.value
+
+
+def router_logits_lane64(x, router_w):
+    x = _c(np.atleast_2d(x), np.float32); r = _c(router_w, np.float32)
+    out = np.zeros((x.shape[0], r.shape[0]), np.float32)
+    lib().pwo_router_logits_lane64(_p(x, _f32p), x.shape[0], _p(r, _f32p), r.shape[0], r.shape[1], _p(out, _f32p))
+    return out
+
+
+def route(x, router_w, bias):
+    x = _c(np.atleast_2d(x), np.float32); r = _c(router_w, np.float32); b = _c(bias, np.float32)
+    rows, experts, k = x.shape[0], r.shape[0], r.shape[1]
+    logits = np.zeros((rows, experts), np.float32)
+    scores = np.zeros((rows, experts), np.float32)
+    sel = np.zeros((rows, 8), np.uint32)
+    w = np.zeros((rows, 8), np.float32)
+    ties = ctypes.c_uint64(0)
+    rc = lib().pwo_route(_p(x, _f32p), rows, _p(r, _f32p), _p(b, _f32p), experts, k, _p(logits, _f32p),
+                         _p(scores, _f32p), _p(sel, _u32p), _p(w, _f32p), ctypes.byref(ties))
+    if rc != 0:
+        raise ValueError(f"route failed: {rc}")
+    return logits, scores, sel, w, ties.value
+
+
+def _expert_array(experts: dict, n_experts: int):
+    """experts: {id: (gate_w, gate_s, up_w, up_s, down_w, down_s)} numpy arrays."""
+    arr = (PwoExpert * n_experts)()
+    keep = []
+    for e, (gw, gs, uw, us, dw, ds) in experts.items():
+        t = [_c(gw, np.uint8), _c(gs, np.float32), _c(uw, np.uint8), _c(us, np.float32),
+             _c(dw, np.uint8), _c(ds, np.float32)]
+        keep.extend(t)
+        arr[e] = PwoExpert(_p(t[0], _u8p), _p(t[1], _f32p), _p(t[2], _u8p), _p(t[3], _f32p),
+                           _p(t[4], _u8p), _p(t[5], _f32p))
+    return arr, keep
+
+
+def moe_layer(mode: str, x, experts: dict, n_experts: int, selected, weights, hidden=None, inter=None):
+    x = _c(np.atleast_2d(x), np.float32)
+    rows = x.shape[0]
+    hidden = hidden or x.shape[1]
+    any_e = next(iter(experts.values()))
+    inter = inter or any_e[0].shape[0]
+    sel = _c(selected, np.uint32); w = _c(weights, np.float32)
+    arr, keep = _expert_array(experts, n_experts)
+    out = np.zeros((rows, hidden), np.float32)
+    fn = lib().pwo_moe_layer_mode_a if mode == "a" else lib().pwo_moe_layer_mode_b
+    rc = fn(_p(x, _f32p), rows, hidden, inter, arr, n_experts, _p(sel, _u32p), _p(w, _f32p),
+            sel.shape[1], _p(out, _f32p))
+    del keep
+    if rc != 0:
+        raise ValueError(f"moe_layer_mode_{mode} failed: {rc}")
+    return out
+
+
+def expert_mode_a(x, expert):
+    x = _c(np.atleast_2d(x), np.float32)
+    rows, hidden = x.shape
+    arr, keep = _expert_array({0: expert}, 1)
+    inter = expert[0].shape[0]
+    out32 = np.zeros((rows, hidden), np.float32)
+    outbf = np.zeros((rows, hidden), np.float32)
+    rc = lib().pwo_expert_mode_a(_p(x, _f32p), rows, hidden, inter, arr, _p(out32, _f32p), _p(outbf, _f32p))
+    del keep
+    if rc != 0:
+        raise ValueError(f"expert_mode_a failed: {rc}")
+    return out32, outbf
+
+
+def full_qkv_source_row(r: int) -> int:
+    return lib().pwo_full_qkv_source_row(r)
+
+
+def full_qkv_scale_row(r: int) -> int:
+    return lib().pwo_full_qkv_scale_row(r)
+
+
+def swa_qkv_source_row(r: int) -> int:
+    return lib().pwo_swa_qkv_source_row(r)

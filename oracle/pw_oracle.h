@@ -1,0 +1,120 @@
+/*
+ * CPU oracle for the block-scaled FP8 projection and routed-MoE path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library restates, in plain single-threaded C, the reference
+ * (x3haloed/mimo-prismwing) CPU numerics for the path. It is the checker that the HIP product is
+ * compared against: only the tests, the smoke check and the benchmark's CPU-baseline leg load it.
+ * The product library never links, loads or calls it.
+ *
+ * Every function cites the reference file:line it follows. Build: `make -C oracle` (gcc,
+ * -ffp-contract=off so that a*b+c is never fused, matching Rust's default semantics).
+ *
+ * Pinning status (what checks each function independently of a retyped formula):
+ *   pwo_decode_e4m3fn        golden f8-e4m3fn-all-bytes.json (all 256 bytes) + real block fixture
+ *   pwo_round_bf16           golden pw0054-bf16-boundary.json (532 inputs incl. NaN/Inf)
+ *   pwo_encode_e4m3fn        golden pw0053 codes; brute-force nearest search near every midpoint
+ *   pwo_dynamic_fp8          golden pw0053-dynamic-fp8-activation.json (scales, codes, dequant bits)
+ *   pwo_gemm_mode_a          real mtp-gate-fp8-gemv.json (abs 2e-7), closed form 384/896, f64 brute force
+ *   pwo_gemm_mode_b_equation closed-form probe inputs vs f64 brute force; equals mode A when the
+ *                            activation codes are exact and scales are 1
+ *   pwo_fp8_linear_mode_b    f64 brute force on tiny shapes; bf16-rounding idempotence
+ *   pwo_swiglu_f32           golden swiglu-f32.json (f64 oracle)
+ *   pwo_sleef_expf_u10       golden pw0068-sleef-boundaries.json; pw0062 via the sigmoid
+ *   pwo_sigmoid_f32          golden pw0062-router-sigmoid.json, pw0068
+ *   pwo_topk_unsorted        golden pw0063-topk-order.json + 5 tie cases of pw0157 (order and set)
+ *   pwo_noaux_routes         pw0157 tie counting; weights sum to 1 within 1e-6; tiny-MoE fixture set
+ *   pwo_router_logits_lane64 f64 brute force (tolerance) — summation order is this build's declared
+ *                            order; the reference's (Apple Accelerate SGEMM) is unknowable
+ *   pwo_moe_layer_mode_a/_b  schedule bijection + exact reconstruction with one-hot weights; f64
+ *                            brute force on tiny shapes; moe-noaux-tc-swiglu.json structure
+ *   pwo_full/swa_qkv_*       known-answer row/scale maps of src/text_endpoint.rs:13686-13732
+ */
+#ifndef PW_ORACLE_H
+#define PW_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- scalar numerics ---------------------------------------------------------------------- */
+float pwo_decode_e4m3fn(uint8_t bits);
+float pwo_round_bf16(float value);
+/* 0 on success, -1 when value is non-finite or |value| > 448 */
+int pwo_encode_e4m3fn(float value, uint8_t *out);
+float pwo_sleef_expf_u10(float d);
+float pwo_sigmoid_f32(float value);
+
+/* ---- dynamic activation quantiser (per row, per 128-column group) ------------------------- */
+/* codes [rows*cols], scales [rows*cols/128], dequantized [rows*cols] (any may be NULL) */
+int pwo_dynamic_fp8(const float *input, size_t rows, size_t cols, uint8_t *codes, float *scales,
+                    float *dequantized);
+
+/* ---- projections --------------------------------------------------------------------------- */
+/* Mode A: y[p, r] = sum_c dec(W[r, c]) * S[r/128, c/128] * x[p, c], f32, sequential over c.
+ * W [n x k] e4m3fn, S [ceil(n/128) x k/128] f32, x [rows x k] f32 -> y [rows x n] f32.
+ * Returns -1 on shape error, -2 on non-finite input/scale/weight (0x7f/0xff), -3 non-finite out. */
+int pwo_gemm_mode_a(const uint8_t *w, const float *s, size_t n, size_t k, const float *x,
+                    size_t rows, float *y);
+/* Block-scaled equation of the GPU mode-B kernels:
+ * y[p, r] = sum_b (sum_{c in b} dec(W) * dec(q[p, c])) * S[r/128, b] * a[p, b], blocks ascending. */
+int pwo_gemm_mode_b_equation(const uint8_t *w, const float *s, size_t n, size_t k,
+                             const uint8_t *q, const float *a, size_t rows, float *y);
+/* fp8_linear: quantise->dequantise x per 128 group, dequantise W, f32 GEMM (sequential k), bf16. */
+int pwo_fp8_linear_mode_b(const uint8_t *w, const float *s, size_t n, size_t k, const float *x,
+                          size_t rows, float *y);
+
+/* ---- SwiGLU --------------------------------------------------------------------------------- */
+void pwo_swiglu_f32(const float *gate, const float *up, float *out, size_t count);
+void pwo_swiglu_bf16_staged(const float *gate, const float *up, float *out, size_t count);
+
+/* ---- router ---------------------------------------------------------------------------------- */
+/* libc++ std::nth_element(first, first+k-1, last, greater-by-value) over (value, index) pairs,
+ * returning the first k indices in partition order. -1 on bad arguments. */
+int pwo_topk_unsorted(const float *values, size_t count, size_t top_k, uint32_t *selected);
+/* noaux-tc routes: scores [rows x 256] (sigmoid outputs), bias [256] -> selected [rows x 8],
+ * weights [rows x 8]; *tie_rows counts rows whose selected boundary equals the best rejected. */
+int pwo_noaux_routes(const float *scores, const float *bias, size_t rows, size_t experts,
+                     uint32_t *selected, float *weights, uint64_t *tie_rows);
+/* Router logits in the declared lane-64 order: for each (p, e) 64 partial sums, partial l
+ * accumulating k = l, l+64, ... with fmaf, then the halving tree 32,16,8,4,2,1. */
+void pwo_router_logits_lane64(const float *x, size_t rows, const float *router_w, size_t experts,
+                              size_t k, float *logits);
+/* Full route: logits (lane-64) -> sigmoid -> noaux routes. */
+int pwo_route(const float *x, size_t rows, const float *router_w, const float *bias,
+              size_t experts, size_t k, float *logits, float *scores, uint32_t *selected,
+              float *weights, uint64_t *tie_rows);
+
+/* ---- routed MoE layer ------------------------------------------------------------------------- */
+typedef struct {
+    const uint8_t *gate_w; const float *gate_s;  /* [inter x hidden], [inter/128 x hidden/128] */
+    const uint8_t *up_w;   const float *up_s;
+    const uint8_t *down_w; const float *down_s;  /* [hidden x inter], [hidden/128 x inter/128] */
+} pwo_expert;
+
+/* experts: array indexed by expert id (entries of unrouted experts may hold NULL pointers).
+ * selected/weights: [rows x top_k]. Output [rows x hidden] bf16-rounded f32.
+ * Mode A = the reference's f32 CPU control (src/lib.rs:5807-5862): f32 activations, f32 SwiGLU,
+ * f32 expert outputs, f32 weighted combine in ascending expert id, bf16 at the end.
+ * Mode B = routed_mlp_traced (src/text_endpoint.rs:5290-5381) over fp8_linear. */
+int pwo_moe_layer_mode_a(const float *x, size_t rows, size_t hidden, size_t inter,
+                         const pwo_expert *experts, size_t n_experts, const uint32_t *selected,
+                         const float *weights, size_t top_k, float *out);
+int pwo_moe_layer_mode_b(const float *x, size_t rows, size_t hidden, size_t inter,
+                         const pwo_expert *experts, size_t n_experts, const uint32_t *selected,
+                         const float *weights, size_t top_k, float *out);
+/* One complete expert in mode A (config "one routed expert"): y = bf16(down(swiglu(gate x, up x))). */
+int pwo_expert_mode_a(const float *x, size_t rows, size_t hidden, size_t inter,
+                      const pwo_expert *expert, float *out_f32, float *out_bf16);
+
+/* ---- QKV tensor-parallel layouts ---------------------------------------------------------------- */
+int64_t pwo_full_qkv_source_row(int64_t logical_row);
+int64_t pwo_full_qkv_scale_row(int64_t logical_row);
+int64_t pwo_swa_qkv_source_row(int64_t logical_row);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
