@@ -1,0 +1,150 @@
+// Device helpers for gfx950 (CDNA4): MFMA operand types, FP8 -> bf16 conversion, bf16 splitting,
+// wave reductions, and the shared plan structures used by the kernels and the host runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pw_numerics.h"
+
+namespace pw {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
+
+// 16-byte load of data read once (weights): a global (not flat) load, so it is counted only by
+// the vector-memory counter, with the nontemporal hint so it does not displace reused lines.
+__device__ __forceinline__ uint4 load_stream16(const void *p)
+{
+    const u32x4 v = __builtin_nontemporal_load((global_u32x4 *)p);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// 16-byte global load of reused data (activations, partial sums).
+__device__ __forceinline__ uint4 load_global16(const void *p)
+{
+    const u32x4 v = *(global_u32x4 *)p;
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// Error bits raised by kernels into the runtime's device error word. The low bits keep the
+// meaning of the reference's Metal error word (kernels/block_fp8_gemv.metal, bits 1..128).
+enum : uint32_t {
+    FLAG_LANES = 1u,
+    FLAG_QUANT_NONFINITE = 2u,
+    FLAG_SWIGLU_NONFINITE = 4u,
+    FLAG_REDUCE_NONFINITE = 16u,
+    FLAG_ROUND_NONFINITE = 32u,
+    FLAG_FUSED_SWIGLU_NONFINITE = 128u,
+    FLAG_SCHEDULE = 256u,
+    FLAG_OUTPUT_NONFINITE = 512u,
+};
+
+// A 16-row output tile of a projection: weight rows [w, w + 16*K), one scale row (all 16 rows sit
+// in one 128-row scale block), output rows [out_row, out_row + valid).
+struct ProjTile {
+    const uint8_t *w;
+    const float *s;
+    uint32_t out_row;
+    uint32_t valid;
+};
+
+// Per-expert device pointers of a routed-expert bank.
+struct ExpertPtrs {
+    const uint8_t *gate_w;
+    const float *gate_s;
+    const uint8_t *up_w;
+    const float *up_s;
+    const uint8_t *down_w;
+    const float *down_s;
+};
+
+// One routed expert's entry of the device schedule: its weights and its placement slots
+// [off, off + cnt). Entries past the last routed expert have cnt = 0.
+struct ActiveExpert {
+    ExpertPtrs ep;
+    uint32_t off;
+    uint32_t cnt;
+    uint32_t pad[2];
+};
+
+// Device-side routed schedule (ascending expert id, positions ascending per expert), the
+// layout of the reference's BTreeMap<expert, [(position, weight)]> (src/text_endpoint.rs:4767-4775).
+struct MoePlan {
+    uint32_t n_active;        // U, distinct routed experts
+    uint32_t n_placements;    // rows * top_k
+    uint32_t max_count;       // largest placement count of any expert
+    uint32_t pad;
+};
+
+// MFMA wrappers (gfx950). 16x16 output tile, lane l holds D[4*(l/16)+i][l%16], i = 0..3.
+__device__ __forceinline__ f32x4 mfma_bf16_16x16x32(bf16x8 a, bf16x8 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// FP8 (OCP e4m3fn) x FP8, K = 128 per instruction, E8M0 scales fixed at 2^0.
+__device__ __forceinline__ f32x4 mfma_fp8_16x16x128(i32x8 a, i32x8 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// Eight e4m3fn bytes (two dwords) -> eight bf16 (exact: e4m3 values are bf16 values).
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t lo, uint32_t hi)
+{
+    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
+    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
+    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
+    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
+    bf16x8 r;
+    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
+    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
+    return r;
+}
+
+__device__ __forceinline__ __bf16 bf16_from_bits(uint16_t u) { return __builtin_bit_cast(__bf16, u); }
+
+// f32 -> three bf16 planes with x == hi + mid + lo exactly (normal range): each remainder is
+// exact in f32 (the operands are within a factor of two) and the last one has at most 8
+// significant bits. Mode A feeds all three planes to the bf16 MFMA so products stay exact and
+// only the f32 accumulation order differs from the reference.
+__device__ __forceinline__ uint16_t rne_bf16_bits(float v)
+{
+    const uint32_t b = f32_bits(v);
+    return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ void split3_bf16(float x, uint16_t &hi, uint16_t &mid, uint16_t &lo)
+{
+    hi = rne_bf16_bits(x);
+    const float r1 = x - f32_from((uint32_t)hi << 16);
+    mid = rne_bf16_bits(r1);
+    const float r2 = r1 - f32_from((uint32_t)mid << 16);
+    lo = rne_bf16_bits(r2);
+}
+
+// Eight bf16 from a 16-byte word (bf16 activations are used as they are).
+__device__ __forceinline__ bf16x8 bf16x8_from_u4(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ bool finite_f32(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
+
+// Butterfly max over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v = fmaxf(v, __shfl_xor(v, offset, 64));
+    return v;
+}
+
+__device__ __forceinline__ void raise_flag(uint32_t *flags, uint32_t bit)
+{
+    if (flags)
+        __hip_atomic_fetch_or(flags, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace pw

@@ -1,0 +1,143 @@
+// Host-side launchers of the gfx950 kernels (internal to the library; the public surface is the
+// C ABI in include/pwfp8.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pw_device.h"
+
+namespace pw {
+
+// Kernels whose launches can be timed with HIP events (benchmark diagnostics).
+enum KernelId : uint32_t {
+    K_LINEAR_A = 0,
+    K_LINEAR_B,
+    K_QUANT,
+    K_MOE_SCHEDULE,
+    K_MOE_GATEUP,
+    K_MOE_DOWN,
+    K_MOE_COMBINE,
+    K_PREFILL_GATEUP,
+    K_PREFILL_DOWN,
+    K_ROUTER,
+    K_COUNT
+};
+
+// Optional event recorder: when enabled, each timed launch records a start and a stop event on
+// the stream it is launched on. Summaries synchronise and sum hipEventElapsedTime per kernel.
+struct KernelTimer {
+    bool enabled = false;
+    uint32_t capacity = 0, used = 0;
+    hipEvent_t *events = nullptr;  // [2 * capacity]
+    uint32_t *ids = nullptr;       // [capacity]
+    int begin(uint32_t id, hipStream_t s)
+    {
+        if (!enabled || used >= capacity)
+            return -1;
+        const int slot = (int)used++;
+        ids[slot] = id;
+        (void)hipEventRecord(events[2 * slot], s);
+        return slot;
+    }
+    void end(int slot, hipStream_t s)
+    {
+        if (slot >= 0)
+            (void)hipEventRecord(events[2 * slot + 1], s);
+    }
+};
+
+// Per-layer device scratch of the routed-MoE launch, sized for `max_rows` token rows.
+struct MoeBuffers {
+    MoePlan *plan;
+    uint32_t *active_expert;   // [E]
+    uint32_t *active_offset;   // [E + 1]
+    uint32_t *placement_pos;   // [rows * 8]
+    float *placement_w;        // [rows * 8]
+    uint32_t *row_slots;       // [rows * 8]
+    float *hidden;             // [rows * 8 * I]      mode B bf16-staged SwiGLU output
+    uint16_t *hidden_planes;   // [3][rows * 8][I]    mode A SwiGLU output as exact bf16 planes
+    uint16_t *x_planes;        // [3][rows][H]        mode A f32 activations as bf16 planes
+    float *y;                  // [rows * 8 * H]
+    ActiveExpert *active;      // [E]   per routed expert: weights, placement slots
+    float *partial;            // split-K partial sums of the mode A projections
+    uint32_t *counters;        // [E * max(I, H) / 64] split-K arrival counters
+    uint32_t n_counters;
+    uint8_t *xq;               // [rows * H]      mode B activation codes
+    float *xs;                 // [rows * H/128]  mode B activation scales
+    uint8_t *hq;               // [rows * 8 * I]
+    float *hs;                 // [rows * 8 * I/128]
+    uint32_t max_rows;
+    uint32_t experts;
+};
+
+// Arguments of the split-K mode A expert projection (pw_moe_a.hip).
+struct SplitArgs {
+    const ActiveExpert *active;
+    const uint32_t *placement_pos;  // gate/up: token row per placement slot; down: null (rows = slots)
+    const uint16_t *x;              // activation planes [NS][rows][K]
+    size_t x_plane;
+    uint32_t K, R, KS, rows, P;     // columns, weight rows, K splits, activation rows, placements
+    float *partial;                 // [KS][MATS][P][R]
+    uint32_t *counters;             // [active][R / 64]
+    uint16_t *hidden;               // gate/up output: three bf16 planes [3][P][R]
+    size_t h_plane;
+    float *y;                       // down output [P][R]
+    uint32_t *flags;
+};
+
+struct SplitPlan {
+    uint32_t bpw, kc, ks;
+    size_t lds;
+};
+
+// K split of a mode A expert projection with K columns, NS activation planes and up to max_cnt
+// routed rows per expert.
+SplitPlan plan_split(uint32_t K, int ns, uint32_t max_cnt);
+void launch_moe_a_split(int mats, int ns, int nt, const SplitArgs &args, const SplitPlan &sp,
+                        uint32_t max_active, hipStream_t stream);
+
+// The runtime points this at its timer for the duration of one ABI call (calls on a runtime are
+// serialised by the caller, and each thread has its own pointer).
+extern thread_local KernelTimer *tl_timer;
+inline int timer_begin(uint32_t id, hipStream_t s) { return tl_timer ? tl_timer->begin(id, s) : -1; }
+inline void timer_end(int slot, hipStream_t s)
+{
+    if (tl_timer)
+        tl_timer->end(slot, s);
+}
+
+int pick_ksplit(uint32_t n_tiles, uint32_t blocks);
+
+// x: `planes` bf16 planes [planes][W][K] (1: bf16 activations, 3: f32 split by launch_split_planes)
+void launch_linear_a(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, int planes,
+                     uint32_t W, uint32_t K, float *y32, uint16_t *y16, uint32_t N,
+                     uint32_t round_f32, hipStream_t stream);
+void launch_split_planes(const float *x, uint32_t n, uint16_t *planes, hipStream_t stream);
+void launch_linear_b(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *codes,
+                     const float *scales, uint32_t W, uint32_t K, float *y32, uint16_t *y16,
+                     uint32_t N, uint32_t round_f32, hipStream_t stream);
+void launch_quant_group128(const void *x, bool x_f32, uint32_t rows, uint32_t K, uint8_t *codes,
+                           float *scales, uint32_t *flags, hipStream_t stream);
+
+void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
+                         uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
+                         uint32_t *flags, hipStream_t stream);
+void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
+                      bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
+                      uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
+                      hipStream_t stream);
+
+void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, uint32_t expert, const MoeBuffers &mb,
+                           const void *x, bool x_f32, uint32_t rows, uint32_t H, uint32_t I,
+                           float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream);
+
+// Seeded synthetic data for benchmarks and tests (counter-based, reproducible on one device).
+void launch_synth_fp8(uint8_t *w, const float *scales, uint64_t rows, uint64_t cols, uint64_t seed,
+                      hipStream_t stream);
+void launch_synth_scales(float *s, uint64_t count, uint64_t seed, float log2_lo, float log2_hi,
+                         hipStream_t stream);
+void launch_synth_normal_bf16(uint16_t *x, uint64_t count, uint64_t seed, float stddev,
+                              hipStream_t stream);
+
+}  // namespace pw

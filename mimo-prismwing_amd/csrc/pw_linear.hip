@@ -1,0 +1,380 @@
+// Block-scaled FP8 projections for decode widths (1..32 activation rows) on gfx950.
+//
+// Mode A (FP8 weight x f32/bf16 activation, f32 accumulation) follows the reference's
+// block_fp8_gemv_parallel_lut_blocked / block_fp8_gemm{1..8}_shared_weight_lut_blocked
+// (kernels/block_fp8_gemv.metal:665-703, :751-800, :855-933) and its CPU twin mapped_fp8_gemv
+// (src/lib.rs:1272-1309). Mode B (dynamic FP8 activation, block-scaled) follows
+// block_fp8_gemm{1..32}_sglang_blockscaled (kernels/block_fp8_gemv.metal:935-1046).
+//
+// Design: a 64-lane wave owns a 16-row output tile. Each lane streams 16 (mode A) or 32 (mode B)
+// weight bytes of one row per instruction, so one wave-load covers 16 rows x 64 (128) contiguous
+// bytes. Mode A converts e4m3 to bf16 exactly (v_cvt_scalef32_pk_bf16_fp8) and feeds
+// v_mfma_f32_16x16x32_bf16 with the activation rows as the 16-wide N operand; f32 activations
+// are split once into three bf16 planes (hi + mid + lo == x exactly), so every product is exact
+// and only the f32 accumulation order differs from the reference. Mode B feeds
+// the e4m3 codes of weights and activations straight into v_mfma_scale_f32_16x16x128_f8f6f4:
+// one instruction is one 128-column scale block. The 128x128 block scale (and in mode B the
+// per-token activation scale) is applied to the f32 block partial in registers. The waves of a
+// workgroup split K and are reduced through LDS in a fixed order, so results are deterministic.
+// Decode widths are HBM-bound; MFMA is used because f32 VALU FMA (no packed math) cannot reach
+// 8 TB/s x 8 rows x 2 FLOP/B.
+#include "pw_device.h"
+#include "pw_launch.h"
+
+namespace pw {
+
+template <int NT>
+struct Acc {
+    f32x4 v[NT];
+};
+
+// ------------------------------------------------------------------------------------ mode A
+// Activations arrive as NS bf16 planes [NS][W][K] (NS = 1: bf16 input; NS = 3: an f32 input split
+// exactly into hi + mid + lo), so the inner loop does no conversion work on them.
+template <int NS, int KSPLIT, int NT>
+__global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
+    const ProjTile *__restrict__ tiles, uint32_t n_tiles, const uint16_t *__restrict__ x, uint32_t W,
+    uint32_t K, float *__restrict__ y_f32, uint16_t *__restrict__ y_bf16, uint32_t N,
+    uint32_t round_f32)
+{
+    const size_t plane = (size_t)W * K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane >> 4, r16 = lane & 15;
+    __shared__ f32x4 red[KSPLIT > 1 ? KSPLIT : 1][NT][64];
+    const uint32_t blocks = K >> 7;
+    const uint32_t b_begin = wave * blocks / KSPLIT, b_end = (wave + 1) * blocks / KSPLIT;
+
+    for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+        const ProjTile tile = tiles[t];
+        const bool row_ok = (uint32_t)r16 < tile.valid;
+        const uint8_t *wrow = tile.w + (size_t)r16 * K;
+        f32x4 total[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+            total[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        for (uint32_t b = b_begin; b < b_end; ++b) {
+            f32x4 acc[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const uint32_t col = (b << 7) + half * 64 + q * 16;
+                uint4 wv = make_uint4(0, 0, 0, 0);
+                if (row_ok)
+                    wv = load_stream16(wrow + col);
+                const bf16x8 a0 = fp8x8_to_bf16x8(wv.x, wv.y);
+                const bf16x8 a1 = fp8x8_to_bf16x8(wv.z, wv.w);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const uint32_t token = nt * 16 + r16;
+#pragma unroll
+                    for (int s = 0; s < NS; ++s) {
+                        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+                        if (token < W) {
+                            const uint4 *xp = (const uint4 *)(x + s * plane + (size_t)token * K + col);
+                            x0 = xp[0];
+                            x1 = xp[1];
+                        }
+                        acc[nt] = mfma_bf16_16x16x32(a0, bf16x8_from_u4(x0), acc[nt]);
+                        acc[nt] = mfma_bf16_16x16x32(a1, bf16x8_from_u4(x1), acc[nt]);
+                    }
+                }
+            }
+            const float sc = tile.s[b];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    total[nt][i] = __builtin_fmaf(sc, acc[nt][i], total[nt][i]);
+        }
+
+        if constexpr (KSPLIT > 1) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                red[wave][nt][lane] = total[nt];
+            __syncthreads();
+            if (wave == 0) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    f32x4 s = red[0][nt][lane];
+                    for (int w = 1; w < KSPLIT; ++w) {
+                        const f32x4 o = red[w][nt][lane];
+                        s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
+                    }
+                    total[nt] = s;
+                }
+            }
+        }
+        if (wave == 0) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const uint32_t token = nt * 16 + r16;
+                if (token >= W)
+                    continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t row = q * 4 + i;
+                    if (row >= tile.valid)
+                        continue;
+                    const size_t at = (size_t)token * N + tile.out_row + row;
+                    const float v = total[nt][i];
+                    if (y_f32)
+                        y_f32[at] = round_f32 ? round_bf16(v) : v;
+                    if (y_bf16)
+                        y_bf16[at] = bf16_bits(v);
+                }
+            }
+        }
+        if constexpr (KSPLIT > 1)
+            __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------------------------ mode B
+template <int KSPLIT, int NT>
+__global__ __launch_bounds__(64 * KSPLIT) void linear_b_kernel(
+    const ProjTile *__restrict__ tiles, uint32_t n_tiles, const uint8_t *__restrict__ codes,
+    const float *__restrict__ act_scales, uint32_t W, uint32_t K, float *__restrict__ y_f32,
+    uint16_t *__restrict__ y_bf16, uint32_t N, uint32_t round_f32)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane >> 4, r16 = lane & 15;
+    __shared__ f32x4 red[KSPLIT > 1 ? KSPLIT : 1][NT][64];
+    const uint32_t blocks = K >> 7;
+    const uint32_t b_begin = wave * blocks / KSPLIT, b_end = (wave + 1) * blocks / KSPLIT;
+
+    for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+        const ProjTile tile = tiles[t];
+        const bool row_ok = (uint32_t)r16 < tile.valid;
+        const uint8_t *wrow = tile.w + (size_t)r16 * K;
+        f32x4 total[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+            total[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t b = b_begin; b < b_end; ++b) {
+            const uint32_t col = (b << 7) + q * 32;
+            uint4 w0 = make_uint4(0, 0, 0, 0), w1 = w0;
+            if (row_ok) {
+                w0 = load_stream16(wrow + col);
+                w1 = load_stream16(wrow + col + 16);
+            }
+            const i32x8 wa = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                              (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+            const float sw = tile.s[b];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const uint32_t token = nt * 16 + r16;
+                uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
+                float sa = 0.f;
+                if (token < W) {
+                    const uint4 *cp = (const uint4 *)(codes + (size_t)token * K + col);
+                    c0 = cp[0];
+                    c1 = cp[1];
+                    sa = act_scales[(size_t)token * blocks + b];
+                }
+                const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
+                                  (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
+                const f32x4 p = mfma_fp8_16x16x128(wa, xb, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    total[nt][i] = __builtin_fmaf(p[i] * sw, sa, total[nt][i]);
+            }
+        }
+        if constexpr (KSPLIT > 1) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+                red[wave][nt][lane] = total[nt];
+            __syncthreads();
+            if (wave == 0) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    f32x4 s = red[0][nt][lane];
+                    for (int w = 1; w < KSPLIT; ++w) {
+                        const f32x4 o = red[w][nt][lane];
+                        s[0] += o[0]; s[1] += o[1]; s[2] += o[2]; s[3] += o[3];
+                    }
+                    total[nt] = s;
+                }
+            }
+        }
+        if (wave == 0) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const uint32_t token = nt * 16 + r16;
+                if (token >= W)
+                    continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t row = q * 4 + i;
+                    if (row >= tile.valid)
+                        continue;
+                    const size_t at = (size_t)token * N + tile.out_row + row;
+                    const float v = total[nt][i];
+                    if (y_f32)
+                        y_f32[at] = round_f32 ? round_bf16(v) : v;
+                    if (y_bf16)
+                        y_bf16[at] = bf16_bits(v);
+                }
+            }
+        }
+        if constexpr (KSPLIT > 1)
+            __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ dynamic FP8 quantiser
+// dynamic_fp8_quantized_group128 (kernels/block_fp8_gemv.metal:84-137) and its CPU authority
+// dynamic_fp8_activations (src/text_endpoint.rs:3008-3051): one wave per (row, 128-group), two
+// values per lane; scale = max(absmax, 1e-10) / 448; code = nearest e4m3 of clamp(x/scale).
+// A non-finite input raises FLAG_QUANT_NONFINITE and counts as 0 in the group maximum.
+template <typename T>
+__device__ __forceinline__ float load_act(const T *p, size_t i);
+template <>
+__device__ __forceinline__ float load_act<float>(const float *p, size_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_act<uint16_t>(const uint16_t *p, size_t i)
+{
+    return f32_from((uint32_t)p[i] << 16);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quant_group128_kernel(const T *__restrict__ x, uint32_t rows,
+                                                             uint32_t K, uint8_t *__restrict__ codes,
+                                                             float *__restrict__ scales,
+                                                             uint32_t *flags)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t groups_per_row = K >> 7;
+    const uint32_t group = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (group >= rows * groups_per_row)
+        return;
+    const size_t base = (size_t)group * 128 + lane * 2;
+    float v0 = load_act<T>(x, base), v1 = load_act<T>(x, base + 1);
+    const bool f0 = finite_f32(v0), f1 = finite_f32(v1);
+    if (!(f0 && f1))
+        raise_flag(flags, FLAG_QUANT_NONFINITE);
+    float m = fmaxf(f0 ? fabsf(v0) : 0.f, f1 ? fabsf(v1) : 0.f);
+    m = wave_max(m);
+    const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
+    if (lane == 0)
+        scales[group] = scale;
+    float n0 = v0 / scale, n1 = v1 / scale;
+    n0 = n0 < -448.f ? -448.f : (n0 > 448.f ? 448.f : n0);
+    n1 = n1 < -448.f ? -448.f : (n1 > 448.f ? 448.f : n1);
+    const uint16_t packed = (uint16_t)encode_e4m3fn_rne(f0 ? n0 : 0.f) |
+                            ((uint16_t)encode_e4m3fn_rne(f1 ? n1 : 0.f) << 8);
+    *(uint16_t *)(codes + base) = packed;
+}
+
+// f32 [n] -> bf16 planes hi [n], mid [n], lo [n] with x == hi + mid + lo.
+__global__ __launch_bounds__(256) void split_planes_kernel(const float *__restrict__ x, uint32_t n,
+                                                           uint16_t *__restrict__ planes)
+{
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n)
+        return;
+    uint16_t h, m, l;
+    split3_bf16(x[i], h, m, l);
+    planes[i] = h;
+    planes[n + i] = m;
+    planes[2 * (size_t)n + i] = l;
+}
+
+// ------------------------------------------------------------------------------- launchers
+static int grid_for(uint32_t n_tiles, uint32_t max_grid)
+{
+    return (int)(n_tiles < max_grid ? n_tiles : max_grid);
+}
+
+void launch_split_planes(const float *x, uint32_t n, uint16_t *planes, hipStream_t stream)
+{
+    hipLaunchKernelGGL(split_planes_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, n, planes);
+}
+
+template <int NS, int KSPLIT>
+static void launch_a_ks(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, uint32_t W,
+                        uint32_t K, float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32,
+                        hipStream_t stream)
+{
+    const int grid = grid_for(n_tiles, 65535);
+    if (W <= 16)
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1>), dim3(grid), dim3(64 * KSPLIT), 0,
+                           stream, tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+    else
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 2>), dim3(grid), dim3(64 * KSPLIT), 0,
+                           stream, tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+}
+
+int pick_ksplit(uint32_t n_tiles, uint32_t blocks)
+{
+    // enough waves to cover 256 CUs several times over; every wave keeps >= 2 blocks
+    if (n_tiles < 512 && blocks % 8 == 0 && blocks >= 16)
+        return 8;
+    if (blocks % 4 == 0 && blocks >= 8)
+        return 4;
+    if (blocks % 2 == 0)
+        return 2;
+    return 1;
+}
+
+void launch_linear_a(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, int planes,
+                     uint32_t W, uint32_t K, float *y32, uint16_t *y16, uint32_t N,
+                     uint32_t round_f32, hipStream_t stream)
+{
+    const int ks = pick_ksplit(n_tiles, K >> 7);
+    const int t = timer_begin(K_LINEAR_A, stream);
+#define PW_A(NS, KS) launch_a_ks<NS, KS>(tiles, n_tiles, x, W, K, y32, y16, N, round_f32, stream)
+    if (planes == 3) {
+        if (ks == 8) PW_A(3, 8); else if (ks == 4) PW_A(3, 4); else if (ks == 2) PW_A(3, 2); else PW_A(3, 1);
+    } else {
+        if (ks == 8) PW_A(1, 8); else if (ks == 4) PW_A(1, 4); else if (ks == 2) PW_A(1, 2); else PW_A(1, 1);
+    }
+#undef PW_A
+    timer_end(t, stream);
+}
+
+template <int KSPLIT>
+static void launch_b_ks(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *codes,
+                        const float *scales, uint32_t W, uint32_t K, float *y32, uint16_t *y16,
+                        uint32_t N, uint32_t round_f32, hipStream_t stream)
+{
+    const int grid = grid_for(n_tiles, 65535);
+    if (W <= 16)
+        hipLaunchKernelGGL((linear_b_kernel<KSPLIT, 1>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
+                           tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32);
+    else
+        hipLaunchKernelGGL((linear_b_kernel<KSPLIT, 2>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
+                           tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32);
+}
+
+void launch_linear_b(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *codes,
+                     const float *scales, uint32_t W, uint32_t K, float *y32, uint16_t *y16,
+                     uint32_t N, uint32_t round_f32, hipStream_t stream)
+{
+    const int ks = pick_ksplit(n_tiles, K >> 7);
+    const int t = timer_begin(K_LINEAR_B, stream);
+    if (ks == 8) launch_b_ks<8>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
+    else if (ks == 4) launch_b_ks<4>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
+    else if (ks == 2) launch_b_ks<2>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
+    else launch_b_ks<1>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
+    timer_end(t, stream);
+}
+
+void launch_quant_group128(const void *x, bool x_f32, uint32_t rows, uint32_t K, uint8_t *codes,
+                           float *scales, uint32_t *flags, hipStream_t stream)
+{
+    const uint32_t groups = rows * (K >> 7);
+    const int grid = (int)((groups + 3) / 4);
+    const int t = timer_begin(K_QUANT, stream);
+    if (x_f32)
+        hipLaunchKernelGGL(quant_group128_kernel<float>, dim3(grid), dim3(256), 0, stream,
+                           (const float *)x, rows, K, codes, scales, flags);
+    else
+        hipLaunchKernelGGL(quant_group128_kernel<uint16_t>, dim3(grid), dim3(256), 0, stream,
+                           (const uint16_t *)x, rows, K, codes, scales, flags);
+    timer_end(t, stream);
+}
+
+}  // namespace pw

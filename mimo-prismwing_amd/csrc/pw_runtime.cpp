@@ -1,0 +1,1281 @@
+// C-ABI runtime for the gfx950 block-FP8 projection and routed-MoE path (include/pwfp8.h).
+//
+// Mirrors WideMetalMoeRuntime (src/wide_metal_moe.rs:113-1315): same call surface, same
+// fail-closed validation, same outputs (bf16-rounded f32). What differs is the memory model:
+// weights are bound once into HBM (pw_projection / pw_expert_bank) instead of wrapping mmapped
+// pages per call, and device-resident entry points let a caller keep activations and routes in
+// HBM across calls.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/pwfp8.h"
+#include "pw_launch.h"
+#include "pw_numerics.h"
+
+using pw::ExpertPtrs;
+using pw::MoeBuffers;
+using pw::ProjTile;
+
+namespace pw {
+thread_local KernelTimer *tl_timer = nullptr;
+}
+
+namespace {
+
+const char *const kKernelNames[pw::K_COUNT] = {
+    "linear_a", "linear_b", "quant", "moe_schedule", "moe_gateup", "moe_down", "moe_combine",
+    "prefill_gateup", "prefill_down", "router"};
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+#define PW_HIP(call)                                                                            \
+    do {                                                                                        \
+        hipError_t e_ = (call);                                                                 \
+        if (e_ != hipSuccess)                                                                   \
+            return fail(PW_ERR_DEVICE, "%s failed: %s", #call, hipGetErrorString(e_));          \
+    } while (0)
+
+double now_ms()
+{
+    return std::chrono::duration<double, std::milli>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+bool finite(float v) { return std::isfinite(v); }
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    ~DevBuf() { release(); }
+    void release()
+    {
+        if (p)
+            (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    hipError_t ensure(size_t need)
+    {
+        if (need <= bytes)
+            return hipSuccess;
+        release();
+        hipError_t e = hipMalloc(&p, need);
+        if (e == hipSuccess)
+            bytes = need;
+        return e;
+    }
+};
+
+}  // namespace
+
+struct pw_runtime {
+    int device = 0;
+    uint32_t flags = 0;
+    hipStream_t stream = nullptr;
+    uint32_t *d_flags = nullptr;
+    // scratch: host-call staging and mode-B activation codes
+    DevBuf in, out, codes, scales, route_ids, route_w, bank_table;
+    // routed-MoE per-layer scratch
+    DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
+        moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
+        moe_active, moe_partial, moe_counters;
+    MoeBuffers mb{};
+    pw::KernelTimer timer;
+};
+
+namespace {
+
+// Points the launchers at the runtime's event timer for the duration of one ABI call.
+struct TimerScope {
+    explicit TimerScope(pw_runtime *rt) { pw::tl_timer = rt && rt->timer.enabled ? &rt->timer : nullptr; }
+    ~TimerScope() { pw::tl_timer = nullptr; }
+};
+
+void free_timer(pw::KernelTimer &t)
+{
+    if (t.events) {
+        for (uint32_t i = 0; i < 2 * t.capacity; ++i)
+            (void)hipEventDestroy(t.events[i]);
+        delete[] t.events;
+    }
+    delete[] t.ids;
+    t = pw::KernelTimer{};
+}
+
+}  // namespace
+
+struct pw_projection {
+    pw_runtime *rt = nullptr;
+    uint8_t *w = nullptr;       // device weight base
+    float *s = nullptr;         // device scale base
+    bool owns = false;
+    uint32_t rows = 0, columns = 0;
+    ProjTile *tiles = nullptr;  // device tile table
+    uint32_t n_tiles = 0;
+    uint64_t weight_bytes = 0, scale_bytes = 0;
+};
+
+struct pw_expert_bank {
+    pw_runtime *rt = nullptr;
+    ExpertPtrs *table = nullptr;  // device [E]
+    uint32_t n_experts = 0, hidden = 0, intermediate = 0;
+};
+
+namespace {
+
+hipError_t set_device(pw_runtime *rt) { return hipSetDevice(rt->device); }
+
+// 16-row tiles of one segment: rows [src_row, src_row + rows) of a weight with `columns`
+// columns, scale rows scale_base + r/128, output rows out_row + r.
+void add_segment_tiles(std::vector<ProjTile> &tiles, const uint8_t *w, const float *s,
+                       uint32_t columns, uint64_t src_row, uint32_t rows, uint64_t scale_base,
+                       uint32_t out_row)
+{
+    const uint32_t scale_cols = columns / 128;
+    for (uint32_t r = 0; r < rows; r += 16) {
+        ProjTile t;
+        t.w = w + (src_row + r) * (uint64_t)columns;
+        t.s = s + (scale_base + r / 128) * scale_cols;
+        t.out_row = out_row + r;
+        t.valid = std::min<uint32_t>(16, rows - r);
+        tiles.push_back(t);
+    }
+}
+
+int upload_tiles(pw_projection *p, const std::vector<ProjTile> &tiles)
+{
+    PW_HIP(hipMalloc(&p->tiles, tiles.size() * sizeof(ProjTile)));
+    PW_HIP(hipMemcpy(p->tiles, tiles.data(), tiles.size() * sizeof(ProjTile), hipMemcpyHostToDevice));
+    p->n_tiles = (uint32_t)tiles.size();
+    return PW_OK;
+}
+
+const uint8_t *region_tensor(const pw_region &r) { return (const uint8_t *)r.bytes + r.tensor_offset; }
+
+int check_region(const pw_region &r, size_t expect, const char *what)
+{
+    if (!r.bytes)
+        return fail(PW_ERR_ARGUMENT, "%s region is null", what);
+    if (r.tensor_offset + r.tensor_bytes > r.region_bytes && r.region_bytes != 0)
+        return fail(PW_ERR_LAYOUT, "%s tensor overruns its region", what);
+    if (r.tensor_bytes != expect)
+        return fail(PW_ERR_LAYOUT, "%s is %zu bytes, expected %zu (layout mismatch)", what,
+                    r.tensor_bytes, expect);
+    return PW_OK;
+}
+
+int check_weight_codes(const uint8_t *w, size_t n)
+{
+    for (size_t i = 0; i < n; ++i)
+        if (w[i] == 0x7f || w[i] == 0xff)
+            return fail(PW_ERR_NONFINITE, "non-finite FP8 weight at byte offset %zu", i);
+    return PW_OK;
+}
+
+int check_scales(const float *s, size_t n)
+{
+    for (size_t i = 0; i < n; ++i)
+        if (!finite(s[i]))
+            return fail(PW_ERR_NONFINITE, "FP8 scale %zu is non-finite", i);
+    return PW_OK;
+}
+
+bool all_bf16_exact(const float *x, size_t n)
+{
+    for (size_t i = 0; i < n; ++i)
+        if (pw::f32_bits(x[i]) & 0xffffu)
+            return false;
+    return true;
+}
+
+// Upload a host f32 activation block, as bf16 when every value is a bf16 value (exact), else
+// as f32 (the kernels then split it into bf16 hi + lo).
+int stage_input(pw_runtime *rt, const float *x, size_t n, bool &is_f32)
+{
+    is_f32 = !all_bf16_exact(x, n);
+    if (is_f32) {
+        PW_HIP(rt->in.ensure(n * 4));
+        PW_HIP(hipMemcpyAsync(rt->in.p, x, n * 4, hipMemcpyHostToDevice, rt->stream));
+    } else {
+        std::vector<uint16_t> h(n);
+        for (size_t i = 0; i < n; ++i)
+            h[i] = (uint16_t)(pw::f32_bits(x[i]) >> 16);
+        PW_HIP(rt->in.ensure(n * 2));
+        PW_HIP(hipMemcpyAsync(rt->in.p, h.data(), n * 2, hipMemcpyHostToDevice, rt->stream));
+        PW_HIP(hipStreamSynchronize(rt->stream));  // h is released on return
+    }
+    return PW_OK;
+}
+
+int reset_flags(pw_runtime *rt)
+{
+    PW_HIP(hipMemsetAsync(rt->d_flags, 0, sizeof(uint32_t), rt->stream));
+    return PW_OK;
+}
+
+int read_flags(pw_runtime *rt, uint32_t &flags)
+{
+    PW_HIP(hipMemcpyAsync(&flags, rt->d_flags, sizeof(uint32_t), hipMemcpyDeviceToHost, rt->stream));
+    PW_HIP(hipStreamSynchronize(rt->stream));
+    return PW_OK;
+}
+
+#define PW_TRY(expr)                 \
+    do {                             \
+        int s_ = (expr);             \
+        if (s_ != PW_OK)             \
+            return s_;               \
+    } while (0)
+
+int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I)
+{
+    const size_t P = (size_t)rows * 8;
+    PW_HIP(rt->moe_plan.ensure(sizeof(pw::MoePlan)));
+    PW_HIP(rt->moe_active_expert.ensure((E + 1) * 4));
+    PW_HIP(rt->moe_active_offset.ensure((E + 1) * 4));
+    PW_HIP(rt->moe_pos.ensure(P * 4));
+    PW_HIP(rt->moe_w.ensure(P * 4));
+    PW_HIP(rt->moe_slots.ensure(P * 4));
+    PW_HIP(rt->moe_hidden.ensure(P * I * 4));
+    PW_HIP(rt->moe_hidden_planes.ensure(3 * P * I * 2));
+    PW_HIP(rt->moe_x_planes.ensure(3 * (size_t)rows * H * 2));
+    PW_HIP(rt->moe_y.ensure(P * H * 4));
+    PW_HIP(rt->moe_xq.ensure((size_t)rows * H));
+    PW_HIP(rt->moe_xs.ensure((size_t)rows * (H / 128) * 4));
+    PW_HIP(rt->moe_hq.ensure(P * I));
+    PW_HIP(rt->moe_hs.ensure(P * (I / 128) * 4));
+    // split-K partials of the mode A projections, sized for the widest split the launch can pick
+    const uint32_t cnt = std::min<uint32_t>(rows, 32);
+    const size_t ks_gu = std::max(pw::plan_split(H, 1, cnt).ks, pw::plan_split(H, 3, cnt).ks);
+    const size_t ks_d = pw::plan_split(I, 3, cnt).ks;
+    PW_HIP(rt->moe_active.ensure((size_t)(E + 1) * sizeof(pw::ActiveExpert)));
+    PW_HIP(rt->moe_partial.ensure(std::max(ks_gu * 2 * P * I, ks_d * P * H) * 4));
+    const uint32_t n_counters = E * (std::max(I, H) / 64);
+    PW_HIP(rt->moe_counters.ensure((size_t)n_counters * 4));
+    MoeBuffers &mb = rt->mb;
+    mb.active = (pw::ActiveExpert *)rt->moe_active.p;
+    mb.partial = (float *)rt->moe_partial.p;
+    mb.counters = (uint32_t *)rt->moe_counters.p;
+    mb.n_counters = n_counters;
+    mb.plan = (pw::MoePlan *)rt->moe_plan.p;
+    mb.active_expert = (uint32_t *)rt->moe_active_expert.p;
+    mb.active_offset = (uint32_t *)rt->moe_active_offset.p;
+    mb.placement_pos = (uint32_t *)rt->moe_pos.p;
+    mb.placement_w = (float *)rt->moe_w.p;
+    mb.row_slots = (uint32_t *)rt->moe_slots.p;
+    mb.hidden = (float *)rt->moe_hidden.p;
+    mb.hidden_planes = (uint16_t *)rt->moe_hidden_planes.p;
+    mb.x_planes = (uint16_t *)rt->moe_x_planes.p;
+    mb.y = (float *)rt->moe_y.p;
+    mb.xq = (uint8_t *)rt->moe_xq.p;
+    mb.xs = (float *)rt->moe_xs.p;
+    mb.hq = (uint8_t *)rt->moe_hq.p;
+    mb.hs = (float *)rt->moe_hs.p;
+    mb.max_rows = rows;
+    mb.experts = E;
+    return PW_OK;
+}
+
+// ---- libc++ std::nth_element over (value, index) pairs, greater-by-value ---------------------
+// The reference's top-k (src/pytorch_topk.cpp:8-30) is std::nth_element(first, first + k - 1,
+// last) from the C++ library PyTorch was built with (libc++ for the golden orders). This is that
+// published algorithm: median-of-three, guarded Hoare partition that tracks the pivot, the
+// all-equal fallback partition, the already-partitioned check, selection sort below 8 elements.
+struct Entry {
+    float v;
+    int64_t i;
+};
+
+inline bool greater(const Entry &a, const Entry &b) { return a.v > b.v; }
+
+unsigned sort3(Entry *x, Entry *y, Entry *z)
+{
+    if (!greater(*y, *x)) {
+        if (!greater(*z, *y))
+            return 0;
+        std::swap(*y, *z);
+        if (greater(*y, *x)) {
+            std::swap(*x, *y);
+            return 2;
+        }
+        return 1;
+    }
+    if (greater(*z, *y)) {
+        std::swap(*x, *z);
+        return 1;
+    }
+    std::swap(*x, *y);
+    if (greater(*z, *y)) {
+        std::swap(*y, *z);
+        return 2;
+    }
+    return 1;
+}
+
+void select_sort(Entry *first, Entry *last)
+{
+    for (Entry *lm1 = last - 1; first != lm1; ++first) {
+        Entry *best = first;
+        for (Entry *it = first + 1; it != last; ++it)
+            if (greater(*it, *best))
+                best = it;
+        if (best != first)
+            std::swap(*first, *best);
+    }
+}
+
+void nth_element_cxx(Entry *first, Entry *nth, Entry *last)
+{
+    for (;;) {
+        if (nth == last)
+            return;
+        const ptrdiff_t len = last - first;
+        if (len <= 1)
+            return;
+        if (len == 2) {
+            if (greater(last[-1], *first))
+                std::swap(*first, last[-1]);
+            return;
+        }
+        if (len == 3) {
+            sort3(first, first + 1, last - 1);
+            return;
+        }
+        if (len <= 7) {
+            select_sort(first, last);
+            return;
+        }
+        Entry *m = first + len / 2, *lm1 = last - 1;
+        unsigned swaps = sort3(first, m, lm1);
+        Entry *i = first, *j = lm1;
+        if (!greater(*i, *m)) {
+            bool guard = false;
+            while (!(i == --j)) {
+                if (greater(*j, *m)) {
+                    guard = true;
+                    break;
+                }
+            }
+            if (guard) {
+                std::swap(*i, *j);
+                ++swaps;
+            } else {
+                ++i;
+                j = last;
+                if (!greater(*first, *--j)) {
+                    for (;; ++i) {
+                        if (i == j)
+                            return;
+                        if (greater(*first, *i)) {
+                            std::swap(*i, *j);
+                            ++swaps;
+                            ++i;
+                            break;
+                        }
+                    }
+                }
+                if (i == j)
+                    return;
+                for (;;) {
+                    while (!greater(*first, *i))
+                        ++i;
+                    do
+                        --j;
+                    while (greater(*first, *j));
+                    if (i >= j)
+                        break;
+                    std::swap(*i, *j);
+                    ++swaps;
+                    ++i;
+                }
+                if (nth < i)
+                    return;
+                first = i;
+                continue;
+            }
+        }
+        ++i;
+        if (i < j) {
+            for (;;) {
+                while (greater(*i, *m))
+                    ++i;
+                do
+                    --j;
+                while (!greater(*j, *m));
+                if (i >= j)
+                    break;
+                std::swap(*i, *j);
+                ++swaps;
+                if (m == i)
+                    m = j;
+                ++i;
+            }
+        }
+        if (i != m && greater(*m, *i)) {
+            std::swap(*i, *m);
+            ++swaps;
+        }
+        if (nth == i)
+            return;
+        if (swaps == 0) {
+            Entry *a = nth < i ? first : i, *end = nth < i ? i : last, *prev = a;
+            bool sorted = true;
+            while (++a != end) {
+                if (greater(*a, *prev)) {
+                    sorted = false;
+                    break;
+                }
+                prev = a;
+            }
+            if (sorted)
+                return;
+        }
+        if (nth < i)
+            last = i;
+        else
+            first = i + 1;
+    }
+}
+
+}  // namespace
+
+// ===================================================================================== C ABI
+extern "C" {
+
+const char *pw_last_error(void) { return g_error.c_str(); }
+
+int pw_abi_version(void) { return PW_ABI_VERSION; }
+
+int pw_runtime_create(int device, uint32_t flags, pw_runtime **out)
+{
+    if (!out)
+        return fail(PW_ERR_ARGUMENT, "null output handle");
+    *out = nullptr;
+    int count = 0;
+    PW_HIP(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count)
+        return fail(PW_ERR_ARGUMENT, "device %d out of range (%d devices)", device, count);
+    hipDeviceProp_t prop;
+    PW_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(PW_ERR_DEVICE, "device %d is %s; this library is built for gfx950", device,
+                    prop.gcnArchName);
+    pw_runtime *rt = new pw_runtime;
+    rt->device = device;
+    rt->flags = flags;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess)
+        e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking);
+    if (e == hipSuccess)
+        e = hipMalloc((void **)&rt->d_flags, sizeof(uint32_t));
+    if (e == hipSuccess)
+        e = hipMemset(rt->d_flags, 0, sizeof(uint32_t));
+    if (e != hipSuccess) {
+        pw_runtime_destroy(rt);
+        return fail(PW_ERR_DEVICE, "runtime setup failed: %s", hipGetErrorString(e));
+    }
+    *out = rt;
+    return PW_OK;
+}
+
+void pw_runtime_destroy(pw_runtime *rt)
+{
+    if (!rt)
+        return;
+    (void)hipSetDevice(rt->device);
+    if (rt->stream)
+        (void)hipStreamSynchronize(rt->stream);
+    if (rt->d_flags)
+        (void)hipFree(rt->d_flags);
+    free_timer(rt->timer);
+    if (rt->stream)
+        (void)hipStreamDestroy(rt->stream);
+    delete rt;
+}
+
+int pw_runtime_enable_timing(pw_runtime *rt, uint32_t max_launches)
+{
+    if (!rt)
+        return fail(PW_ERR_ARGUMENT, "null runtime");
+    PW_HIP(set_device(rt));
+    PW_HIP(hipDeviceSynchronize());
+    free_timer(rt->timer);
+    if (max_launches == 0)
+        return PW_OK;
+    pw::KernelTimer &t = rt->timer;
+    t.events = new hipEvent_t[2 * max_launches]();
+    t.ids = new uint32_t[max_launches]();
+    for (uint32_t i = 0; i < 2 * max_launches; ++i) {
+        hipError_t e = hipEventCreate(&t.events[i]);
+        if (e != hipSuccess) {
+            t.capacity = i / 2;
+            free_timer(t);
+            return fail(PW_ERR_DEVICE, "hipEventCreate failed: %s", hipGetErrorString(e));
+        }
+    }
+    t.capacity = max_launches;
+    t.used = 0;
+    t.enabled = true;
+    return PW_OK;
+}
+
+int pw_runtime_timing_summary(pw_runtime *rt, const char *kernel, uint32_t *launches, double *total_ms)
+{
+    if (!rt || !kernel || !launches || !total_ms)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    uint32_t id = pw::K_COUNT;
+    for (uint32_t k = 0; k < pw::K_COUNT; ++k)
+        if (std::strcmp(kernel, kKernelNames[k]) == 0)
+            id = k;
+    if (id == pw::K_COUNT)
+        return fail(PW_ERR_ARGUMENT, "unknown kernel name '%s'", kernel);
+    PW_HIP(set_device(rt));
+    PW_HIP(hipDeviceSynchronize());
+    *launches = 0;
+    *total_ms = 0.0;
+    const pw::KernelTimer &t = rt->timer;
+    for (uint32_t i = 0; i < t.used; ++i) {
+        if (t.ids[i] != id)
+            continue;
+        float ms = 0.f;
+        PW_HIP(hipEventElapsedTime(&ms, t.events[2 * i], t.events[2 * i + 1]));
+        *launches += 1;
+        *total_ms += ms;
+    }
+    return PW_OK;
+}
+
+int pw_runtime_timing_reset(pw_runtime *rt)
+{
+    if (!rt)
+        return fail(PW_ERR_ARGUMENT, "null runtime");
+    PW_HIP(set_device(rt));
+    PW_HIP(hipDeviceSynchronize());
+    rt->timer.used = 0;
+    return PW_OK;
+}
+
+void *pw_runtime_stream(pw_runtime *rt) { return rt ? (void *)rt->stream : nullptr; }
+
+int pw_runtime_take_flags(pw_runtime *rt, uint32_t *flags)
+{
+    if (!rt || !flags)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    // device-resident calls may have run on a caller's stream: wait for all of them
+    PW_HIP(hipDeviceSynchronize());
+    PW_TRY(read_flags(rt, *flags));
+    PW_TRY(reset_flags(rt));
+    PW_HIP(hipStreamSynchronize(rt->stream));
+    return PW_OK;
+}
+
+// ------------------------------------------------------------------------------ projections
+int pw_projection_bind(pw_runtime *rt, const pw_projection_desc *d, int scan_codes,
+                       pw_projection **out)
+{
+    if (!rt || !d || !out)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    *out = nullptr;
+    const uint32_t rows = d->rows, cols = d->columns;
+    if (rows == 0 || cols == 0 || cols % 128 != 0)
+        return fail(PW_ERR_LAYOUT, "FP8 projection dimensions must be nonzero, columns a multiple of 128");
+    size_t scale_rows;
+    if (d->layout == PW_LAYOUT_PLAIN) {
+        scale_rows = (rows + 127) / 128;
+    } else if (d->layout == PW_LAYOUT_FULL_QKV_TP4) {
+        if (rows != 13568 || cols != 4096)
+            return fail(PW_ERR_LAYOUT, "wide full-QKV layout mismatch");
+        scale_rows = 108;
+    } else if (d->layout == PW_LAYOUT_SWA_QKV_TP4) {
+        if (rows != 14848 || cols != 4096)
+            return fail(PW_ERR_LAYOUT, "wide SWA-QKV layout mismatch");
+        scale_rows = 116;
+    } else {
+        return fail(PW_ERR_ARGUMENT, "unknown layout %u", d->layout);
+    }
+    const size_t wbytes = (size_t)rows * cols, sbytes = scale_rows * (cols / 128) * 4;
+    PW_TRY(check_region(d->weight, wbytes, "weight"));
+    PW_TRY(check_region(d->scale, sbytes, "scale"));
+    const uint8_t *hw = region_tensor(d->weight);
+    const float *hs = (const float *)region_tensor(d->scale);
+    PW_TRY(check_scales(hs, sbytes / 4));
+    if (scan_codes)
+        PW_TRY(check_weight_codes(hw, wbytes));
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    pw_projection *p = new pw_projection;
+    p->rt = rt;
+    p->rows = rows;
+    p->columns = cols;
+    p->owns = true;
+    p->weight_bytes = wbytes;
+    p->scale_bytes = sbytes;
+    hipError_t e = hipMalloc(&p->w, wbytes);
+    if (e == hipSuccess)
+        e = hipMalloc(&p->s, sbytes);
+    if (e == hipSuccess)
+        e = hipMemcpy(p->w, hw, wbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(p->s, hs, sbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        pw_projection_release(p);
+        return fail(PW_ERR_DEVICE, "weight upload failed: %s", hipGetErrorString(e));
+    }
+    std::vector<ProjTile> tiles;
+    if (d->layout == PW_LAYOUT_PLAIN) {
+        add_segment_tiles(tiles, p->w, p->s, cols, 0, rows, 0, 0);
+    } else if (d->layout == PW_LAYOUT_FULL_QKV_TP4) {
+        // shards of [Q 3072 | K 192 | V 128], 27 scale rows each (24 Q, 2 K incl. a 64-row
+        // partial block, 1 V); outputs deinterleaved as all Q, all K, all V
+        for (uint32_t s = 0; s < 4; ++s) {
+            add_segment_tiles(tiles, p->w, p->s, cols, s * 3392ull, 3072, s * 27ull, s * 3072);
+            add_segment_tiles(tiles, p->w, p->s, cols, s * 3392ull + 3072, 192, s * 27ull + 24, 12288 + s * 192);
+            add_segment_tiles(tiles, p->w, p->s, cols, s * 3392ull + 3264, 128, s * 27ull + 26, 13056 + s * 128);
+        }
+    } else {
+        // shards of [Q 3072 | K 384 | V 256], uniform scale rows source_row / 128
+        for (uint32_t s = 0; s < 4; ++s) {
+            add_segment_tiles(tiles, p->w, p->s, cols, s * 3712ull, 3072, s * 29ull, s * 3072);
+            add_segment_tiles(tiles, p->w, p->s, cols, s * 3712ull + 3072, 384, s * 29ull + 24, 12288 + s * 384);
+            add_segment_tiles(tiles, p->w, p->s, cols, s * 3712ull + 3456, 256, s * 29ull + 27, 13824 + s * 256);
+        }
+    }
+    int st = upload_tiles(p, tiles);
+    if (st != PW_OK) {
+        pw_projection_release(p);
+        return st;
+    }
+    *out = p;
+    return PW_OK;
+}
+
+int pw_projection_bind_segments(pw_runtime *rt, const pw_segment_desc *segs, uint32_t count,
+                                uint32_t columns, int scan_codes, pw_projection **out)
+{
+    if (!rt || !segs || !out || count == 0)
+        return fail(PW_ERR_ARGUMENT, "null argument or empty segment list");
+    *out = nullptr;
+    if (columns == 0 || columns % 128 != 0)
+        return fail(PW_ERR_LAYOUT, "columns must be a nonzero multiple of 128");
+    size_t total_rows = 0, wbytes = 0, sbytes = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (segs[i].rows == 0)
+            return fail(PW_ERR_LAYOUT, "segment %u has no rows", i);
+        const size_t w = (size_t)segs[i].rows * columns;
+        const size_t s = (size_t)((segs[i].rows + 127) / 128) * (columns / 128) * 4;
+        PW_TRY(check_region(segs[i].weight, w, "segment weight"));
+        PW_TRY(check_region(segs[i].scale, s, "segment scale"));
+        PW_TRY(check_scales((const float *)region_tensor(segs[i].scale), s / 4));
+        if (scan_codes)
+            PW_TRY(check_weight_codes(region_tensor(segs[i].weight), w));
+        total_rows += segs[i].rows;
+        wbytes += w;
+        sbytes += s;
+    }
+    if (total_rows > 0xffffffffull)
+        return fail(PW_ERR_LAYOUT, "too many rows");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    pw_projection *p = new pw_projection;
+    p->rt = rt;
+    p->rows = (uint32_t)total_rows;
+    p->columns = columns;
+    p->owns = true;
+    p->weight_bytes = wbytes;
+    p->scale_bytes = sbytes;
+    hipError_t e = hipMalloc(&p->w, wbytes);
+    if (e == hipSuccess)
+        e = hipMalloc(&p->s, sbytes);
+    std::vector<ProjTile> tiles;
+    size_t woff = 0, soff = 0;
+    uint32_t out_row = 0;
+    for (uint32_t i = 0; i < count && e == hipSuccess; ++i) {
+        const size_t w = (size_t)segs[i].rows * columns;
+        const size_t srows = (segs[i].rows + 127) / 128;
+        const size_t s = srows * (columns / 128) * 4;
+        e = hipMemcpy(p->w + woff, region_tensor(segs[i].weight), w, hipMemcpyHostToDevice);
+        if (e == hipSuccess)
+            e = hipMemcpy((uint8_t *)p->s + soff, region_tensor(segs[i].scale), s, hipMemcpyHostToDevice);
+        add_segment_tiles(tiles, p->w + woff, (const float *)((const uint8_t *)p->s + soff), columns,
+                          0, segs[i].rows, 0, out_row);
+        woff += w;
+        soff += s;
+        out_row += segs[i].rows;
+    }
+    if (e != hipSuccess) {
+        pw_projection_release(p);
+        return fail(PW_ERR_DEVICE, "segment upload failed: %s", hipGetErrorString(e));
+    }
+    int st = upload_tiles(p, tiles);
+    if (st != PW_OK) {
+        pw_projection_release(p);
+        return st;
+    }
+    *out = p;
+    return PW_OK;
+}
+
+int pw_projection_bind_device(pw_runtime *rt, const void *weight, const float *scale, uint32_t rows,
+                              uint32_t columns, pw_projection **out)
+{
+    if (!rt || !weight || !scale || !out)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (rows == 0 || columns == 0 || columns % 128 != 0)
+        return fail(PW_ERR_LAYOUT, "FP8 projection dimensions must be nonzero, columns a multiple of 128");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    pw_projection *p = new pw_projection;
+    p->rt = rt;
+    p->w = (uint8_t *)weight;
+    p->s = (float *)scale;
+    p->owns = false;
+    p->rows = rows;
+    p->columns = columns;
+    p->weight_bytes = (uint64_t)rows * columns;
+    p->scale_bytes = (uint64_t)((rows + 127) / 128) * (columns / 128) * 4;
+    std::vector<ProjTile> tiles;
+    add_segment_tiles(tiles, p->w, p->s, columns, 0, rows, 0, 0);
+    int st = upload_tiles(p, tiles);
+    if (st != PW_OK) {
+        pw_projection_release(p);
+        return st;
+    }
+    *out = p;
+    return PW_OK;
+}
+
+void pw_projection_release(pw_projection *p)
+{
+    if (!p)
+        return;
+    if (p->rt)
+        (void)hipSetDevice(p->rt->device);
+    if (p->owns) {
+        if (p->w)
+            (void)hipFree(p->w);
+        if (p->s)
+            (void)hipFree(p->s);
+    }
+    if (p->tiles)
+        (void)hipFree(p->tiles);
+    delete p;
+}
+
+int pw_projection_shape(const pw_projection *p, uint32_t *rows, uint32_t *columns)
+{
+    if (!p)
+        return fail(PW_ERR_ARGUMENT, "null projection");
+    if (rows)
+        *rows = p->rows;
+    if (columns)
+        *columns = p->columns;
+    return PW_OK;
+}
+
+static int enqueue_linear(pw_runtime *rt, uint32_t mode, const void *x, bool x_f32, uint32_t rows,
+                          const pw_projection *p, float *y32, uint16_t *y16, uint32_t round_f32,
+                          hipStream_t stream)
+{
+    if (mode == PW_MODE_A) {
+        const uint16_t *planes = (const uint16_t *)x;
+        if (x_f32) {
+            const size_t n = (size_t)rows * p->columns;
+            PW_HIP(rt->lin_planes.ensure(3 * n * 2));
+            pw::launch_split_planes((const float *)x, (uint32_t)n, (uint16_t *)rt->lin_planes.p, stream);
+            planes = (const uint16_t *)rt->lin_planes.p;
+        }
+        pw::launch_linear_a(p->tiles, p->n_tiles, planes, x_f32 ? 3 : 1, rows, p->columns, y32, y16,
+                            p->rows, round_f32, stream);
+    } else if (mode == PW_MODE_B) {
+        PW_HIP(rt->codes.ensure((size_t)rows * p->columns));
+        PW_HIP(rt->scales.ensure((size_t)rows * (p->columns / 128) * 4));
+        pw::launch_quant_group128(x, x_f32, rows, p->columns, (uint8_t *)rt->codes.p,
+                                  (float *)rt->scales.p, rt->d_flags, stream);
+        pw::launch_linear_b(p->tiles, p->n_tiles, (const uint8_t *)rt->codes.p,
+                            (const float *)rt->scales.p, rows, p->columns, y32, y16, p->rows,
+                            round_f32, stream);
+    } else {
+        return fail(PW_ERR_ARGUMENT, "unknown mode %u", mode);
+    }
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_fp8_linear(pw_runtime *rt, uint32_t mode, const float *input, uint32_t rows,
+                  const pw_projection *p, float *output, pw_linear_stats *stats)
+{
+    const double t0 = now_ms();
+    if (!rt || !input || !p || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (rows < 1 || rows > 32)
+        return fail(PW_ERR_ARGUMENT, "wide row count must be between one and 32");
+    const size_t n_in = (size_t)rows * p->columns, n_out = (size_t)rows * p->rows;
+    for (size_t i = 0; i < n_in; ++i)
+        if (!finite(input[i]))
+            return fail(PW_ERR_NONFINITE, "wide FP8 linear input is non-finite");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    PW_TRY(reset_flags(rt));
+    bool x_f32;
+    PW_TRY(stage_input(rt, input, n_in, x_f32));
+    PW_HIP(rt->out.ensure(n_out * 4));
+    PW_TRY(enqueue_linear(rt, mode, rt->in.p, x_f32, rows, p, (float *)rt->out.p, nullptr, 1, rt->stream));
+    PW_HIP(hipMemcpyAsync(output, rt->out.p, n_out * 4, hipMemcpyDeviceToHost, rt->stream));
+    uint32_t flags = 0;
+    PW_TRY(read_flags(rt, flags));
+    if (stats) {
+        stats->wall_ms = now_ms() - t0;
+        stats->mapped_source_bytes = 0;
+        stats->resident_source_bytes = p->weight_bytes + p->scale_bytes;
+        stats->gpu_flags = flags;
+    }
+    if (flags)
+        return fail(PW_ERR_GPU_FLAGS, "wide FP8 linear kernels set error flags %u", flags);
+    for (size_t i = 0; i < n_out; ++i)
+        if (!finite(output[i]))
+            return fail(PW_ERR_OUTPUT, "wide FP8 linear produced non-finite output");
+    return PW_OK;
+}
+
+int pw_fp8_linear_device(pw_runtime *rt, uint32_t mode, const void *input, uint32_t input_dtype,
+                         uint32_t rows, const pw_projection *p, void *output, uint32_t output_dtype,
+                         uint32_t round_output, void *stream)
+{
+    if (!rt || !input || !p || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (rows < 1 || rows > 32)
+        return fail(PW_ERR_ARGUMENT, "wide row count must be between one and 32");
+    if (input_dtype > PW_DTYPE_BF16 || output_dtype > PW_DTYPE_F32_RAW)
+        return fail(PW_ERR_ARGUMENT, "unknown dtype");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    float *y32 = output_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr;
+    uint16_t *y16 = output_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr;
+    const uint32_t round_f32 = output_dtype == PW_DTYPE_F32 && round_output ? 1u : 0u;
+    return enqueue_linear(rt, mode, input, input_dtype == PW_DTYPE_F32, rows, p, y32, y16, round_f32, s);
+}
+
+int pw_quantize_fp8_group128_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows,
+                                    uint32_t cols, uint8_t *codes, float *scales, void *stream)
+{
+    if (!rt || !x || !codes || !scales || rows == 0)
+        return fail(PW_ERR_ARGUMENT, "null argument or zero rows");
+    if (cols == 0 || cols % 128 != 0)
+        return fail(PW_ERR_LAYOUT, "dynamic FP8 activation shape mismatch");
+    if (x_dtype > PW_DTYPE_BF16)
+        return fail(PW_ERR_ARGUMENT, "unknown dtype");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    pw::launch_quant_group128(x, x_dtype == PW_DTYPE_F32, rows, cols, codes, scales, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+// ------------------------------------------------------------------------------- routed MoE
+static int check_expert_projection(const pw_projection *p, uint32_t rows, uint32_t cols)
+{
+    return p && p->rows == rows && p->columns == cols && rows % 128 == 0 && cols % 128 == 0;
+}
+
+int pw_moe_execute(pw_runtime *rt, uint32_t mode, uint32_t fused_gate_up, const float *input,
+                   uint32_t rows, const pw_expert_binding *experts, uint32_t n_experts,
+                   float *output, pw_moe_stats *stats)
+{
+    (void)fused_gate_up;  // gate and up always share one pass
+    const double t0 = now_ms();
+    if (!rt || !input || !experts || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (mode > PW_MODE_B)
+        return fail(PW_ERR_ARGUMENT, "unknown mode %u", mode);
+    if (rows < 1 || rows > 128)
+        return fail(PW_ERR_ARGUMENT, "wide row count must be between one and 128");
+    if (n_experts == 0 || !experts[0].gate || !experts[0].down)
+        return fail(PW_ERR_SCHEDULE, "wide MoE input or schedule mismatch");
+    const uint32_t H = experts[0].gate->columns, I = experts[0].gate->rows;
+    const size_t n_in = (size_t)rows * H;
+    for (size_t i = 0; i < n_in; ++i)
+        if (!finite(input[i]))
+            return fail(PW_ERR_NONFINITE, "wide MoE input or schedule mismatch");
+    // validation of src/wide_metal_moe.rs:858-938
+    size_t total = 0;
+    uint32_t max_count = 0;
+    std::vector<uint32_t> ids((size_t)rows * 8), fill(rows, 0);
+    std::vector<float> ws((size_t)rows * 8);
+    std::vector<ExpertPtrs> table(n_experts);
+    std::vector<uint32_t> seen;
+    uint64_t resident = 0;
+    for (uint32_t k = 0; k < n_experts; ++k) {
+        const pw_expert_binding &b = experts[k];
+        if (b.count == 0 || b.count > 32 || !b.positions || !b.route_weights ||
+            !check_expert_projection(b.gate, I, H) || !check_expert_projection(b.up, I, H) ||
+            !check_expert_projection(b.down, H, I))
+            return fail(PW_ERR_SCHEDULE, "wide MoE expert %u identity mismatch", b.expert);
+        for (uint32_t j = 0; j < b.count; ++j) {
+            const uint32_t pos = b.positions[j];
+            if (pos >= rows || !finite(b.route_weights[j]))
+                return fail(PW_ERR_SCHEDULE, "wide MoE expert %u identity mismatch", b.expert);
+            if (fill[pos] >= 8)
+                return fail(PW_ERR_SCHEDULE, "wide MoE input or schedule mismatch");
+            ids[(size_t)pos * 8 + fill[pos]] = k;
+            ws[(size_t)pos * 8 + fill[pos]] = b.route_weights[j];
+            fill[pos]++;
+        }
+        total += b.count;
+        max_count = std::max(max_count, b.count);
+        table[k] = ExpertPtrs{b.gate->w, b.gate->s, b.up->w, b.up->s, b.down->w, b.down->s};
+        if (std::find(seen.begin(), seen.end(), b.expert) == seen.end()) {
+            seen.push_back(b.expert);
+            resident += b.gate->weight_bytes + b.gate->scale_bytes + b.up->weight_bytes +
+                        b.up->scale_bytes + b.down->weight_bytes + b.down->scale_bytes;
+        }
+    }
+    if (total != (size_t)rows * 8)
+        return fail(PW_ERR_SCHEDULE, "wide MoE input or schedule mismatch");
+    // a position routed twice to the same binding would be summed twice by the reference; the
+    // device schedule rejects it, so refuse it here with the same error class
+    for (uint32_t p = 0; p < rows; ++p)
+        for (int a = 0; a < 8; ++a)
+            for (int b2 = a + 1; b2 < 8; ++b2)
+                if (ids[(size_t)p * 8 + a] == ids[(size_t)p * 8 + b2])
+                    return fail(PW_ERR_SCHEDULE, "position %u routed twice to one expert binding", p);
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    PW_TRY(reset_flags(rt));
+    bool x_f32;
+    PW_TRY(stage_input(rt, input, n_in, x_f32));
+    PW_HIP(rt->route_ids.ensure(ids.size() * 4));
+    PW_HIP(rt->route_w.ensure(ws.size() * 4));
+    PW_HIP(rt->bank_table.ensure(table.size() * sizeof(ExpertPtrs)));
+    PW_HIP(hipMemcpyAsync(rt->route_ids.p, ids.data(), ids.size() * 4, hipMemcpyHostToDevice, rt->stream));
+    PW_HIP(hipMemcpyAsync(rt->route_w.p, ws.data(), ws.size() * 4, hipMemcpyHostToDevice, rt->stream));
+    PW_HIP(hipMemcpyAsync(rt->bank_table.p, table.data(), table.size() * sizeof(ExpertPtrs),
+                          hipMemcpyHostToDevice, rt->stream));
+    PW_TRY(ensure_moe(rt, rows, n_experts, H, I));
+    PW_HIP(rt->out.ensure(n_in * 4));
+    pw::launch_moe_schedule((const ExpertPtrs *)rt->bank_table.p, (const uint32_t *)rt->route_ids.p,
+                            (const float *)rt->route_w.p, rows, n_experts,
+                            std::min<uint32_t>(n_experts, rows * 8), rt->mb, rt->d_flags, rt->stream);
+    pw::launch_moe_layer(mode, (const ExpertPtrs *)rt->bank_table.p, rt->mb, rt->in.p, x_f32, rows,
+                         std::min<uint32_t>(n_experts, rows * 8), max_count, H, I,
+                         (float *)rt->out.p, nullptr, false, rt->d_flags, rt->stream);
+    PW_HIP(hipGetLastError());
+    PW_HIP(hipMemcpyAsync(output, rt->out.p, n_in * 4, hipMemcpyDeviceToHost, rt->stream));
+    uint32_t flags = 0;
+    PW_TRY(read_flags(rt, flags));  // also completes the stream (ids/ws/table stay valid until here)
+    if (stats) {
+        stats->wall_ms = now_ms() - t0;
+        stats->unique_experts = (uint32_t)seen.size();
+        stats->expert_rows = (uint32_t)total;
+        stats->mapped_source_bytes = 0;
+        stats->resident_source_bytes = resident;
+        stats->gpu_flags = flags;
+    }
+    if (flags)
+        return fail(PW_ERR_GPU_FLAGS, "wide MoE semantic kernels set error flags %u", flags);
+    for (size_t i = 0; i < n_in; ++i)
+        if (!finite(output[i]))
+            return fail(PW_ERR_OUTPUT, "wide MoE produced non-finite output");
+    return PW_OK;
+}
+
+int pw_expert_bank_create(pw_runtime *rt, uint32_t n_experts, const pw_projection *const *gate,
+                          const pw_projection *const *up, const pw_projection *const *down,
+                          pw_expert_bank **out)
+{
+    if (!rt || !gate || !up || !down || !out || n_experts == 0)
+        return fail(PW_ERR_ARGUMENT, "null argument or empty bank");
+    *out = nullptr;
+    if (!gate[0])
+        return fail(PW_ERR_LAYOUT, "expert 0 has no gate projection");
+    const uint32_t I = gate[0]->rows, H = gate[0]->columns;
+    std::vector<ExpertPtrs> table(n_experts);
+    for (uint32_t e = 0; e < n_experts; ++e) {
+        if (!check_expert_projection(gate[e], I, H) || !check_expert_projection(up[e], I, H) ||
+            !check_expert_projection(down[e], H, I))
+            return fail(PW_ERR_LAYOUT, "expert %u projection shape mismatch", e);
+        table[e] = ExpertPtrs{gate[e]->w, gate[e]->s, up[e]->w, up[e]->s, down[e]->w, down[e]->s};
+    }
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    pw_expert_bank *b = new pw_expert_bank;
+    b->rt = rt;
+    b->n_experts = n_experts;
+    b->hidden = H;
+    b->intermediate = I;
+    hipError_t e = hipMalloc(&b->table, table.size() * sizeof(ExpertPtrs));
+    if (e == hipSuccess)
+        e = hipMemcpy(b->table, table.data(), table.size() * sizeof(ExpertPtrs), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        pw_expert_bank_release(b);
+        return fail(PW_ERR_DEVICE, "bank upload failed: %s", hipGetErrorString(e));
+    }
+    *out = b;
+    return PW_OK;
+}
+
+void pw_expert_bank_release(pw_expert_bank *b)
+{
+    if (!b)
+        return;
+    if (b->rt)
+        (void)hipSetDevice(b->rt->device);
+    if (b->table)
+        (void)hipFree(b->table);
+    delete b;
+}
+
+int pw_expert_bank_shape(const pw_expert_bank *b, uint32_t *n, uint32_t *h, uint32_t *i)
+{
+    if (!b)
+        return fail(PW_ERR_ARGUMENT, "null bank");
+    if (n) *n = b->n_experts;
+    if (h) *h = b->hidden;
+    if (i) *i = b->intermediate;
+    return PW_OK;
+}
+
+int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
+                        uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
+                        const float *route_weights, void *output, uint32_t out_dtype, void *stream)
+{
+    if (!rt || !bank || !x || !route_ids || !route_weights || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (mode > PW_MODE_B || x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
+        return fail(PW_ERR_ARGUMENT, "unknown mode or dtype");
+    if (rows < 1 || rows > 32)
+        return fail(PW_ERR_ARGUMENT, "device MoE row count must be between one and 32");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    PW_TRY(ensure_moe(rt, rows, bank->n_experts, bank->hidden, bank->intermediate));
+    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, bank->n_experts,
+                            std::min<uint32_t>(bank->n_experts, rows * 8), rt->mb, rt->d_flags, s);
+    pw::launch_moe_layer(mode, bank->table, rt->mb, x, x_dtype == PW_DTYPE_F32, rows,
+                         std::min<uint32_t>(bank->n_experts, rows * 8), rows, bank->hidden,
+                         bank->intermediate, out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
+                         out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
+                         out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t expert,
+                             uint32_t mode, const void *x, uint32_t x_dtype, uint32_t rows,
+                             void *output, uint32_t out_dtype, void *stream)
+{
+    if (!rt || !bank || !x || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (mode > PW_MODE_B || x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
+        return fail(PW_ERR_ARGUMENT, "unknown mode or dtype");
+    if (expert >= bank->n_experts)
+        return fail(PW_ERR_ARGUMENT, "expert %u outside the bank of %u", expert, bank->n_experts);
+    if (rows < 1 || rows > 32)
+        return fail(PW_ERR_ARGUMENT, "expert row count must be between one and 32");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    PW_TRY(ensure_moe(rt, rows, bank->n_experts, bank->hidden, bank->intermediate));
+    pw::launch_expert_forward(mode, bank->table, expert, rt->mb, x, x_dtype == PW_DTYPE_F32, rows,
+                              bank->hidden, bank->intermediate,
+                              out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
+                              out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
+                              out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+// ----------------------------------------------------------------------------- host routing
+int pw_topk_unsorted_f32(const float *values, size_t count, size_t top_k, uint32_t *selected)
+{
+    if (!values || !selected || top_k == 0 || top_k >= count)
+        return -1;
+    try {
+        std::vector<Entry> q(count);
+        for (size_t i = 0; i < count; ++i)
+            q[i] = Entry{values[i], (int64_t)i};
+        nth_element_cxx(q.data(), q.data() + top_k - 1, q.data() + count);
+        for (size_t i = 0; i < top_k; ++i)
+            selected[i] = (uint32_t)q[i].i;
+    } catch (...) {
+        return -2;
+    }
+    return 0;
+}
+
+int pw_noaux_routes(const float *scores, const float *bias, uint32_t rows, uint32_t experts,
+                    uint32_t *selected, float *weights, uint64_t *tie_rows)
+{
+    constexpr uint32_t K = 8;
+    if (!scores || !bias || !selected || !weights || experts <= K)
+        return fail(PW_ERR_ARGUMENT, "invalid PyTorch noaux-tc inputs");
+    for (size_t i = 0; i < (size_t)rows * experts; ++i)
+        if (!finite(scores[i]))
+            return fail(PW_ERR_NONFINITE, "invalid PyTorch noaux-tc inputs");
+    for (uint32_t e = 0; e < experts; ++e)
+        if (!finite(bias[e]))
+            return fail(PW_ERR_NONFINITE, "invalid PyTorch noaux-tc inputs");
+    std::vector<float> corrected(experts);
+    std::vector<uint8_t> chosen(experts);
+    uint64_t ties = 0;
+    for (uint32_t p = 0; p < rows; ++p) {
+        const float *row = scores + (size_t)p * experts;
+        for (uint32_t e = 0; e < experts; ++e)
+            corrected[e] = row[e] + bias[e];
+        uint32_t sel[K];
+        if (pw_topk_unsorted_f32(corrected.data(), experts, K, sel) != 0)
+            return fail(PW_ERR_SCHEDULE, "PyTorch top-k failed at position %u", p);
+        std::fill(chosen.begin(), chosen.end(), 0);
+        for (uint32_t i = 0; i < K; ++i) {
+            if (sel[i] >= experts || chosen[sel[i]])
+                return fail(PW_ERR_SCHEDULE, "PyTorch top-k failed at position %u", p);
+            chosen[sel[i]] = 1;
+        }
+        float boundary = INFINITY, rejected = -INFINITY;
+        for (uint32_t i = 0; i < K; ++i)
+            boundary = std::fmin(boundary, corrected[sel[i]]);
+        for (uint32_t e = 0; e < experts; ++e)
+            if (!chosen[e])
+                rejected = std::fmax(rejected, corrected[e]);
+        if (!finite(boundary) || boundary < rejected)
+            return fail(PW_ERR_SCHEDULE, "top-k selected a value below the rejected boundary at position %u", p);
+        if (boundary == rejected)
+            ++ties;
+        // pytorch_sum_eight (src/text_endpoint.rs:4382-4390) + 1e-20
+        float c[K];
+        for (uint32_t i = 0; i < K; ++i)
+            c[i] = row[sel[i]];
+        const float lanes[4] = {c[0] + c[4], c[1] + c[5], c[2] + c[6], c[3] + c[7]};
+        float sum = 0.0f;
+        for (float l : lanes)
+            sum = sum + l;
+        const float denominator = sum + 1.0e-20f;
+        float wsum = 0.0f;
+        for (uint32_t i = 0; i < K; ++i) {
+            const float w = row[sel[i]] / denominator;
+            if (!finite(w) || w < 0.0f)
+                return fail(PW_ERR_NONFINITE, "PyTorch route weights invalid at position %u", p);
+            weights[(size_t)p * K + i] = w;
+            selected[(size_t)p * K + i] = sel[i];
+            wsum += w;
+        }
+        if (std::fabs(wsum - 1.0f) > 1.0e-6f)
+            return fail(PW_ERR_NONFINITE, "PyTorch route weights invalid at position %u", p);
+    }
+    if (tie_rows)
+        *tie_rows = ties;
+    return PW_OK;
+}
+
+int pw_route_from_logits(const float *logits, const float *bias, uint32_t rows, uint32_t experts,
+                         float *scores, uint32_t *selected, float *weights, uint64_t *tie_rows)
+{
+    if (!logits || !scores)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    for (size_t i = 0; i < (size_t)rows * experts; ++i)
+        scores[i] = pw::sigmoid_pytorch(logits[i]);
+    return pw_noaux_routes(scores, bias, rows, experts, selected, weights, tie_rows);
+}
+
+// ------------------------------------------------------------------------------ layout maps
+int64_t pw_full_qkv_source_row(int64_t r)
+{
+    constexpr int64_t QS = 3072, SHARD = 3392, Q = 4 * QS, KR = 4 * 192, VR = 4 * 128;
+    if (r < 0)
+        return -1;
+    if (r < Q)
+        return (r / QS) * SHARD + r % QS;
+    if (r < Q + KR)
+        return ((r - Q) / 192) * SHARD + QS + (r - Q) % 192;
+    if (r < Q + KR + VR)
+        return ((r - Q - KR) / 128) * SHARD + QS + 192 + (r - Q - KR) % 128;
+    return -1;
+}
+
+int64_t pw_full_qkv_scale_row(int64_t r)
+{
+    const int64_t src = pw_full_qkv_source_row(r);
+    if (src < 0)
+        return -1;
+    const int64_t shard = src / 3392, local = src % 3392;
+    const int64_t ls = local < 3072 ? local / 128 : (local < 3264 ? 24 + (local - 3072) / 128 : 26);
+    return shard * 27 + ls;
+}
+
+int64_t pw_swa_qkv_source_row(int64_t r)
+{
+    constexpr int64_t QS = 3072, KS = 384, VS = 256, SHARD = QS + KS + VS;
+    if (r < 0)
+        return -1;
+    if (r < 4 * QS)
+        return r / QS * SHARD + r % QS;
+    if (r < 4 * (QS + KS))
+        return (r - 4 * QS) / KS * SHARD + QS + (r - 4 * QS) % KS;
+    if (r < 4 * SHARD)
+        return (r - 4 * (QS + KS)) / VS * SHARD + QS + KS + (r - 4 * (QS + KS)) % VS;
+    return -1;
+}
+
+// ------------------------------------------------------------------------------- synthetic
+int pw_synth_scales(pw_runtime *rt, float *scales, uint64_t count, uint64_t seed, float lo, float hi)
+{
+    if (!rt || !scales || count == 0)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    pw::launch_synth_scales(scales, count, seed, lo, hi, rt->stream);
+    PW_HIP(hipGetLastError());
+    PW_HIP(hipStreamSynchronize(rt->stream));
+    return PW_OK;
+}
+
+int pw_synth_fp8(pw_runtime *rt, uint8_t *w, const float *scales, uint64_t rows, uint64_t cols,
+                 uint64_t seed)
+{
+    if (!rt || !w || !scales || rows == 0 || cols == 0 || cols % 128 != 0)
+        return fail(PW_ERR_ARGUMENT, "bad synthetic FP8 arguments");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    pw::launch_synth_fp8(w, scales, rows, cols, seed, rt->stream);
+    PW_HIP(hipGetLastError());
+    PW_HIP(hipStreamSynchronize(rt->stream));
+    return PW_OK;
+}
+
+int pw_synth_normal_bf16(pw_runtime *rt, uint16_t *x, uint64_t count, uint64_t seed, float stddev)
+{
+    if (!rt || !x || count == 0 || count % 2 != 0)
+        return fail(PW_ERR_ARGUMENT, "bad synthetic bf16 arguments");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    pw::launch_synth_normal_bf16(x, count, seed, stddev, rt->stream);
+    PW_HIP(hipGetLastError());
+    PW_HIP(hipStreamSynchronize(rt->stream));
+    return PW_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,128 @@
+"""ctypes declarations of the C ABI in include/pwfp8.h.
+
+Loading fails loudly when libpwfp8.so is absent: there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libpwfp8.so")
+
+PW_OK = 0
+ERRORS = {
+    -1: "PW_ERR_ARGUMENT", -2: "PW_ERR_LAYOUT", -3: "PW_ERR_NONFINITE", -4: "PW_ERR_SCHEDULE",
+    -5: "PW_ERR_DEVICE", -6: "PW_ERR_GPU_FLAGS", -7: "PW_ERR_NOMEM", -8: "PW_ERR_OUTPUT",
+}
+MODE_A, MODE_B = 0, 1
+DTYPE_F32, DTYPE_BF16, DTYPE_F32_RAW = 0, 1, 2
+LAYOUT_PLAIN, LAYOUT_FULL_QKV_TP4, LAYOUT_SWA_QKV_TP4 = 0, 1, 2
+RUNTIME_FUSED_GATE_UP = 1
+
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_u32 = ctypes.c_uint32
+_i = ctypes.c_int
+
+
+class Region(ctypes.Structure):
+    _fields_ = [("bytes", _vp), ("region_bytes", _sz), ("tensor_offset", _sz), ("tensor_bytes", _sz)]
+
+
+class ProjectionDesc(ctypes.Structure):
+    _fields_ = [("weight", Region), ("scale", Region), ("rows", _u32), ("columns", _u32),
+                ("layout", _u32), ("copy_weight", _u32)]
+
+
+class SegmentDesc(ctypes.Structure):
+    _fields_ = [("weight", Region), ("scale", Region), ("rows", _u32)]
+
+
+class ExpertBindingC(ctypes.Structure):
+    _fields_ = [("expert", _u32), ("count", _u32), ("positions", _u32p), ("route_weights", _f32p),
+                ("gate", _vp), ("up", _vp), ("down", _vp)]
+
+
+class LinearStats(ctypes.Structure):
+    _fields_ = [("wall_ms", ctypes.c_double), ("mapped_source_bytes", ctypes.c_uint64),
+                ("resident_source_bytes", ctypes.c_uint64), ("gpu_flags", _u32)]
+
+
+class MoeStats(ctypes.Structure):
+    _fields_ = [("wall_ms", ctypes.c_double), ("unique_experts", _u32), ("expert_rows", _u32),
+                ("mapped_source_bytes", ctypes.c_uint64), ("resident_source_bytes", ctypes.c_uint64),
+                ("gpu_flags", _u32)]
+
+
+# name -> (restype, argtypes); the list is also the export manifest checked by the tests
+SIGNATURES = {
+    "pw_last_error": (ctypes.c_char_p, []),
+    "pw_abi_version": (_i, []),
+    "pw_runtime_create": (_i, [_i, _u32, ctypes.POINTER(_vp)]),
+    "pw_runtime_destroy": (None, [_vp]),
+    "pw_runtime_stream": (_vp, [_vp]),
+    "pw_runtime_take_flags": (_i, [_vp, _u32p]),
+    "pw_runtime_enable_timing": (_i, [_vp, _u32]),
+    "pw_runtime_timing_summary": (_i, [_vp, ctypes.c_char_p, _u32p, ctypes.POINTER(ctypes.c_double)]),
+    "pw_runtime_timing_reset": (_i, [_vp]),
+    "pw_projection_bind": (_i, [_vp, ctypes.POINTER(ProjectionDesc), _i, ctypes.POINTER(_vp)]),
+    "pw_projection_bind_segments": (_i, [_vp, ctypes.POINTER(SegmentDesc), _u32, _u32, _i, ctypes.POINTER(_vp)]),
+    "pw_projection_bind_device": (_i, [_vp, _vp, _vp, _u32, _u32, ctypes.POINTER(_vp)]),
+    "pw_projection_release": (None, [_vp]),
+    "pw_projection_shape": (_i, [_vp, _u32p, _u32p]),
+    "pw_fp8_linear": (_i, [_vp, _u32, _f32p, _u32, _vp, _f32p, ctypes.POINTER(LinearStats)]),
+    "pw_fp8_linear_device": (_i, [_vp, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp]),
+    "pw_quantize_fp8_group128_device": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "pw_moe_execute": (_i, [_vp, _u32, _u32, _f32p, _u32, ctypes.POINTER(ExpertBindingC), _u32, _f32p,
+                            ctypes.POINTER(MoeStats)]),
+    "pw_expert_bank_create": (_i, [_vp, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                   ctypes.POINTER(_vp)]),
+    "pw_expert_bank_release": (None, [_vp]),
+    "pw_expert_bank_shape": (_i, [_vp, _u32p, _u32p, _u32p]),
+    "pw_moe_layer_device": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
+    "pw_expert_forward_device": (_i, [_vp, _vp, _u32, _u32, _vp, _u32, _u32, _vp, _u32, _vp]),
+    "pw_topk_unsorted_f32": (_i, [_f32p, _sz, _sz, _u32p]),
+    "pw_noaux_routes": (_i, [_f32p, _f32p, _u32, _u32, _u32p, _f32p, _u64p]),
+    "pw_route_from_logits": (_i, [_f32p, _f32p, _u32, _u32, _f32p, _u32p, _f32p, _u64p]),
+    "pw_full_qkv_source_row": (ctypes.c_int64, [ctypes.c_int64]),
+    "pw_full_qkv_scale_row": (ctypes.c_int64, [ctypes.c_int64]),
+    "pw_swa_qkv_source_row": (ctypes.c_int64, [ctypes.c_int64]),
+    "pw_synth_scales": (_i, [_vp, _vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float, ctypes.c_float]),
+    "pw_synth_fp8": (_i, [_vp, _vp, _vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64]),
+    "pw_synth_normal_bf16": (_i, [_vp, _vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float]),
+}
+
+_lib = None
+
+
+class PwError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {message}")
+        self.code = code
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with `python mimo-prismwing_amd/build.py` "
+                              "(there is no fallback implementation)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(code: int):
+    if code != PW_OK:
+        raise PwError(code, lib().pw_last_error().decode())
+    return code

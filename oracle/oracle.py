@@ -65,7 +65,7 @@ def lib():
         L.pwo_route.argtypes = [_f32p, _sz, _f32p, _f32p, _sz, _sz, _f32p, _f32p, _u32p, _f32p, _u64p]
         for name in ("pwo_moe_layer_mode_a", "pwo_moe_layer_mode_b"):
             getattr(L, name).argtypes = [_f32p, _sz, _sz, _sz, ctypes.POINTER(PwoExpert), _sz,
-                                         _u32p, _f32p, _sz, _f32p]
+                                         _u32p, _f32p, _sz, _f32p, _f32p]
         L.pwo_expert_mode_a.argtypes = [_f32p, _sz, _sz, _sz, ctypes.POINTER(PwoExpert), _f32p, _f32p]
         for name in ("pwo_full_qkv_source_row", "pwo_full_qkv_scale_row", "pwo_swa_qkv_source_row"):
             getattr(L, name).argtypes = [ctypes.c_int64]
@@ -218,7 +218,9 @@ def _expert_array(experts: dict, n_experts: int):
     return arr, keep
 
 
-def moe_layer(mode: str, x, experts: dict, n_experts: int, selected, weights, hidden=None, inter=None):
+def moe_layer(mode: str, x, experts: dict, n_experts: int, selected, weights, hidden=None, inter=None,
+              raw=False):
+    """Routed MoE layer; returns the bf16-rounded output, plus the f32 combine when raw=True."""
     x = _c(np.atleast_2d(x), np.float32)
     rows = x.shape[0]
     hidden = hidden or x.shape[1]
@@ -227,13 +229,14 @@ def moe_layer(mode: str, x, experts: dict, n_experts: int, selected, weights, hi
     sel = _c(selected, np.uint32); w = _c(weights, np.float32)
     arr, keep = _expert_array(experts, n_experts)
     out = np.zeros((rows, hidden), np.float32)
+    out_raw = np.zeros((rows, hidden), np.float32)
     fn = lib().pwo_moe_layer_mode_a if mode == "a" else lib().pwo_moe_layer_mode_b
     rc = fn(_p(x, _f32p), rows, hidden, inter, arr, n_experts, _p(sel, _u32p), _p(w, _f32p),
-            sel.shape[1], _p(out, _f32p))
+            sel.shape[1], _p(out, _f32p), _p(out_raw, _f32p))
     del keep
     if rc != 0:
         raise ValueError(f"moe_layer_mode_{mode} failed: {rc}")
-    return out
+    return (out, out_raw) if raw else out
 
 
 def expert_mode_a(x, expert):

@@ -649,7 +649,7 @@ static void free_schedule(expert_slot *slots, size_t n)
 
 static int moe_layer(int mode_b, const float *x, size_t rows, size_t hidden, size_t inter,
                      const pwo_expert *experts, size_t n_experts, const uint32_t *selected,
-                     const float *weights, size_t top_k, float *out)
+                     const float *weights, size_t top_k, float *out, float *out_raw)
 {
     if (x == NULL || experts == NULL || selected == NULL || weights == NULL || out == NULL ||
         rows == 0 || hidden % 128 != 0 || inter % 128 != 0)
@@ -707,7 +707,11 @@ static int moe_layer(int mode_b, const float *x, size_t rows, size_t hidden, siz
     }
     if (status == 0)
         for (size_t i = 0; i < rows * hidden; ++i)
+        {
+            if (out_raw)
+                out_raw[i] = block[i];
             out[i] = pwo_round_bf16(block[i]);
+        }
     free(block);
     free(gathered);
     free(gate);
@@ -721,16 +725,18 @@ static int moe_layer(int mode_b, const float *x, size_t rows, size_t hidden, siz
 
 int pwo_moe_layer_mode_a(const float *x, size_t rows, size_t hidden, size_t inter,
                          const pwo_expert *experts, size_t n_experts, const uint32_t *selected,
-                         const float *weights, size_t top_k, float *out)
+                         const float *weights, size_t top_k, float *out, float *out_raw)
 {
-    return moe_layer(0, x, rows, hidden, inter, experts, n_experts, selected, weights, top_k, out);
+    return moe_layer(0, x, rows, hidden, inter, experts, n_experts, selected, weights, top_k, out,
+                     out_raw);
 }
 
 int pwo_moe_layer_mode_b(const float *x, size_t rows, size_t hidden, size_t inter,
                          const pwo_expert *experts, size_t n_experts, const uint32_t *selected,
-                         const float *weights, size_t top_k, float *out)
+                         const float *weights, size_t top_k, float *out, float *out_raw)
 {
-    return moe_layer(1, x, rows, hidden, inter, experts, n_experts, selected, weights, top_k, out);
+    return moe_layer(1, x, rows, hidden, inter, experts, n_experts, selected, weights, top_k, out,
+                     out_raw);
 }
 
 int pwo_expert_mode_a(const float *x, size_t rows, size_t hidden, size_t inter,

@@ -99,12 +99,13 @@ typedef struct {
  * Mode A = the reference's f32 CPU control (src/lib.rs:5807-5862): f32 activations, f32 SwiGLU,
  * f32 expert outputs, f32 weighted combine in ascending expert id, bf16 at the end.
  * Mode B = routed_mlp_traced (src/text_endpoint.rs:5290-5381) over fp8_linear. */
+/* out_raw (may be NULL) receives the f32 combine before the final bf16 round. */
 int pwo_moe_layer_mode_a(const float *x, size_t rows, size_t hidden, size_t inter,
                          const pwo_expert *experts, size_t n_experts, const uint32_t *selected,
-                         const float *weights, size_t top_k, float *out);
+                         const float *weights, size_t top_k, float *out, float *out_raw);
 int pwo_moe_layer_mode_b(const float *x, size_t rows, size_t hidden, size_t inter,
                          const pwo_expert *experts, size_t n_experts, const uint32_t *selected,
-                         const float *weights, size_t top_k, float *out);
+                         const float *weights, size_t top_k, float *out, float *out_raw);
 /* One complete expert in mode A (config "one routed expert"): y = bf16(down(swiglu(gate x, up x))). */
 int pwo_expert_mode_a(const float *x, size_t rows, size_t hidden, size_t inter,
                       const pwo_expert *expert, float *out_f32, float *out_bf16);

@@ -19,3 +19,15 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def golden_dir():
     return GOLDEN
+
+
+@pytest.fixture(scope="session")
+def rt():
+    """One runtime on device 0 for the whole GPU session (the library must be built)."""
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import prismwing_amd as P
+    runtime = P.WideMoeRuntime.compile(0)
+    yield runtime
+    runtime.close()

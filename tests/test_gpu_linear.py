@@ -1,0 +1,266 @@
+"""GPU parity of the block-scaled FP8 projections (modes A and B, plain / segmented / TP4 layouts)
+against the C oracle, through the C ABI.
+
+Tolerances: mode A f32 accumulation <= 1e-3 max|d|/max|ref| on the f32
+result before the final bf16 round (in practice ~1e-7: products are exact, only the summation
+order differs), and bf16 outputs within one bf16 rounding step plus 1e-5 * sum|terms| of the
+oracle's; mode B <= 2e-2 max|d|/max|ref|. Integer work (codes, scales) is bit-exact.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import prismwing_amd as P
+from helpers import (bf16_normal, bf16_round, condition, decode_table, dequant, fp8_weight,
+                     from_bf16_bits, log_uniform_scales, normwise, rel_l2, to_bf16_bits,
+                     within_bf16_cond)
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def run_device(rt, proj, x, mode=P.MODE_A, x_dtype=P.DTYPE_BF16, out_dtype=P.DTYPE_F32_RAW):
+    """Device-resident projection on torch's stream; returns numpy f32 [rows, proj.rows]."""
+    torch = _torch()
+    rows = x.shape[0]
+    if x_dtype == P.DTYPE_BF16:
+        xt = torch.from_numpy(to_bf16_bits(x).view(np.int16)).cuda()
+    else:
+        xt = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    if out_dtype == P.DTYPE_BF16:
+        out = torch.empty((rows, proj.rows), dtype=torch.int16, device="cuda")
+    else:
+        out = torch.empty((rows, proj.rows), dtype=torch.float32, device="cuda")
+    rt.fp8_linear_device(proj, xt, rows, out, mode=mode, x_dtype=x_dtype, out_dtype=out_dtype,
+                         stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    host = out.cpu().numpy()
+    return from_bf16_bits(host.view(np.uint16)) if out_dtype == P.DTYPE_BF16 else host
+
+
+def test_fp8_hardware_decode_all_bytes_mode_a(rt):
+    """v_cvt_scalef32_pk_bf16_fp8 reads OCP e4m3fn: every finite byte decodes to the oracle value."""
+    codes = np.arange(256, dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    w = np.repeat(codes[:, None], 256, axis=1)  # row r is all byte r
+    s = np.ones((2, 2), np.float32)
+    proj = rt.bind_projection(w, s)
+    for col in (0, 77, 200):
+        x = np.zeros((1, 256), np.float32)
+        x[0, col] = 1.0
+        y = run_device(rt, proj, x)[0]
+        want = np.array([O.decode_e4m3fn(int(c)) for c in codes], np.float32)
+        assert np.array_equal(y.view(np.uint32) & 0x7FFFFFFF, want.view(np.uint32) & 0x7FFFFFFF)
+        assert np.array_equal(np.signbit(y[want != 0]), np.signbit(want[want != 0]))
+
+
+def test_fp8_hardware_decode_all_bytes_mode_b(rt):
+    """The FP8 MFMA reads OCP e4m3fn codes: x one-hot 448 quantises to code 0x7e, scale 1."""
+    codes = np.arange(256, dtype=np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0
+    w = np.repeat(codes[:, None], 128, axis=1)
+    proj = rt.bind_projection(w, np.ones((2, 1), np.float32))
+    x = np.zeros((1, 128), np.float32)
+    x[0, 5] = 448.0
+    y = run_device(rt, proj, x, mode=P.MODE_B, x_dtype=P.DTYPE_F32)[0]
+    want = np.array([O.decode_e4m3fn(int(c)) * 448.0 for c in codes], np.float32)
+    assert np.array_equal(y, want)
+
+
+def test_closed_form_row_and_column_blocks(rt):
+    w = np.full((256, 256), 0x38, np.uint8)
+    s = np.array([[1.0, 2.0], [3.0, 4.0]], np.float32)
+    proj = rt.bind_projection(w, s)
+    for mode in (P.MODE_A, P.MODE_B):
+        y = rt.execute_fp8_linear(np.ones((1, 256), np.float32), proj, mode=mode).output[0]
+        assert np.all(y[:128] == 384.0) and np.all(y[128:] == 896.0)
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 8, 16, 17, 32])
+@pytest.mark.parametrize("x_kind", ["bf16", "f32"])
+def test_mode_a_matches_oracle(rt, rows, x_kind):
+    rng = np.random.default_rng(100 + rows)
+    n, k = 200, 512  # partial 16-row tile and partial 128-row scale block
+    s = log_uniform_scales(rng, n, k)
+    w = fp8_weight(rng, n, k, s)
+    x = bf16_normal(rng, (rows, k)) if x_kind == "bf16" else rng.standard_normal((rows, k)).astype(np.float32)
+    ref = O.gemm_mode_a(w, s, x)
+    proj = rt.bind_projection(w, s)
+    got = run_device(rt, proj, x, x_dtype=P.DTYPE_BF16 if x_kind == "bf16" else P.DTYPE_F32)
+    assert normwise(got, ref) <= 2e-6  # exact products, f32 accumulation order only
+    host = rt.execute_fp8_linear(x, proj, mode=P.MODE_A).output
+    assert within_bf16_cond(host, bf16_round(ref), condition(w, s, x))
+
+
+def test_real_checkpoint_gemv_fixture(rt, golden_dir):
+    with open(os.path.join(golden_dir, "mtp-gate-fp8-gemv.json")) as f:
+        fx = json.load(f)
+    w = np.array(fx["raw_u8"], np.uint8)
+    s = np.array(fx["scale_inv"], np.float32).reshape(1, -1)
+    x = np.array(fx["input"], np.float32).reshape(1, -1)
+    proj = rt.bind_projection(w, s)
+    got = run_device(rt, proj, x, x_dtype=P.DTYPE_F32)[0]
+    # the reference's Metal harness bound for this fixture (tools/test_all.sh:9-21)
+    assert np.all(np.abs(got - np.array(fx["expected_f32"], np.float32)) < 2e-6)
+
+
+def test_projection_2048x4096_width1(rt):
+    """A single block-scaled FP8 projection GEMV at 2048 x 4096, width 1, bf16 output."""
+    rng = np.random.default_rng(0x50570000)
+    s = log_uniform_scales(rng, 2048, 4096)
+    w = fp8_weight(rng, 2048, 4096, s)
+    x = bf16_normal(rng, (1, 4096))
+    ref = O.gemm_mode_a(w, s, x)
+    proj = rt.bind_projection(w, s)
+    raw = run_device(rt, proj, x)
+    assert normwise(raw, ref) <= 1e-3 and rel_l2(raw, ref) <= 1e-5
+    out = run_device(rt, proj, x, out_dtype=P.DTYPE_BF16)
+    assert within_bf16_cond(out, bf16_round(ref), condition(w, s, x))
+
+
+def test_quantiser_bit_exact(rt, golden_dir):
+    rng = np.random.default_rng(9)
+    x = np.concatenate([rng.standard_normal((4, 512)) * 10, rng.standard_normal((2, 512)) * 1e-3,
+                        np.zeros((1, 512))]).astype(np.float32)
+    x[1, :128] = 0.0
+    x[1, 5] = -0.0
+    x[2, 130] = 1e-12
+    with open(os.path.join(golden_dir, "pw0053-dynamic-fp8-activation.json")) as f:
+        fx = json.load(f)
+    fixture_rows = np.array([b & 0xFFFFFFFF for b in np.array(fx["input_f32_bits"]).reshape(-1)],
+                            np.uint32).view(np.float32).reshape(2, 256)
+    for data in (x, fixture_rows):
+        codes_ref, scales_ref, _ = O.dynamic_fp8(data)
+        codes, scales = quantize_device(rt, data)
+        assert np.array_equal(codes, codes_ref)
+        assert np.array_equal(scales.view(np.uint32), scales_ref.view(np.uint32))
+
+
+def quantize_device(rt, data):
+    torch = _torch()
+    rows, k = data.shape
+    xt = torch.from_numpy(np.ascontiguousarray(data, np.float32)).cuda()
+    codes = torch.empty((rows, k), dtype=torch.uint8, device="cuda")
+    scales = torch.empty((rows, k // 128), dtype=torch.float32, device="cuda")
+    rt.quantize_fp8_group128_device(xt, rows, k, codes, scales, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    return codes.cpu().numpy(), scales.cpu().numpy()
+
+
+def test_quantiser_flags_nonfinite(rt):
+    torch = _torch()
+    data = np.ones((1, 128), np.float32)
+    data[0, 17] = np.inf
+    xt = torch.from_numpy(data).cuda()
+    codes = torch.empty((1, 128), dtype=torch.uint8, device="cuda")
+    scales = torch.empty((1, 1), dtype=torch.float32, device="cuda")
+    rt.quantize_fp8_group128_device(xt, 1, 128, codes, scales, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 2  # PW_FLAG_QUANT_NONFINITE
+    assert rt.take_flags() == 0
+
+
+@pytest.mark.parametrize("active", [2, 9, 26, 32])
+def test_mode_b_reference_probe(rt, active):
+    """The reference's block-scaled probe (src/wide_metal_moe.rs:387-532): codes and scales equal
+    the CPU quantiser, projection within 0.01 of the CPU block equation."""
+    rows, cols = 128, 256
+    x = ((np.arange(active * cols) * 29 % 401 - 200) / 37).astype(np.float32).reshape(active, cols)
+    q, a, _ = O.dynamic_fp8(x)
+    w = ((np.arange(rows * cols) * 37 + 11) % 0x7F).astype(np.uint8).reshape(rows, cols)
+    s = (0.003 + np.arange(2) * 0.0017).astype(np.float32).reshape(1, 2)
+    ref = O.gemm_mode_b_equation(w, s, q, a)
+    proj = rt.bind_projection(w, s)
+    got = run_device(rt, proj, x, mode=P.MODE_B, x_dtype=P.DTYPE_F32)
+    codes, scales = quantize_device(rt, x)
+    assert np.array_equal(codes, q) and np.array_equal(scales.view(np.uint32), a.view(np.uint32))
+    assert np.max(np.abs(got - ref)) <= 0.01
+
+
+@pytest.mark.parametrize("rows", [1, 8, 32])
+def test_mode_b_matches_fp8_linear(rt, rows):
+    rng = np.random.default_rng(200 + rows)
+    n, k = 384, 1024
+    s = log_uniform_scales(rng, n, k)
+    w = fp8_weight(rng, n, k, s)
+    x = bf16_normal(rng, (rows, k))
+    ref = O.fp8_linear_mode_b(w, s, x)
+    proj = rt.bind_projection(w, s)
+    got = rt.execute_fp8_linear(x, proj, mode=P.MODE_B).output
+    assert normwise(got, ref) <= 2e-2
+    _, _, xd = O.dynamic_fp8(x)
+    assert within_bf16_cond(got, ref, np.abs(xd.astype(np.float64)) @ np.abs(dequant(w, s)).T)
+
+
+def _segments(rng, rows_list, k=4096):
+    segs = []
+    for rows in rows_list:
+        s = log_uniform_scales(rng, rows, k)
+        segs.append((fp8_weight(rng, rows, k, s), s))
+    return segs
+
+
+@pytest.mark.parametrize("k_rows", [768, 1000])
+@pytest.mark.parametrize("width", [1, 8])
+def test_qkv_segments_nonuniform_scales(rt, k_rows, width):
+    """Separate q [12288], k [768 or 1000 (partial trailing block)], v [512] x 4096 tensors, each
+    with its own ceil(rows/128) x 32 scale grid, output concatenated."""
+    rng = np.random.default_rng(0x50570003 + k_rows + width)
+    segs = _segments(rng, [12288, k_rows, 512])
+    x = bf16_normal(rng, (width, 4096))
+    ref = np.concatenate([O.gemm_mode_a(w, s, x) for w, s in segs], axis=1)
+    proj = rt.bind_segments(segs)
+    assert proj.rows == 12288 + k_rows + 512
+    raw = run_device(rt, proj, x)
+    assert normwise(raw, ref) <= 1e-3 and rel_l2(raw, ref) <= 1e-5
+    out = run_device(rt, proj, x, out_dtype=P.DTYPE_BF16)
+    cond = np.concatenate([condition(w, s, x) for w, s in segs], axis=1)
+    assert within_bf16_cond(out, bf16_round(ref), cond)
+
+
+@pytest.mark.parametrize("layout", [P.LAYOUT_FULL_QKV_TP4, P.LAYOUT_SWA_QKV_TP4])
+def test_tp4_qkv_layouts(rt, layout):
+    """The checkpoint's four TP shards deinterleaved on one device (src/text_endpoint.rs:3174-3242)
+    checked against an f64 brute force that applies the reference's row and scale-row maps."""
+    rng = np.random.default_rng(7 + layout)
+    rows, srows = (13568, 108) if layout == P.LAYOUT_FULL_QKV_TP4 else (14848, 116)
+    w = rng.integers(0, 0x7F, size=(rows, 4096), dtype=np.uint8) | (rng.integers(0, 2, size=(rows, 4096), dtype=np.uint8) << 7)
+    s = (2.0 ** rng.uniform(-10, -6, size=(srows, 32))).astype(np.float32)
+    x = bf16_normal(rng, (8, 4096))
+    proj = rt.bind_projection(w, s, layout=layout)
+    got = run_device(rt, proj, x)
+    src = np.array([(O.full_qkv_source_row if layout == P.LAYOUT_FULL_QKV_TP4 else O.swa_qkv_source_row)(r)
+                    for r in range(rows)])
+    srow = (np.array([O.full_qkv_scale_row(r) for r in range(rows)]) if layout == P.LAYOUT_FULL_QKV_TP4
+            else src // 128)
+    dec = decode_table()[w[src]].astype(np.float32)
+    wd = dec * np.repeat(s[srow], 128, axis=1)
+    ref = x.astype(np.float64) @ wd.T.astype(np.float64)
+    assert normwise(got, ref) <= 1e-5
+
+
+def test_fail_closed_validation(rt):
+    w = np.full((128, 128), 0x38, np.uint8)
+    s = np.ones((1, 1), np.float32)
+    proj = rt.bind_projection(w, s)
+    bad = np.ones((1, 128), np.float32)
+    bad[0, 3] = np.nan
+    with pytest.raises(P.PwError, match="NONFINITE"):
+        rt.execute_fp8_linear(bad, proj, mode=P.MODE_A)
+    w2 = w.copy()
+    w2[3, 9] = 0x7F
+    with pytest.raises(P.PwError, match="non-finite FP8 weight"):
+        rt.bind_projection(w2, s)
+    with pytest.raises(P.PwError, match="LAYOUT"):
+        rt.bind_projection(w, np.ones((2, 1), np.float32))
+    with pytest.raises(P.PwError, match="NONFINITE"):
+        rt.bind_projection(w, np.full((1, 1), np.inf, np.float32))

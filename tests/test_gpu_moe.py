@@ -1,0 +1,195 @@
+"""GPU parity of the routed-MoE path (schedule, fused gate/up + SwiGLU, down, combine) against the
+C oracle, through the C ABI: the reference's execute/execute_fused_gate_up host surface and the
+device-resident layer on a full 256-expert bank.
+
+Tolerances: mode A <= 1e-3 max|d|/max|ref| on the f32 combine before the final bf16 round and
+<= 8e-3 on bf16 outputs (one rounding step of the largest element); mode B <= 2e-2. Routes, placement
+counts and the schedule are integer work and bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import prismwing_amd as P
+from prismwing_amd import workloads as WL
+from helpers import bf16_normal, fp8_weight, log_uniform_scales, normwise, rel_l2
+
+# bf16 outputs: the f32 result may sit on the other side of a bf16 rounding boundary, so the
+# largest element may move by one step (<= 2^-7 of its magnitude); the f32 result itself is
+# held to the 1e-3 bound through the F32_RAW outputs.
+BF16_OUT = 8e-3
+
+pytestmark = pytest.mark.gpu
+
+
+def make_experts(rng, n, hidden, inter):
+    ex = {}
+    for e in range(n):
+        gs = log_uniform_scales(rng, inter, hidden)
+        us = log_uniform_scales(rng, inter, hidden)
+        ds = log_uniform_scales(rng, hidden, inter)
+        ex[e] = (fp8_weight(rng, inter, hidden, gs), gs, fp8_weight(rng, inter, hidden, us), us,
+                 fp8_weight(rng, hidden, inter, ds), ds)
+    return ex
+
+
+def random_routes(rng, rows, n_experts):
+    logits = rng.standard_normal((rows, n_experts)).astype(np.float32)
+    bias = rng.uniform(-0.01, 0.01, n_experts).astype(np.float32)
+    scores = np.vectorize(O.sigmoid_f32, otypes=[np.float32])(logits)
+    sel, w, _ = O.noaux_routes(scores, bias)
+    return sel, w
+
+
+def bindings_from_routes(projs, sel, w):
+    """BTreeMap schedule of src/text_endpoint.rs:4767-4775: experts ascending, positions ascending."""
+    out = []
+    for e in sorted(set(sel.reshape(-1).tolist())):
+        pos, wts = np.nonzero(sel == e)
+        order = np.argsort(pos, kind="stable")
+        g, u, d = projs[e]
+        out.append(P.WideExpertBinding(e, pos[order].astype(np.uint32),
+                                       w[pos[order], wts[order]].astype(np.float32), g, u, d))
+    return out
+
+
+@pytest.fixture(scope="module")
+def small_layer(rt):
+    rng = np.random.default_rng(42)
+    hidden, inter, n = 512, 256, 12
+    experts = make_experts(rng, n, hidden, inter)
+    projs = {e: (rt.bind_projection(v[0], v[1]), rt.bind_projection(v[2], v[3]), rt.bind_projection(v[4], v[5]))
+             for e, v in experts.items()}
+    return experts, projs, hidden, inter, n
+
+
+@pytest.mark.parametrize("rows", [1, 5, 8])
+@pytest.mark.parametrize("mode", [P.MODE_A, P.MODE_B])
+def test_execute_matches_oracle(rt, small_layer, rows, mode):
+    experts, projs, hidden, inter, n = small_layer
+    rng = np.random.default_rng(rows * 10 + mode)
+    x = bf16_normal(rng, (rows, hidden))
+    sel, w = random_routes(rng, rows, n)
+    res = rt.execute(x, bindings_from_routes(projs, sel, w), mode=mode)
+    ref = O.moe_layer("a" if mode == P.MODE_A else "b", x, experts, n, sel, w)
+    assert res.unique_experts == len(set(sel.reshape(-1).tolist()))
+    assert res.expert_rows == rows * 8
+    assert normwise(res.output, ref) <= (BF16_OUT if mode == P.MODE_A else 2e-2)
+
+
+def test_fused_and_unfused_are_byte_identical(rt, small_layer):
+    experts, projs, hidden, inter, n = small_layer
+    rng = np.random.default_rng(3)
+    x = bf16_normal(rng, (6, hidden))
+    sel, w = random_routes(rng, 6, n)
+    b = bindings_from_routes(projs, sel, w)
+    for mode in (P.MODE_A, P.MODE_B):
+        a = rt.execute(x, b, mode=mode).output
+        f = rt.execute_fused_gate_up(x, b, mode=mode).output
+        assert np.array_equal(a.view(np.uint32), f.view(np.uint32))
+
+
+def test_thirty_two_rows_per_expert(rt, small_layer):
+    """The reference's widest specialisation (MAX_EXPERT_ROWS = 32, src/wide_metal_moe.rs:12)."""
+    experts, projs, hidden, inter, n = small_layer
+    rng = np.random.default_rng(4)
+    rows = 32
+    x = rng.standard_normal((rows, hidden)).astype(np.float32)  # f32 activations (three-plane split path)
+    sel = np.tile(np.arange(8, dtype=np.uint32), (rows, 1))
+    w = np.full((rows, 8), 0.125, np.float32)
+    for mode in (P.MODE_A, P.MODE_B):
+        res = rt.execute(x, bindings_from_routes(projs, sel, w), mode=mode)
+        ref = O.moe_layer("a" if mode == P.MODE_A else "b", x, experts, n, sel, w)
+        assert normwise(res.output, ref) <= (BF16_OUT if mode == P.MODE_A else 2e-2)
+
+
+def test_slot_order_does_not_change_output(rt, small_layer):
+    """Placements are combined in ascending expert id whatever the route-slot order."""
+    experts, projs, hidden, inter, n = small_layer
+    rng = np.random.default_rng(5)
+    x = bf16_normal(rng, (4, hidden))
+    sel, w = random_routes(rng, 4, n)
+    base = rt.execute(x, bindings_from_routes(projs, sel, w), mode=P.MODE_A).output
+    perm = np.stack([rng.permutation(8) for _ in range(4)])
+    sel2 = np.take_along_axis(sel, perm, 1)
+    w2 = np.take_along_axis(w, perm, 1)
+    again = rt.execute(x, bindings_from_routes(projs, sel2, w2), mode=P.MODE_A).output
+    assert np.array_equal(base.view(np.uint32), again.view(np.uint32))
+
+
+def test_schedule_validation_fails_closed(rt, small_layer):
+    experts, projs, hidden, inter, n = small_layer
+    x = np.ones((2, hidden), np.float32)
+    g, u, d = projs[0]
+    mk = lambda pos, wts, e=0: P.WideExpertBinding(e, np.array(pos, np.uint32), np.array(wts, np.float32), *projs[e])
+    full = [mk([0, 1], [0.125, 0.125], e) for e in range(8)]
+    assert rt.execute(x, full, mode=P.MODE_A).expert_rows == 16
+    with pytest.raises(P.PwError, match="SCHEDULE"):
+        rt.execute(x, full[:7], mode=P.MODE_A)  # 14 placements for 2 rows
+    with pytest.raises(P.PwError, match="SCHEDULE"):
+        rt.execute(x, full[:7] + [mk([0, 2], [0.1, 0.1], 7)], mode=P.MODE_A)  # position >= rows
+    with pytest.raises(P.PwError, match="SCHEDULE"):
+        rt.execute(x, full[:7] + [mk([0, 1], [0.1, np.nan], 7)], mode=P.MODE_A)
+    with pytest.raises(P.PwError, match="SCHEDULE"):
+        rt.execute(x, full[:6] + [mk([0, 0], [0.1, 0.1], 6), mk([1, 1], [0.1, 0.1], 7)], mode=P.MODE_A)
+    bad = x.copy()
+    bad[1, 3] = np.inf
+    with pytest.raises(P.PwError, match="NONFINITE"):
+        rt.execute(bad, full, mode=P.MODE_A)
+
+
+def test_complete_expert_widths(rt):
+    """One routed expert (gate/up [2 x 2048 x 4096], down [4096 x 2048]) at widths 1, 2, 4, 8."""
+    import torch
+    bank = WL.synth_bank(rt, n_experts=1, seed=WL.SEED_BASE + 1)
+    host = bank.expert_host(0)
+    for width in (1, 2, 4, 8):
+        x = WL.activations(width, WL.SEED_BASE + 10 + width)
+        xt = torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda()
+        out = torch.empty((width, 4096), dtype=torch.float32, device="cuda")
+        rt.expert_forward_device(bank.bank, 0, xt, width, out, mode=P.MODE_A, out_dtype=P.DTYPE_F32_RAW,
+                                 stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert rt.take_flags() == 0
+        raw = out.cpu().numpy()
+        ref32, ref16 = O.expert_mode_a(x, host)
+        assert normwise(raw, ref32) <= 1e-3 and rel_l2(raw, ref32) <= 1e-5
+        out16 = torch.empty((width, 4096), dtype=torch.float32, device="cuda")
+        rt.expert_forward_device(bank.bank, 0, xt, width, out16, mode=P.MODE_A, out_dtype=P.DTYPE_F32,
+                                 stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert normwise(out16.cpu().numpy(), ref16) <= BF16_OUT
+
+
+@pytest.fixture(scope="module")
+def full_bank(rt):
+    return WL.synth_bank(rt, n_experts=256, seed=WL.SEED_BASE + 2)
+
+
+@pytest.mark.parametrize("zipf", [False, True])
+def test_decode_layer_256_experts_width8(rt, full_bank, zipf):
+    """Width-8 routed-MoE decode layer: top-8 of 256 experts, hidden 4096, intermediate 2048."""
+    import torch
+    x = WL.activations(8, WL.SEED_BASE + 2)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
+    _, _, sel, w, ties = O.route(x, rw, bias)
+    ids = torch.from_numpy(sel.astype(np.int32)).cuda()
+    wts = torch.from_numpy(w).cuda()
+    xt = torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda()
+    used = sorted(set(sel.reshape(-1).tolist()))
+    experts = {e: full_bank.expert_host(e) for e in used}
+    stream = torch.cuda.current_stream().cuda_stream
+    for mode in (P.MODE_A, P.MODE_B):
+        raw = torch.empty((8, 4096), dtype=torch.float32, device="cuda")
+        out = torch.empty((8, 4096), dtype=torch.int16, device="cuda")
+        rt.moe_layer_device(full_bank.bank, xt, 8, ids, wts, raw, mode=mode, out_dtype=P.DTYPE_F32_RAW, stream=stream)
+        rt.moe_layer_device(full_bank.bank, xt, 8, ids, wts, out, mode=mode, out_dtype=P.DTYPE_BF16, stream=stream)
+        torch.cuda.synchronize()
+        assert rt.take_flags() == 0
+        ref, ref_raw = O.moe_layer("a" if mode == P.MODE_A else "b", x, experts, 256, sel, w, raw=True)
+        got16 = (out.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        if mode == P.MODE_A:
+            assert normwise(raw.cpu().numpy(), ref_raw) <= 1e-3
+            assert normwise(got16, ref) <= BF16_OUT
+        else:
+            assert normwise(got16, ref) <= 2e-2
