@@ -66,7 +66,9 @@ def gateup_bytes(sel, rows, hidden=4096, inter=2048):
 
 
 def time_layer(torch, rt, bank, P, dev_batches, rows, steps, warmup, mode):
-    stream = torch.cuda.current_stream()
+    # launches and events on the runtime's own stream (torch's default stream is the null stream,
+    # handle 0, which the library would map to its own stream and the events would not see)
+    stream = torch.cuda.ExternalStream(rt.stream)
     out = torch.empty((rows, 4096), dtype=torch.int16, device="cuda")
     nb = len(dev_batches)
 
@@ -95,7 +97,7 @@ def kernel_times(torch, rt, bank, P, dev_batches, rows, steps, mode):
     rt.enable_timing(steps * 8)
     time_layer(torch, rt, bank, P, dev_batches, rows, steps, 0, mode)
     res = {}
-    for k in ("moe_schedule", "quant", "moe_gateup", "moe_down", "moe_combine"):
+    for k in ("moe_schedule", "quant", "moe_gateup", "moe_swiglu", "moe_down", "moe_combine"):
         n, ms = rt.timing(k)
         if n:
             res[k] = {"launches": n, "avg_us": 1000.0 * ms / n}
@@ -166,7 +168,7 @@ def main():
     achieved = gu_bytes / (gu["avg_us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "moe_a_gateup_kernel", "bytes_per_launch": int(gu_bytes),
+                "kernel": "moe_a_split_kernel (gate+up, SwiGLU)", "bytes_per_launch": int(gu_bytes),
                 "avg_us": round(gu["avg_us"], 2)}
 
     extras = {"kernels_us": {k: round(v["avg_us"], 2) for k, v in kt.items()},

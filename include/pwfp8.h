@@ -17,7 +17,8 @@
  *
  * Threading: one runtime per device, calls on one runtime are serialised by the caller (the
  * reference's &self + one command queue). Host-memory calls are synchronous like the reference;
- * the *_device calls are asynchronous on the HIP stream given (NULL = the runtime's stream).
+ * the *_device calls are asynchronous on the HIP stream given (NULL = the runtime's stream, a
+ * blocking stream, so it is ordered with work on the HIP null stream).
  */
 #ifndef PWFP8_H
 #define PWFP8_H
@@ -142,7 +143,7 @@ int pw_runtime_take_flags(pw_runtime *rt, uint32_t *flags);
 /* Per-kernel HIP-event timing for benchmarks (the reference records GPUStartTime/GPUEndTime per
  * command buffer, src/staged_metal_expert.rs:1763-1771): when enabled, every timed launch records
  * a start and a stop event on the stream it runs on, up to max_launches (0 disables). Kernel
- * names: linear_a, linear_b, quant, moe_schedule, moe_gateup, moe_down, moe_combine,
+ * names: linear_a, linear_b, quant, moe_schedule, moe_gateup, moe_swiglu, moe_down, moe_combine,
  * prefill_gateup, prefill_down, router. */
 int pw_runtime_enable_timing(pw_runtime *rt, uint32_t max_launches);
 /* Synchronise the device; report the recorded launches of `kernel` and their summed duration. */

@@ -31,6 +31,24 @@ __device__ __forceinline__ uint4 load_global16(const void *p)
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Scalar-typed global load through a pointer that was itself read from memory (such pointers are
+// generic, and would otherwise become flat loads that also wait on the LDS counter).
+template <class T>
+__device__ __forceinline__ T load_g(const T *p)
+{
+    return *(const __attribute__((address_space(1))) T *)p;
+}
+
+// Direct global -> LDS load of 16 bytes per lane (gfx950 global_load_lds_dwordx4): lane i's bytes
+// land at lds_wave_base + 16 * i, where lds_wave_base is wave-uniform. The data never occupies
+// VGPRs; completion is counted by the vector-memory counter, so the issuing wave must wait for
+// vmcnt before a barrier that publishes the LDS rows to the other waves.
+__device__ __forceinline__ void lds_load16(const void *src_lane, void *lds_wave_base)
+{
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src_lane,
+                                     (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+}
+
 // Error bits raised by kernels into the runtime's device error word. The low bits keep the
 // meaning of the reference's Metal error word (kernels/block_fp8_gemv.metal, bits 1..128).
 enum : uint32_t {

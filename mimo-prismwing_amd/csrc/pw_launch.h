@@ -16,6 +16,7 @@ enum KernelId : uint32_t {
     K_QUANT,
     K_MOE_SCHEDULE,
     K_MOE_GATEUP,
+    K_MOE_SWIGLU,
     K_MOE_DOWN,
     K_MOE_COMBINE,
     K_PREFILL_GATEUP,
@@ -61,8 +62,6 @@ struct MoeBuffers {
     float *y;                  // [rows * 8 * H]
     ActiveExpert *active;      // [E]   per routed expert: weights, placement slots
     float *partial;            // split-K partial sums of the mode A projections
-    uint32_t *counters;        // [E * max(I, H) / 64] split-K arrival counters
-    uint32_t n_counters;
     uint8_t *xq;               // [rows * H]      mode B activation codes
     float *xs;                 // [rows * H/128]  mode B activation scales
     uint8_t *hq;               // [rows * 8 * I]
@@ -78,12 +77,17 @@ struct SplitArgs {
     const uint16_t *x;              // activation planes [NS][rows][K]
     size_t x_plane;
     uint32_t K, R, KS, rows, P;     // columns, weight rows, K splits, activation rows, placements
+    uint32_t cap;                   // routed rows per expert the LDS stage holds
     float *partial;                 // [KS][MATS][P][R]
-    uint32_t *counters;             // [active][R / 64]
-    uint16_t *hidden;               // gate/up output: three bf16 planes [3][P][R]
-    size_t h_plane;
-    float *y;                       // down output [P][R]
     uint32_t *flags;
+};
+
+// Where a launch left the per-placement expert outputs: `ks` split-K partial sums of [P][H] f32,
+// `stride` floats apart, summed in split order by the consumer (ks = 1: plain outputs).
+struct ExpertOut {
+    const float *y;
+    uint32_t ks;
+    size_t stride;
 };
 
 struct SplitPlan {
@@ -91,11 +95,14 @@ struct SplitPlan {
     size_t lds;
 };
 
-// K split of a mode A expert projection with K columns, NS activation planes and up to max_cnt
-// routed rows per expert.
-SplitPlan plan_split(uint32_t K, int ns, uint32_t max_cnt);
+// K split of a mode A expert projection (`mats` weight matrices sharing the activations) with K
+// columns, NS activation planes and up to max_cnt routed rows per expert.
+SplitPlan plan_split(uint32_t K, int mats, int ns, uint32_t max_cnt);
 void launch_moe_a_split(int mats, int ns, int nt, const SplitArgs &args, const SplitPlan &sp,
                         uint32_t max_active, hipStream_t stream);
+// gate/up split sums -> SwiGLU -> hidden as three bf16 planes [3][P][I]
+void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t I, uint16_t *hidden_planes,
+                         uint32_t *flags, hipStream_t stream);
 
 // The runtime points this at its timer for the duration of one ABI call (calls on a runtime are
 // serialised by the caller, and each thread has its own pointer).

@@ -27,8 +27,7 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids,
     const float *__restrict__ weights, uint32_t rows, uint32_t E, uint32_t max_active,
     MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
-    ActiveExpert *__restrict__ active, uint32_t *__restrict__ counters, uint32_t n_counters,
-    uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
+    ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
     uint32_t *__restrict__ row_slots, uint32_t *flags)
 {
     extern __shared__ uint32_t lds[];
@@ -54,8 +53,6 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
         placement_w[i] = 0.f;
         row_slots[i] = 0;
     }
-    for (uint32_t i = tid; i < n_counters; i += nthr)
-        counters[i] = 0;
     __syncthreads();
     for (uint32_t i = tid; i < P; i += nthr) {
         const uint32_t e = ids[i];
@@ -359,8 +356,22 @@ __global__ __launch_bounds__(64 * KSPLIT) void moe_b_down_kernel(
 // 299-315, src/wide_metal_moe.rs:1252-1286); CPU twin src/text_endpoint.rs:5365-5373. Each token
 // sums its eight placements in ascending expert id, out += y * w in f32 (no fused multiply-add),
 // then rounds to bf16.
+// Sum of `ks` split-K partials of 4 consecutive values, in split order (ks = 1: plain load).
+__device__ __forceinline__ float4 split_sum4(const float *p, uint32_t ks, size_t stride)
+{
+    float4 v = *(const float4 *)p;
+    for (uint32_t s = 1; s < ks; ++s) {
+        const float4 o = *(const float4 *)(p + s * stride);
+        v.x += o.x;
+        v.y += o.y;
+        v.z += o.z;
+        v.w += o.w;
+    }
+    return v;
+}
+
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const float *__restrict__ y, const float *__restrict__ placement_w,
+    const float *__restrict__ y, uint32_t ks, size_t split_stride, const float *__restrict__ placement_w,
     const uint32_t *__restrict__ row_slots, uint32_t rows, uint32_t H, float *__restrict__ out_f32,
     uint16_t *__restrict__ out_bf16, uint32_t raw, uint32_t *flags)
 {
@@ -375,7 +386,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
         uint32_t slot = row_slots[row * 8 + j];
         slot = slot < rows * 8 ? slot : 0;
         const float w = placement_w[slot];
-        const float4 v = *(const float4 *)(y + (size_t)slot * H + c4 * 4);
+        const float4 v = split_sum4(y + (size_t)slot * H + c4 * 4, ks, split_stride);
         acc[0] = __fadd_rn(acc[0], __fmul_rn(v.x, w));
         acc[1] = __fadd_rn(acc[1], __fmul_rn(v.y, w));
         acc[2] = __fadd_rn(acc[2], __fmul_rn(v.z, w));
@@ -403,7 +414,6 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
 __global__ void moe_single_plan_kernel(const ExpertPtrs *bank, uint32_t expert, uint32_t rows,
                                        MoePlan *plan, uint32_t *active_expert,
                                        uint32_t *active_offset, ActiveExpert *active,
-                                       uint32_t *counters, uint32_t n_counters,
                                        uint32_t *placement_pos, float *placement_w)
 {
     const uint32_t i = threadIdx.x;
@@ -424,12 +434,11 @@ __global__ void moe_single_plan_kernel(const ExpertPtrs *bank, uint32_t expert, 
         placement_pos[i] = i;
         placement_w[i] = 1.0f;
     }
-    for (uint32_t c = i; c < n_counters; c += blockDim.x)
-        counters[c] = 0;
 }
 
 // y [rows x H] f32 -> output (bf16-rounded f32 or bf16 bits).
-__global__ __launch_bounds__(256) void round_output_kernel(const float *__restrict__ y, uint32_t n,
+__global__ __launch_bounds__(256) void round_output_kernel(const float *__restrict__ y, uint32_t ks,
+                                                           size_t split_stride, uint32_t n,
                                                            float *__restrict__ out_f32,
                                                            uint16_t *__restrict__ out_bf16,
                                                            uint32_t raw, uint32_t *flags)
@@ -437,11 +446,14 @@ __global__ __launch_bounds__(256) void round_output_kernel(const float *__restri
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n)
         return;
-    const float r = round_bf16(y[i]);
+    float v = y[i];
+    for (uint32_t s = 1; s < ks; ++s)
+        v += y[s * split_stride + i];
+    const float r = round_bf16(v);
     if (!finite_f32(r))
         raise_flag(flags, FLAG_ROUND_NONFINITE);
     if (out_f32)
-        out_f32[i] = raw ? y[i] : r;
+        out_f32[i] = raw ? v : r;
     if (out_bf16)
         out_bf16[i] = (uint16_t)(f32_bits(r) >> 16);
 }
@@ -456,14 +468,14 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
     const int t = timer_begin(K_MOE_SCHEDULE, stream);
     hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
                        E, max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active,
-                       mb.counters, mb.n_counters, mb.placement_pos, mb.placement_w, mb.row_slots, flags);
+                       mb.placement_pos, mb.placement_w, mb.row_slots, flags);
     timer_end(t, stream);
 }
 
 // Mode A: gate/up (+SwiGLU) then down, both as split-K expert projections (pw_moe_a.hip).
-static void launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, uint32_t rows,
-                         uint32_t placements, uint32_t max_active, uint32_t max_count, uint32_t H,
-                         uint32_t I, uint32_t *flags, hipStream_t stream)
+static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, uint32_t rows,
+                              uint32_t placements, uint32_t max_active, uint32_t max_count, uint32_t H,
+                              uint32_t I, uint32_t *flags, hipStream_t stream)
 {
     const int nt = max_count > 16 ? 2 : 1;
     const uint32_t cnt = max_count < 16u * nt ? max_count : 16u * nt;
@@ -482,14 +494,15 @@ static void launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, uint32
     ga.rows = rows;
     ga.P = placements;
     ga.partial = mb.partial;
-    ga.counters = mb.counters;
-    ga.hidden = mb.hidden_planes;
-    ga.h_plane = (size_t)placements * I;
     ga.flags = flags;
-    const SplitPlan gp = plan_split(H, x_f32 ? 3 : 1, cnt);
+    ga.cap = cnt;
+    const SplitPlan gp = plan_split(H, 2, x_f32 ? 3 : 1, cnt);
     ga.KS = gp.ks;
     int t = timer_begin(K_MOE_GATEUP, stream);
     launch_moe_a_split(2, x_f32 ? 3 : 1, nt, ga, gp, max_active, stream);
+    timer_end(t, stream);
+    t = timer_begin(K_MOE_SWIGLU, stream);
+    launch_moe_a_swiglu(mb.partial, gp.ks, placements, I, mb.hidden_planes, flags, stream);
     timer_end(t, stream);
 
     SplitArgs da = ga;
@@ -499,13 +512,12 @@ static void launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, uint32
     da.K = I;
     da.R = H;
     da.rows = placements;
-    da.hidden = nullptr;
-    da.y = mb.y;
-    const SplitPlan dp = plan_split(I, 3, cnt);
+    const SplitPlan dp = plan_split(I, 1, 3, cnt);
     da.KS = dp.ks;
     t = timer_begin(K_MOE_DOWN, stream);
     launch_moe_a_split(1, 3, nt, da, dp, max_active, stream);
     timer_end(t, stream);
+    return ExpertOut{mb.partial, dp.ks, (size_t)placements * H};
 }
 
 template <int KS, int NT>
@@ -526,18 +538,17 @@ static void launch_b_moe(const ExpertPtrs *bank, const MoeBuffers &mb, uint32_t 
     timer_end(t, stream);
 }
 
-static void launch_experts(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
-                           bool x_f32, uint32_t rows, uint32_t placements, uint32_t max_active,
-                           uint32_t max_count, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream)
+static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
+                                bool x_f32, uint32_t rows, uint32_t placements, uint32_t max_active,
+                                uint32_t max_count, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream)
 {
     const bool wide = max_count > 16;
-    if (mode == 0) {
-        launch_a_moe(mb, x, x_f32, rows, placements, max_active, max_count, H, I, flags, stream);
-    } else {
-        launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
-        if (wide) launch_b_moe<4, 2>(bank, mb, rows, placements, max_active, H, I, flags, stream);
-        else launch_b_moe<4, 1>(bank, mb, rows, placements, max_active, H, I, flags, stream);
-    }
+    if (mode == 0)
+        return launch_a_moe(mb, x, x_f32, rows, placements, max_active, max_count, H, I, flags, stream);
+    launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
+    if (wide) launch_b_moe<4, 2>(bank, mb, rows, placements, max_active, H, I, flags, stream);
+    else launch_b_moe<4, 1>(bank, mb, rows, placements, max_active, H, I, flags, stream);
+    return ExpertOut{mb.y, 1, 0};
 }
 
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
@@ -545,11 +556,13 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
                       hipStream_t stream)
 {
-    launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, max_active, max_count, H, I, flags, stream);
+    const ExpertOut eo =
+        launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, max_active, max_count, H, I, flags, stream);
     const uint32_t n4 = rows * (H >> 2);
     const int t = timer_begin(K_MOE_COMBINE, stream);
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((n4 + 255) / 256), dim3(256), 0, stream, mb.y,
-                       mb.placement_w, mb.row_slots, rows, H, out_f32, out_bf16, raw ? 1u : 0u, flags);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((n4 + 255) / 256), dim3(256), 0, stream, eo.y, eo.ks,
+                       eo.stride, mb.placement_w, mb.row_slots, rows, H, out_f32, out_bf16, raw ? 1u : 0u,
+                       flags);
     timer_end(t, stream);
 }
 
@@ -558,12 +571,11 @@ void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, uint32_t exper
                            float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream)
 {
     hipLaunchKernelGGL(moe_single_plan_kernel, dim3(1), dim3(256), 0, stream, bank, expert, rows, mb.plan,
-                       mb.active_expert, mb.active_offset, mb.active, mb.counters, mb.n_counters,
-                       mb.placement_pos, mb.placement_w);
-    launch_experts(mode, bank, mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream);
+                       mb.active_expert, mb.active_offset, mb.active, mb.placement_pos, mb.placement_w);
+    const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream);
     const uint32_t n = rows * H;
-    hipLaunchKernelGGL(round_output_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, mb.y, n, out_f32,
-                       out_bf16, raw ? 1u : 0u, flags);
+    hipLaunchKernelGGL(round_output_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, eo.y, eo.ks, eo.stride,
+                       n, out_f32, out_bf16, raw ? 1u : 0u, flags);
 }
 
 }  // namespace pw

@@ -7,28 +7,29 @@
 // 241-252, 751-933).
 //
 // Work item: (routed expert, 64 weight rows, one K split of KC columns). A workgroup of four
-// waves reads each of its 64 rows x KC bytes exactly once: every lane issues all of its weight
-// loads (16 bytes per instruction, one row per lane, global nontemporal loads) before anything
-// else, so each wave keeps up to 32 KB in flight. The expert's routed activation rows for the K
-// split are staged once in LDS (padded rows, conflict-free 16-byte reads) and shared by the four
-// waves. e4m3 -> bf16 is exact (v_cvt_scalef32_pk_bf16_fp8); activations are bf16 planes (f32
-// values arrive as three exact planes), so v_mfma_f32_16x16x32_bf16 forms exact products and
+// waves reads each of its 64 rows x KC bytes exactly once. The expert's routed activation rows for
+// the K split go straight from global memory into LDS (global_load_lds, padded rows so the later
+// 16-byte reads are conflict-free) and are shared by the four waves; then every lane issues all of
+// its weight loads (16 bytes per instruction, one weight row per lane, nontemporal), at most eight
+// 128-column blocks per lane, so a wave keeps 16 KB in flight on 64 VGPRs and several waves fit
+// on each SIMD. e4m3 -> bf16 is exact (v_cvt_scalef32_pk_bf16_fp8); activations are bf16 planes
+// (f32 values arrive as three exact planes), so v_mfma_f32_16x16x32_bf16 forms exact products and
 // accumulates in f32. The 128x128 block scale multiplies each block partial in registers.
-// Split-K partials go to a global buffer; the last workgroup of a tile to finish (acquire/release
-// counter) sums them in split order 0..KS-1 -- deterministic -- and runs the epilogue: SwiGLU
-// (written as three exact bf16 planes for the down projection) or the expert output row.
+// Split-K partials go to a global buffer; the following kernel sums them in split order 0..KS-1
+// (deterministic): moe_a_swiglu_kernel for gate/up (SwiGLU written as three exact bf16 planes for
+// the down projection), the combine (or the single-expert output rounding) for down.
 #include "pw_device.h"
 #include "pw_launch.h"
 
 namespace pw {
 
 template <int MATS, int NS, int NT, int BPW>
-__global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4 : 2))) void moe_a_split_kernel(const SplitArgs args)
 {
     extern __shared__ uint4 lds_x[];  // [NS * cnt][KC/8 + 1]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar scale loads
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int q = lane >> 4, r16 = lane & 15;
     const uint32_t G = args.R >> 6;
     const uint32_t s = blockIdx.x % args.KS;
@@ -37,14 +38,25 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
     const ActiveExpert ae = args.active[a];
     if (ae.cnt == 0)
         return;
-    if (ae.cnt > 16u * NT) {
+    if (ae.cnt > 16u * NT || ae.cnt > args.cap) {
         if (tid == 0)
             raise_flag(args.flags, FLAG_SCHEDULE);
         return;
     }
-    const uint32_t K = args.K, KC = BPW * 128;
+    const uint32_t K = args.K;
+    constexpr uint32_t KC = BPW * 128;
     const uint32_t k0 = s * KC;
     const uint32_t row_base = g * 64 + wave * 16;  // this wave's 16 rows
+
+    // 1. token row of each routed slot (lane t holds slot t's row): gate/up gather the token
+    //    rows, down reads its own slot rows. Issued first, so the staging below waits only for it.
+    uint32_t tok = 0;
+    if constexpr (MATS == 2) {
+        if ((uint32_t)lane < ae.cnt)
+            tok = load_g(args.placement_pos + ae.off + lane);
+    }
+
+    // 2. every weight byte of this wave's rows and K split, in flight at once
     const uint8_t *wbase[MATS];
     const float *sbase[MATS];
     if constexpr (MATS == 2) {
@@ -56,25 +68,6 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
         wbase[0] = ae.ep.down_w;
         sbase[0] = ae.ep.down_s;
     }
-
-    // 0. source rows of the activation units this thread stages (issued before the weights, so
-    //    the staging loads below never wait behind the weight stream)
-    const uint32_t per_row = KC >> 3, stride = per_row + 1;
-    const uint32_t units = NS * ae.cnt * per_row;
-    constexpr int UMAX = NS * NT * 16 * BPW * 16 / 256;
-    uint32_t srcrow[UMAX];
-#pragma unroll
-    for (int k = 0; k < UMAX; ++k) {
-        const uint32_t u = tid + k * 256;
-        uint32_t src = ae.off + (u / per_row) % ae.cnt;
-        if (u < units && args.placement_pos) {
-            src = args.placement_pos[src];
-            src = src < args.rows ? src : args.rows - 1;
-        }
-        srcrow[k] = src;
-    }
-
-    // 1. every weight byte of this wave's rows and K split, in flight at once
     uint4 wv[MATS][BPW][2];
 #pragma unroll
     for (int m = 0; m < MATS; ++m) {
@@ -85,8 +78,7 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
             for (int h = 0; h < 2; ++h)
                 wv[m][j][h] = load_stream16(wrow + j * 128 + h * 64);
     }
-
-    // block scales of this wave's 16 rows (one 128-row scale block), scalar loads
+    // block scales of this wave's 16 rows (one 128-row scale block, wave-uniform)
     const uint32_t blocks = K >> 7;
     const uint32_t srow = row_base >> 7;
     float sc[MATS][BPW];
@@ -94,29 +86,46 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
     for (int m = 0; m < MATS; ++m)
 #pragma unroll
         for (int j = 0; j < BPW; ++j)
-            sc[m][j] = sbase[m][srow * blocks + (k0 >> 7) + j];
+            sc[m][j] = load_g(sbase[m] + srow * blocks + (k0 >> 7) + j);
 
-    // 2. stage the routed activation rows of this K split in LDS: [plane][token][KC/8 + 1]
-    uint4 xv[UMAX];
+    // 3. the routed activation rows of this K split -> LDS [plane][token][KC/8 + 1], one
+    //    direct-to-LDS instruction per (plane, token, 64-unit chunk), no registers involved
+    constexpr uint32_t PER_ROW = KC / 8;                      // 16-byte units per row
+    constexpr uint32_t STRIDE = PER_ROW + 1;                  // padded LDS row
+    constexpr uint32_t LANES = PER_ROW < 64 ? PER_ROW : 64;   // active lanes per instruction
+    constexpr uint32_t CPR = PER_ROW / LANES;                 // instructions per row
+    // Fully unrolled over (token, plane, chunk) -- a loop here would make the compiler wait for
+    // every outstanding weight load before its first iteration -- and dealt round-robin to the
+    // four waves.
+    bool bad_row = false;
 #pragma unroll
-    for (int k = 0; k < UMAX; ++k) {
-        const uint32_t u = tid + k * 256;
-        if (u < units) {
-            const uint32_t c = u % per_row, p = u / (per_row * ae.cnt);
-            xv[k] = load_global16(args.x + p * args.x_plane + (size_t)srcrow[k] * K + k0 + c * 8);
+    for (uint32_t t = 0; t < 16u * NT; ++t) {
+        if (t < ae.cnt) {
+            uint32_t src = ae.off + t;
+            if constexpr (MATS == 2) {
+                src = __builtin_amdgcn_readlane(tok, t);
+                if (src >= args.rows) {
+                    bad_row = true;
+                    src = args.rows - 1;
+                }
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < (uint32_t)NS; ++p)
+#pragma unroll
+                for (uint32_t c = 0; c < CPR; ++c)
+                    if (((t * NS + p) * CPR + c) % 4 == (uint32_t)wave && (uint32_t)lane < LANES)
+                        lds_load16(args.x + p * args.x_plane + (size_t)src * K + k0 + (c * 64 + lane) * 8,
+                                   lds_x + (p * ae.cnt + t) * STRIDE + c * 64);
         }
     }
-#pragma unroll
-    for (int k = 0; k < UMAX; ++k) {
-        const uint32_t u = tid + k * 256;
-        if (u < units) {
-            const uint32_t c = u % per_row, rowi = u / per_row;  // rowi = p * cnt + t
-            lds_x[rowi * stride + c] = xv[k];
-        }
-    }
+    if (bad_row && lane == 0)
+        raise_flag(args.flags, FLAG_SCHEDULE);
+
+    // the LDS rows this wave loaded are complete before the barrier publishes them
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    // 3. block partials on the MFMA, block scale in registers
+    // 4. block partials on the MFMA, block scale in registers
     f32x4 tot[MATS][NT];
 #pragma unroll
     for (int m = 0; m < MATS; ++m)
@@ -139,7 +148,7 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
                 A[m][0] = fp8x8_to_bf16x8(wv[m][j][h].x, wv[m][j][h].y);
                 A[m][1] = fp8x8_to_bf16x8(wv[m][j][h].z, wv[m][j][h].w);
             }
-            const uint32_t cu = j * 16 + h * 8 + q * 2;  // column in uint4 units
+            const uint32_t cu = j * 16 + h * 8 + q * 2;  // column in 16-byte units
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const uint32_t t = nt * 16 + r16;
@@ -148,7 +157,7 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
                 for (int p = 0; p < NS; ++p) {
                     uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
                     if (ok) {
-                        const uint4 *xp = lds_x + (p * ae.cnt + t) * stride + cu;
+                        const uint4 *xp = lds_x + (p * ae.cnt + t) * STRIDE + cu;
                         x0 = xp[0];
                         x1 = xp[1];
                     }
@@ -169,7 +178,9 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
                     tot[m][nt][i] = __builtin_fmaf(sc[m][j], acc[m][nt][i], tot[m][nt][i]);
     }
 
-    // 4. split-K partials: partial[s][m][slot][row]
+    // 5. split-K partials: partial[s][m][slot][row]. The splits are summed in split order by the
+    //    next kernel (moe_a_swiglu_kernel, or the combine for the down projection): no
+    //    cross-workgroup synchronisation, so no device-scope cache maintenance per workgroup.
     const uint32_t P = args.P, R = args.R;
     const uint32_t row4 = row_base + q * 4;
 #pragma unroll
@@ -181,76 +192,71 @@ __global__ __launch_bounds__(256) void moe_a_split_kernel(const SplitArgs args)
                 *(float4 *)(args.partial + (((size_t)s * MATS + m) * P + ae.off + t) * R + row4) =
                     make_float4(tot[m][nt][0], tot[m][nt][1], tot[m][nt][2], tot[m][nt][3]);
         }
-    __threadfence();
-    __syncthreads();
-    __shared__ uint32_t s_last;
-    if (tid == 0) {
-        uint32_t *ctr = args.counters + a * G + g;
-        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = old == args.KS - 1;
-        if (s_last)
-            __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!s_last)
-        return;
-    __threadfence();
+}
 
-    // 5. epilogue by the last workgroup: sum the splits in order, then SwiGLU or the output row
+// Gate/up split sums (in split order 0..KS-1) -> h = (g / (1 + e^-g)) * u in f32 (swiglu_f32,
+// kernels/block_fp8_gemv.metal:241-252; CPU src/lib.rs:5840-5844), written as three exact bf16
+// planes for the down projection's MFMA. One thread per (slot, 4 rows).
+__global__ __launch_bounds__(256) void moe_a_swiglu_kernel(const float *__restrict__ partial, uint32_t KS,
+                                                           uint32_t P, uint32_t R, uint16_t *__restrict__ hidden,
+                                                           uint32_t *flags)
+{
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t per_slot = R >> 2;
+    if (idx >= P * per_slot)
+        return;
+    const uint32_t slot = idx / per_slot, row4 = (idx - slot * per_slot) * 4;
+    float v[2][4];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        float4 sum = *(const float4 *)(partial + ((size_t)m * P + slot) * R + row4);
+        for (uint32_t sp = 1; sp < KS; ++sp) {
+            const float4 o = *(const float4 *)(partial + (((size_t)sp * 2 + m) * P + slot) * R + row4);
+            sum.x += o.x;
+            sum.y += o.y;
+            sum.z += o.z;
+            sum.w += o.w;
+        }
+        v[m][0] = sum.x; v[m][1] = sum.y; v[m][2] = sum.z; v[m][3] = sum.w;
+    }
+    uint16_t hp[3][4];
     bool bad = false;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t t = nt * 16 + r16;
-        if (t >= ae.cnt)
-            continue;
-        const uint32_t slot = ae.off + t;
-        float v[MATS][4];
-#pragma unroll
-        for (int m = 0; m < MATS; ++m) {
-            const uint4 first = load_global16(args.partial + ((size_t)m * P + slot) * R + row4);
-            float4 sum = make_float4(f32_from(first.x), f32_from(first.y), f32_from(first.z), f32_from(first.w));
-            for (uint32_t sp = 1; sp < args.KS; ++sp) {
-                const uint4 o = load_global16(args.partial + (((size_t)sp * MATS + m) * P + slot) * R + row4);
-                sum.x += f32_from(o.x);
-                sum.y += f32_from(o.y);
-                sum.z += f32_from(o.z);
-                sum.w += f32_from(o.w);
-            }
-            v[m][0] = sum.x; v[m][1] = sum.y; v[m][2] = sum.z; v[m][3] = sum.w;
-        }
-        if constexpr (MATS == 2) {
-            uint16_t hp[3][4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float gv = v[0][i];
-                const float hv = (gv / (1.0f + expf(-gv))) * v[1][i];
-                bad |= !finite_f32(hv);
-                split3_bf16(hv, hp[0][i], hp[1][i], hp[2][i]);
-            }
-            uint16_t *dst = args.hidden + (size_t)slot * R + row4;
-#pragma unroll
-            for (int pl = 0; pl < 3; ++pl)
-                *(uint2 *)(dst + pl * args.h_plane) =
-                    make_uint2((uint32_t)hp[pl][0] | ((uint32_t)hp[pl][1] << 16),
-                               (uint32_t)hp[pl][2] | ((uint32_t)hp[pl][3] << 16));
-        } else {
-            *(float4 *)(args.y + (size_t)slot * R + row4) = make_float4(v[0][0], v[0][1], v[0][2], v[0][3]);
-        }
+    for (int i = 0; i < 4; ++i) {
+        const float gv = v[0][i];
+        const float hv = (gv / (1.0f + expf(-gv))) * v[1][i];
+        bad |= !finite_f32(hv);
+        split3_bf16(hv, hp[0][i], hp[1][i], hp[2][i]);
     }
+    const size_t plane = (size_t)P * R;
+    uint16_t *dst = hidden + (size_t)slot * R + row4;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+        *(uint2 *)(dst + pl * plane) = make_uint2((uint32_t)hp[pl][0] | ((uint32_t)hp[pl][1] << 16),
+                                                  (uint32_t)hp[pl][2] | ((uint32_t)hp[pl][3] << 16));
     if (bad)
-        raise_flag(args.flags, FLAG_SWIGLU_NONFINITE);
+        raise_flag(flags, FLAG_SWIGLU_NONFINITE);
+}
+
+void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t I, uint16_t *hidden_planes,
+                         uint32_t *flags, hipStream_t stream)
+{
+    const uint32_t n = P * (I >> 2);
+    hipLaunchKernelGGL(moe_a_swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, partial, ks, P, I,
+                       hidden_planes, flags);
 }
 
 // LDS bytes of a split: NS planes x cnt rows x (KC/8 + 1) 16-byte units.
 static size_t split_lds(int ns, uint32_t cnt, uint32_t kc) { return (size_t)ns * cnt * (kc / 8 + 1) * 16; }
 
-SplitPlan plan_split(uint32_t K, int ns, uint32_t max_cnt)
+SplitPlan plan_split(uint32_t K, int mats, int ns, uint32_t max_cnt)
 {
-    // widest K split whose activation stage fits 64 KB of LDS, at most 8 blocks per lane
+    // widest K split with at most eight 128-column weight blocks per lane (64 VGPRs of weights)
+    // whose activation stage fits 64 KB of LDS
     SplitPlan sp{};
-    for (uint32_t bpw = 8; bpw >= 2; bpw /= 2) {
+    for (uint32_t bpw = 8 / (uint32_t)mats; bpw >= 1; bpw /= 2) {
         const uint32_t kc = bpw * 128;
-        if (K % kc == 0 && split_lds(ns, max_cnt, kc) <= 65536) {
+        if ((K % kc == 0 && split_lds(ns, max_cnt, kc) <= 65536) || bpw == 1) {
             sp.bpw = bpw;
             sp.kc = kc;
             sp.ks = K / kc;
@@ -258,10 +264,6 @@ SplitPlan plan_split(uint32_t K, int ns, uint32_t max_cnt)
             return sp;
         }
     }
-    sp.bpw = 1;
-    sp.kc = 128;
-    sp.ks = K / 128;
-    sp.lds = split_lds(ns, max_cnt, 128);
     return sp;
 }
 
@@ -270,8 +272,11 @@ static void launch_split_nt(const SplitArgs &args, const SplitPlan &sp, uint32_t
 {
     switch (sp.bpw) {
     case 8:
-        hipLaunchKernelGGL((moe_a_split_kernel<MATS, NS, NT, 8>), dim3(grid), dim3(256), sp.lds, stream, args);
-        break;
+        if constexpr (MATS == 1) {
+            hipLaunchKernelGGL((moe_a_split_kernel<MATS, NS, NT, 8>), dim3(grid), dim3(256), sp.lds, stream, args);
+            break;
+        }
+        [[fallthrough]];
     case 4:
         hipLaunchKernelGGL((moe_a_split_kernel<MATS, NS, NT, 4>), dim3(grid), dim3(256), sp.lds, stream, args);
         break;

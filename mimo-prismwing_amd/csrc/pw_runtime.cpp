@@ -31,8 +31,8 @@ thread_local KernelTimer *tl_timer = nullptr;
 namespace {
 
 const char *const kKernelNames[pw::K_COUNT] = {
-    "linear_a", "linear_b", "quant", "moe_schedule", "moe_gateup", "moe_down", "moe_combine",
-    "prefill_gateup", "prefill_down", "router"};
+    "linear_a", "linear_b", "quant", "moe_schedule", "moe_gateup", "moe_swiglu", "moe_down",
+    "moe_combine", "prefill_gateup", "prefill_down", "router"};
 
 thread_local std::string g_error;
 
@@ -98,7 +98,7 @@ struct pw_runtime {
     // routed-MoE per-layer scratch
     DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
         moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
-        moe_active, moe_partial, moe_counters;
+        moe_active, moe_partial;
     MoeBuffers mb{};
     pw::KernelTimer timer;
 };
@@ -266,17 +266,13 @@ int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I
     PW_HIP(rt->moe_hs.ensure(P * (I / 128) * 4));
     // split-K partials of the mode A projections, sized for the widest split the launch can pick
     const uint32_t cnt = std::min<uint32_t>(rows, 32);
-    const size_t ks_gu = std::max(pw::plan_split(H, 1, cnt).ks, pw::plan_split(H, 3, cnt).ks);
-    const size_t ks_d = pw::plan_split(I, 3, cnt).ks;
+    const size_t ks_gu = std::max(pw::plan_split(H, 2, 1, cnt).ks, pw::plan_split(H, 2, 3, cnt).ks);
+    const size_t ks_d = pw::plan_split(I, 1, 3, cnt).ks;
     PW_HIP(rt->moe_active.ensure((size_t)(E + 1) * sizeof(pw::ActiveExpert)));
     PW_HIP(rt->moe_partial.ensure(std::max(ks_gu * 2 * P * I, ks_d * P * H) * 4));
-    const uint32_t n_counters = E * (std::max(I, H) / 64);
-    PW_HIP(rt->moe_counters.ensure((size_t)n_counters * 4));
     MoeBuffers &mb = rt->mb;
     mb.active = (pw::ActiveExpert *)rt->moe_active.p;
     mb.partial = (float *)rt->moe_partial.p;
-    mb.counters = (uint32_t *)rt->moe_counters.p;
-    mb.n_counters = n_counters;
     mb.plan = (pw::MoePlan *)rt->moe_plan.p;
     mb.active_expert = (uint32_t *)rt->moe_active_expert.p;
     mb.active_offset = (uint32_t *)rt->moe_active_offset.p;
@@ -485,7 +481,9 @@ int pw_runtime_create(int device, uint32_t flags, pw_runtime **out)
     rt->flags = flags;
     hipError_t e = hipSetDevice(device);
     if (e == hipSuccess)
-        e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking);
+        // a blocking stream: work the caller enqueued on the null stream (e.g. a framework's default
+        // stream) is ordered before the runtime's launches, and vice versa
+        e = hipStreamCreateWithFlags(&rt->stream, hipStreamDefault);
     if (e == hipSuccess)
         e = hipMalloc((void **)&rt->d_flags, sizeof(uint32_t));
     if (e == hipSuccess)
