@@ -81,14 +81,18 @@ struct ExpertPtrs {
     const float *down_s;
 };
 
-// One routed expert's entry of the device schedule: its weights and its placement slots
-// [off, off + cnt). Entries past the last routed expert have cnt = 0.
+// One routed expert's entry of the device schedule: its weights, its placement slots
+// [off, off + cnt) and the token rows of its first 16 slots (read with the entry's scalar load,
+// so the gate/up kernel can start its activation gather without a dependent load). Entries past
+// the last routed expert have cnt = 0.
 struct ActiveExpert {
     ExpertPtrs ep;
     uint32_t off;
     uint32_t cnt;
+    uint16_t tok[16];
     uint32_t pad[2];
 };
+static_assert(sizeof(ActiveExpert) == 96, "ActiveExpert is read as 96 bytes");
 
 // Device-side routed schedule (ascending expert id, positions ascending per expert), the
 // layout of the reference's BTreeMap<expert, [(position, weight)]> (src/text_endpoint.rs:4767-4775).

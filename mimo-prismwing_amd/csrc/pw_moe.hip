@@ -21,8 +21,46 @@
 namespace pw {
 
 // ------------------------------------------------------------------------------- schedule
-// One workgroup. LDS holds a bit per (expert, token row): rank of a placement inside its expert =
-// number of set bits below its row, so placements land in ascending row order without sorting.
+// Exclusive prefix sum over the workgroup (blockDim.x <= 1024): wave scans with lane shuffles,
+// then a scan of the per-wave totals. `tmp` holds 16 words of LDS. Returns the total in *total.
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp, uint32_t *total)
+{
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(inc, d, 64);
+        if (lane >= (uint32_t)d)
+            inc += o;
+    }
+    if (lane == 63)
+        tmp[wave] = inc;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        uint32_t w = threadIdx.x < nw ? tmp[threadIdx.x] : 0u;
+        uint32_t wi = w;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            const uint32_t o = __shfl_up(wi, d, 64);
+            if (threadIdx.x >= (uint32_t)d)
+                wi += o;
+        }
+        if (threadIdx.x < nw)
+            tmp[16 + threadIdx.x] = wi - w;  // exclusive wave offsets
+        if (threadIdx.x == nw - 1)
+            tmp[32] = wi;
+    }
+    __syncthreads();
+    const uint32_t r = tmp[16 + wave] + inc - v;
+    *total = tmp[32];
+    __syncthreads();  // tmp is reused by the next scan
+    return r;
+}
+
+// One workgroup (1024 threads, E <= 1024 experts). LDS holds a bit per (expert, token row): the
+// rank of a placement inside its expert is the number of set bits below its row, so placements
+// land in ascending row order without sorting (the reference's BTreeMap<expert, [(position,
+// weight)]>, src/text_endpoint.rs:4767-4775). Counts and offsets come from block-wide scans.
 __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids,
     const float *__restrict__ weights, uint32_t rows, uint32_t E, uint32_t max_active,
@@ -33,26 +71,16 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     extern __shared__ uint32_t lds[];
     const uint32_t words = (rows + 31) >> 5;
     uint32_t *mask = lds;                  // [E][words]
-    uint32_t *count = mask + E * words;    // [E]
-    uint32_t *offset = count + E;          // [E]
-    uint32_t *act_idx = offset + E;        // [E]
-    __shared__ uint32_t s_bad, s_total, s_active, s_max;
+    uint32_t *offset = mask + E * words;   // [E]
+    __shared__ uint32_t s_bad, s_max, s_scan[48];
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t P = rows * 8;
     if (tid == 0) {
         s_bad = 0;
-        s_total = 0;
-        s_active = 0;
         s_max = 0;
     }
     for (uint32_t i = tid; i < E * words; i += nthr)
         mask[i] = 0;
-    // every consumer index starts valid even when the route buffers are rejected below
-    for (uint32_t i = tid; i < P; i += nthr) {
-        placement_pos[i] = 0;
-        placement_w[i] = 0.f;
-        row_slots[i] = 0;
-    }
     __syncthreads();
     for (uint32_t i = tid; i < P; i += nthr) {
         const uint32_t e = ids[i];
@@ -67,71 +95,80 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
             atomicOr(&s_bad, 1u);  // the same expert twice in one token's routes
     }
     __syncthreads();
-    for (uint32_t e = tid; e < E; e += nthr) {
-        uint32_t c = 0;
+    // thread e: expert e's count, its slot offset and its index among the routed experts
+    const uint32_t e = tid;
+    uint32_t c = 0;
+    if (e < E)
         for (uint32_t w = 0; w < words; ++w)
             c += __popc(mask[e * words + w]);
-        count[e] = c;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        // serial exclusive scans over <= 256 experts: a few microseconds at most, once per layer
-        uint32_t run = 0, act = 0, mx = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            offset[e] = run;
-            act_idx[e] = act;
-            if (count[e]) {
-                active_expert[act] = e;
-                active_offset[act] = run;
-                ++act;
-                mx = count[e] > mx ? count[e] : mx;
+    uint32_t total, n_active;
+    const uint32_t off = block_exclusive_scan(c, s_scan, &total);
+    const uint32_t act = block_exclusive_scan(c ? 1u : 0u, s_scan, &n_active);
+    if (e < E) {
+        offset[e] = off;
+        if (c) {
+            active_expert[act] = e;
+            active_offset[act] = off;
+            ActiveExpert ae{};
+            ae.ep = bank[e];
+            ae.off = off;
+            ae.cnt = c;
+            uint32_t k = 0;  // token rows of the first 16 slots, ascending
+            for (uint32_t w = 0; w < words && k < 16; ++w) {
+                uint32_t bits = mask[e * words + w];
+                while (bits && k < 16) {
+                    ae.tok[k++] = (uint16_t)(w * 32 + __builtin_ctz(bits));
+                    bits &= bits - 1;
+                }
             }
-            run += count[e];
+            if (act < max_active)
+                active[act] = ae;
+            atomicMax(&s_max, c);
         }
-        active_offset[act] = run;
-        s_total = run;
-        s_active = act;
-        s_max = mx;
+    }
+    if (tid == 0)
+        active_offset[n_active] = total;
+    // entries past the last routed expert: cnt = 0, the projection workgroups exit at once
+    for (uint32_t a = n_active + tid; a < max_active; a += nthr)
+        active[a] = ActiveExpert{};
+    // every consumer index starts valid even when the route buffers are rejected
+    for (uint32_t i = tid; i < P; i += nthr) {
+        placement_pos[i] = 0;
+        placement_w[i] = 0.f;
+        row_slots[i] = 0;
     }
     __syncthreads();
     for (uint32_t i = tid; i < P; i += nthr) {
-        const uint32_t e = ids[i];
-        if (e >= E)
+        const uint32_t ei = ids[i];
+        if (ei >= E || !finite_f32(weights[i]))
             continue;
         const uint32_t p = i >> 3;
         uint32_t rank = 0;
         for (uint32_t w = 0; w < (p >> 5); ++w)
-            rank += __popc(mask[e * words + w]);
-        rank += __popc(mask[e * words + (p >> 5)] & ((1u << (p & 31)) - 1u));
-        const uint32_t slot = offset[e] + rank;
+            rank += __popc(mask[ei * words + w]);
+        rank += __popc(mask[ei * words + (p >> 5)] & ((1u << (p & 31)) - 1u));
+        const uint32_t slot = offset[ei] + rank;
+        if (slot >= P)
+            continue;  // only when the routes were rejected above
         placement_pos[slot] = p;
         placement_w[slot] = weights[i];
         // position of this placement among its token's eight, ordered by expert id
         uint32_t before = 0;
         for (uint32_t j = 0; j < 8; ++j) {
             const uint32_t other = ids[p * 8 + j];
-            before += other < e ? 1u : 0u;
+            before += other < ei ? 1u : 0u;
         }
         row_slots[p * 8 + (before & 7)] = slot;
     }
-    // per-expert entries read by the projection kernels (cnt = 0 past the last routed expert)
-    for (uint32_t a = tid; a < max_active; a += nthr) {
-        ActiveExpert ae{};
-        if (a < s_active) {
-            ae.ep = bank[active_expert[a]];
-            ae.off = active_offset[a];
-            ae.cnt = active_offset[a + 1] - ae.off;
-        }
-        active[a] = ae;
-    }
     if (tid == 0) {
-        plan->n_active = s_active;
-        plan->n_placements = s_total;
+        plan->n_active = n_active;
+        plan->n_placements = total;
         plan->max_count = s_max;
-        if (s_bad || s_total != P)
+        if (s_bad || total != P)
             raise_flag(flags, FLAG_SCHEDULE);
     }
 }
+
 
 // --------------------------------------------------------------- shared tile preamble
 struct ExpertTile {
@@ -428,6 +465,8 @@ __global__ void moe_single_plan_kernel(const ExpertPtrs *bank, uint32_t expert, 
         ae.ep = bank[expert];
         ae.off = 0;
         ae.cnt = rows;
+        for (uint32_t k = 0; k < 16; ++k)
+            ae.tok[k] = (uint16_t)k;
         active[0] = ae;
     }
     if (i < rows) {
@@ -464,7 +503,7 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
                          uint32_t *flags, hipStream_t stream)
 {
     const uint32_t words = (rows + 31) >> 5;
-    const size_t lds = (size_t)(E * words + 3 * E) * sizeof(uint32_t);
+    const size_t lds = (size_t)(E * words + E) * sizeof(uint32_t);
     const int t = timer_begin(K_MOE_SCHEDULE, stream);
     hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
                        E, max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active,

@@ -48,11 +48,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
     const uint32_t k0 = s * KC;
     const uint32_t row_base = g * 64 + wave * 16;  // this wave's 16 rows
 
-    // 1. token row of each routed slot (lane t holds slot t's row): gate/up gather the token
-    //    rows, down reads its own slot rows. Issued first, so the staging below waits only for it.
+    // 1. token rows of routed slots 16..31 (lane t holds slot t's row; slots 0..15 come with the
+    //    schedule entry): gate/up gather the token rows, down reads its own slot rows. Issued
+    //    first, so the staging below waits only for it.
     uint32_t tok = 0;
-    if constexpr (MATS == 2) {
-        if ((uint32_t)lane < ae.cnt)
+    if constexpr (MATS == 2 && NT == 2) {
+        if ((uint32_t)lane >= 16 && (uint32_t)lane < ae.cnt)
             tok = load_g(args.placement_pos + ae.off + lane);
     }
 
@@ -103,7 +104,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
         if (t < ae.cnt) {
             uint32_t src = ae.off + t;
             if constexpr (MATS == 2) {
-                src = __builtin_amdgcn_readlane(tok, t);
+                src = t < 16 ? (uint32_t)ae.tok[t] : __builtin_amdgcn_readlane(tok, t);
                 if (src >= args.rows) {
                     bad_row = true;
                     src = args.rows - 1;

@@ -1007,6 +1007,8 @@ int pw_expert_bank_create(pw_runtime *rt, uint32_t n_experts, const pw_projectio
 {
     if (!rt || !gate || !up || !down || !out || n_experts == 0)
         return fail(PW_ERR_ARGUMENT, "null argument or empty bank");
+    if (n_experts > 1024)  // the device schedule gives one thread to each expert
+        return fail(PW_ERR_ARGUMENT, "a bank holds at most 1024 experts (got %u)", n_experts);
     *out = nullptr;
     if (!gate[0])
         return fail(PW_ERR_LAYOUT, "expert 0 has no gate projection");
