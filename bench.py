@@ -105,6 +105,57 @@ def kernel_times(torch, rt, bank, P, dev_batches, rows, steps, mode):
     return res
 
 
+PREFILL_ROWS = 2048
+EXPERT_MACS = 3 * 2048 * 4096                  # multiply-adds per placement (gate, up, down)
+FP8_PEAK_TFLOPS = 5000.0                       # MI355X dense FP8 MFMA
+
+
+def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
+    """Routed-MoE prefill over 2048 tokens (16 384 placements, mode B grouped FP8 GEMM)."""
+    rows = PREFILL_ROWS
+    x = WL.activations(rows, WL.SEED_BASE + 4)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
+    sel, w, _ = WL.route_host(x, rw, bias)
+    xt = torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda()
+    ids = torch.from_numpy(sel.astype(np.int32)).cuda()
+    wts = torch.from_numpy(w).cuda()
+    out = torch.empty((rows, 4096), dtype=torch.int16, device="cuda")
+    stream = torch.cuda.ExternalStream(rt.stream)
+
+    def run():
+        rt.moe_prefill_device(bank.bank, xt, rows, ids, wts, out, out_dtype=P.DTYPE_BF16, stream=stream.cuda_stream)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        run()
+    end.record(stream)
+    torch.cuda.synchronize()
+    if rt.take_flags():
+        raise RuntimeError("prefill kernels raised error flags")
+    ms = start.elapsed_time(end) / steps
+    rt.enable_timing(steps * 8)
+    for _ in range(steps):
+        run()
+    kt = {}  # average µs per launch (the quantiser runs twice per layer: x, then the hidden)
+    for k in ("moe_schedule", "quant", "prefill_gateup", "prefill_down", "moe_combine"):
+        n, tot = rt.timing(k)
+        if n:
+            kt[k] = round(1000.0 * tot / n, 2)
+    rt.enable_timing(0)
+    u = int(np.unique(sel).size)
+    flops = 2.0 * rows * 8 * EXPERT_MACS
+    wbytes = u * (EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES)
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"layer_us": round(ms * 1000, 2), "TFLOP/s": round(tflops, 1),
+            "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+            "weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1), "unique_experts": u,
+            "max_count": int(np.bincount(sel.reshape(-1), minlength=256).max()), "kernels_us": kt}
+
+
 def cpu_baseline(WL, bank, batch, budget_s=12.0):
     """The C oracle (mode A, single thread) on a bounded sample of the same layer: the routed
     experts of one width-8 batch, taken in ascending id until ~budget_s of CPU work."""
@@ -191,6 +242,8 @@ def main():
         ms1 = time_layer(torch, rt, bank, P, d1, 1, args.steps, args.warmup, P.MODE_A)
         extras["w1"] = {"layer_us": round(ms1 * 1000, 2),
                         "GB/s": round(float(np.mean([b for _, b in s1])) / (ms1 * 1e-3) / 1e9, 1)}
+        for zipf in (False, True):
+            extras["prefill_t2048" + ("_zipf" if zipf else "")] = prefill_leg(torch, rt, bank, P, WL, zipf)
         for k, v in extras.items():
             if isinstance(v, dict) and "layer_us" in v:
                 log(f"{k}: {v}")

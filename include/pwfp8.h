@@ -217,6 +217,17 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
                         uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
                         const float *route_weights, void *output, uint32_t out_dtype, void *stream);
 
+/* Routed-MoE prefill over many token rows (rows 1..4096, e.g. 2048 tokens -> 16 384 placements)
+ * with inputs in device memory, in mode B: the reference's layer-major prefill runs 128-row
+ * slices through WideMetalMoeRuntime::execute (run_layer_major_moe_slice_mode,
+ * src/text_endpoint.rs:4951-5287; src/wide_metal_moe.rs:852-1314), here one grouped block-FP8
+ * GEMM per projection on the FP8 MFMA (any number of placements per expert). x [rows x hidden]
+ * (x_dtype), route_ids / route_weights [rows x 8], output [rows x hidden] (out_dtype,
+ * bf16-rounded). Asynchronous on stream; kernel error bits accumulate in the runtime's word. */
+int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void *x, uint32_t x_dtype,
+                          uint32_t rows, const uint32_t *route_ids, const float *route_weights, void *output,
+                          uint32_t out_dtype, void *stream);
+
 /* One complete expert (gate/up -> SwiGLU -> down, no routing, no combine) on device rows
  * x [rows x hidden] -> output [rows x hidden] bf16-rounded: the reference's complete-expert
  * measurement (direct-checkpoint L3 expert, src/lib.rs:4008-6590; mode A widths 1..8 via

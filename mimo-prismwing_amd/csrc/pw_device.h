@@ -169,4 +169,40 @@ __device__ __forceinline__ void raise_flag(uint32_t *flags, uint32_t bit)
         __hip_atomic_fetch_or(flags, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Exclusive prefix sum over the workgroup (blockDim.x <= 1024): wave scans with lane shuffles,
+// then a scan of the per-wave totals. `tmp` holds 33 words of LDS. Returns the total in *total.
+__device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp, uint32_t *total)
+{
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(inc, d, 64);
+        if (lane >= (uint32_t)d)
+            inc += o;
+    }
+    if (lane == 63)
+        tmp[wave] = inc;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        uint32_t w = threadIdx.x < nw ? tmp[threadIdx.x] : 0u;
+        uint32_t wi = w;
+#pragma unroll
+        for (int d = 1; d < 16; d <<= 1) {
+            const uint32_t o = __shfl_up(wi, d, 64);
+            if (threadIdx.x >= (uint32_t)d)
+                wi += o;
+        }
+        if (threadIdx.x < nw)
+            tmp[16 + threadIdx.x] = wi - w;  // exclusive wave offsets
+        if (threadIdx.x == nw - 1)
+            tmp[32] = wi;
+    }
+    __syncthreads();
+    const uint32_t r = tmp[16 + wave] + inc - v;
+    *total = tmp[32];
+    __syncthreads();  // tmp is reused by the next scan
+    return r;
+}
+
 }  // namespace pw

@@ -135,6 +135,18 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
                       hipStream_t stream);
 
+// Routed-MoE prefill (mode B grouped block-FP8 GEMM, pw_prefill.hip) after launch_moe_schedule.
+struct PrefillBuffers {
+    uint2 *tiles;       // [prefill_max_tiles] (schedule entry, first slot of a 64-slot m-tile)
+    uint32_t *n_tiles;  // [1]
+    uint16_t *hidden;   // [rows * 8][I] bf16 SwiGLU output
+    uint16_t *y;        // [rows * 8][H] bf16 expert outputs
+};
+uint32_t prefill_max_tiles(uint32_t rows, uint32_t E);
+void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
+                        bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,
+                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream);
+
 void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, uint32_t expert, const MoeBuffers &mb,
                            const void *x, bool x_f32, uint32_t rows, uint32_t H, uint32_t I,
                            float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream);

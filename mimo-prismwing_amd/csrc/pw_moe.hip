@@ -21,42 +21,6 @@
 namespace pw {
 
 // ------------------------------------------------------------------------------- schedule
-// Exclusive prefix sum over the workgroup (blockDim.x <= 1024): wave scans with lane shuffles,
-// then a scan of the per-wave totals. `tmp` holds 16 words of LDS. Returns the total in *total.
-__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp, uint32_t *total)
-{
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-    uint32_t inc = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_up(inc, d, 64);
-        if (lane >= (uint32_t)d)
-            inc += o;
-    }
-    if (lane == 63)
-        tmp[wave] = inc;
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        uint32_t w = threadIdx.x < nw ? tmp[threadIdx.x] : 0u;
-        uint32_t wi = w;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-            const uint32_t o = __shfl_up(wi, d, 64);
-            if (threadIdx.x >= (uint32_t)d)
-                wi += o;
-        }
-        if (threadIdx.x < nw)
-            tmp[16 + threadIdx.x] = wi - w;  // exclusive wave offsets
-        if (threadIdx.x == nw - 1)
-            tmp[32] = wi;
-    }
-    __syncthreads();
-    const uint32_t r = tmp[16 + wave] + inc - v;
-    *total = tmp[32];
-    __syncthreads();  // tmp is reused by the next scan
-    return r;
-}
-
 // One workgroup (1024 threads, E <= 1024 experts). LDS holds a bit per (expert, token row): the
 // rank of a placement inside its expert is the number of set bits below its row, so placements
 // land in ascending row order without sorting (the reference's BTreeMap<expert, [(position,
@@ -504,6 +468,9 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
 {
     const uint32_t words = (rows + 31) >> 5;
     const size_t lds = (size_t)(E * words + E) * sizeof(uint32_t);
+    if (lds > 65536)  // long prefill batches: up to 160 KB of LDS per workgroup on gfx950
+        (void)hipFuncSetAttribute((const void *)moe_schedule_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
     const int t = timer_begin(K_MOE_SCHEDULE, stream);
     hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
                        E, max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active,

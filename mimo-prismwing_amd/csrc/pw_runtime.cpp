@@ -98,7 +98,7 @@ struct pw_runtime {
     // routed-MoE per-layer scratch
     DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
         moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
-        moe_active, moe_partial;
+        moe_active, moe_partial, pf_tiles;
     MoeBuffers mb{};
     pw::KernelTimer timer;
 };
@@ -247,7 +247,9 @@ int read_flags(pw_runtime *rt, uint32_t &flags)
             return s_;               \
     } while (0)
 
-int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I)
+// Routed-MoE scratch for `rows` token rows. mode_a_split: also the mode A buffers (activation
+// and hidden bf16 planes, split-K partial sums), which the decode paths (rows <= 128) use.
+int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, bool mode_a_split = true)
 {
     const size_t P = (size_t)rows * 8;
     PW_HIP(rt->moe_plan.ensure(sizeof(pw::MoePlan)));
@@ -257,8 +259,10 @@ int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I
     PW_HIP(rt->moe_w.ensure(P * 4));
     PW_HIP(rt->moe_slots.ensure(P * 4));
     PW_HIP(rt->moe_hidden.ensure(P * I * 4));
-    PW_HIP(rt->moe_hidden_planes.ensure(3 * P * I * 2));
-    PW_HIP(rt->moe_x_planes.ensure(3 * (size_t)rows * H * 2));
+    if (mode_a_split) {
+        PW_HIP(rt->moe_hidden_planes.ensure(3 * P * I * 2));
+        PW_HIP(rt->moe_x_planes.ensure(3 * (size_t)rows * H * 2));
+    }
     PW_HIP(rt->moe_y.ensure(P * H * 4));
     PW_HIP(rt->moe_xq.ensure((size_t)rows * H));
     PW_HIP(rt->moe_xs.ensure((size_t)rows * (H / 128) * 4));
@@ -269,7 +273,8 @@ int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I
     const size_t ks_gu = std::max(pw::plan_split(H, 2, 1, cnt).ks, pw::plan_split(H, 2, 3, cnt).ks);
     const size_t ks_d = pw::plan_split(I, 1, 3, cnt).ks;
     PW_HIP(rt->moe_active.ensure((size_t)(E + 1) * sizeof(pw::ActiveExpert)));
-    PW_HIP(rt->moe_partial.ensure(std::max(ks_gu * 2 * P * I, ks_d * P * H) * 4));
+    if (mode_a_split)
+        PW_HIP(rt->moe_partial.ensure(std::max(ks_gu * 2 * P * I, ks_d * P * H) * 4));
     MoeBuffers &mb = rt->mb;
     mb.active = (pw::ActiveExpert *)rt->moe_active.p;
     mb.partial = (float *)rt->moe_partial.p;
@@ -1080,6 +1085,45 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
                          bank->intermediate, out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
                          out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
                          out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void *x, uint32_t x_dtype,
+                          uint32_t rows, const uint32_t *route_ids, const float *route_weights, void *output,
+                          uint32_t out_dtype, void *stream)
+{
+    if (!rt || !bank || !x || !route_ids || !route_weights || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
+        return fail(PW_ERR_ARGUMENT, "unknown dtype");
+    if (rows < 1 || rows > 4096)
+        return fail(PW_ERR_ARGUMENT, "prefill row count must be between one and 4096");
+    const uint32_t E = bank->n_experts, H = bank->hidden, I = bank->intermediate;
+    // the device schedule keeps one bit per (expert, row) in LDS (160 KB per workgroup)
+    const size_t sched_lds = ((size_t)E * ((rows + 31) / 32) + E) * 4;
+    if (sched_lds > 160 * 1024)
+        return fail(PW_ERR_ARGUMENT, "%u experts x %u rows exceed the schedule's LDS bitmap", E, rows);
+    if (H % 128 || I % 128)
+        return fail(PW_ERR_LAYOUT, "prefill needs hidden and intermediate sizes in multiples of 128");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    PW_TRY(ensure_moe(rt, rows, E, H, I, false));
+    const uint32_t max_tiles = pw::prefill_max_tiles(rows, E);
+    PW_HIP(rt->pf_tiles.ensure((size_t)max_tiles * 8 + 16));
+    pw::PrefillBuffers pb{};
+    pb.tiles = (uint2 *)rt->pf_tiles.p;
+    pb.n_tiles = (uint32_t *)((char *)rt->pf_tiles.p + (size_t)max_tiles * 8);
+    pb.hidden = (uint16_t *)rt->moe_hidden.p;  // [P][I] f32 scratch holds the bf16 hidden
+    pb.y = (uint16_t *)rt->moe_y.p;            // [P][H] f32 scratch holds the bf16 outputs
+    const uint32_t P = rows * 8;
+    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, std::min<uint32_t>(E, P), rt->mb,
+                            rt->d_flags, s);
+    pw::launch_moe_prefill(bank->table, rt->mb, pb, x, x_dtype == PW_DTYPE_F32, rows, E, H, I,
+                           out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
+                           out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
+                           out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s);
     PW_HIP(hipGetLastError());
     return PW_OK;
 }

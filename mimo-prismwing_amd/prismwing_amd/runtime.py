@@ -262,6 +262,12 @@ class WideMoeRuntime:
                                         _ptr(route_ids), _ptr(route_weights), _ptr(out), out_dtype,
                                         stream or 0))
 
+    def moe_prefill_device(self, bank: ExpertBank, x, rows: int, route_ids, route_weights, out,
+                           x_dtype: int = DTYPE_BF16, out_dtype: int = DTYPE_BF16, stream: Optional[int] = None):
+        """Mode B routed-MoE layer over up to 4096 token rows (grouped FP8 GEMM), device buffers."""
+        check(lib().pw_moe_prefill_device(self.handle, bank.handle, _ptr(x), x_dtype, rows, _ptr(route_ids),
+                                          _ptr(route_weights), _ptr(out), out_dtype, stream or 0))
+
     def expert_forward_device(self, bank: ExpertBank, expert: int, x, rows: int, out, mode: int = MODE_A,
                               x_dtype: int = DTYPE_BF16, out_dtype: int = DTYPE_BF16,
                               stream: Optional[int] = None):

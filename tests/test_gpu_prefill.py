@@ -1,0 +1,151 @@
+"""GPU parity of the routed-MoE prefill (mode B grouped block-FP8 GEMM) through the C ABI.
+
+The reference runs its layer-major prefill as 128-row slices through the wide MoE runtime
+(src/text_endpoint.rs:4951-5287); every placement depends only on its own token row, so the
+prefill over all rows must agree with the C oracle's mode B layer on the same rows and with the
+decode-path layer run on 32-row chunks. Tolerance: mode B <= 2e-2 max|d|/max|ref| (the
+reference's own mode B gate, src/wide_metal_moe.rs:394-421 uses 0.01 on its probe inputs).
+Schedules and tile tables are integer work: the flags word stays zero.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import prismwing_amd as P
+from prismwing_amd import workloads as WL
+from helpers import normwise, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+MODE_B_TOL = 2e-2
+
+
+def _dev(torch, a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return (t if dtype is None else t.to(dtype)).cuda()
+
+
+def _bf16_dev(torch, x):
+    return torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda()
+
+
+def _from_bf16(t):
+    return (t.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _prefill(rt, torch, bank, x, sel, w, out_dtype=P.DTYPE_BF16, x_f32=False):
+    rows = x.shape[0]
+    xt = _dev(torch, x.astype(np.float32)) if x_f32 else _bf16_dev(torch, x)
+    ids = _dev(torch, sel.astype(np.int32))
+    wts = _dev(torch, w.astype(np.float32))
+    out = torch.empty((rows, bank.bank.hidden), dtype=torch.int16 if out_dtype == P.DTYPE_BF16 else torch.float32,
+                      device="cuda")
+    rt.moe_prefill_device(bank.bank, xt, rows, ids, wts, out, x_dtype=P.DTYPE_F32 if x_f32 else P.DTYPE_BF16,
+                          out_dtype=out_dtype, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    return _from_bf16(out) if out_dtype == P.DTYPE_BF16 else out.cpu().numpy()
+
+
+def _routes(rng, rows, n_experts):
+    logits = rng.standard_normal((rows, n_experts)).astype(np.float32)
+    bias = rng.uniform(-0.01, 0.01, n_experts).astype(np.float32)
+    sel, w, _ = P.route_from_logits(logits, bias)[1:]
+    return sel, w
+
+
+class _SmallBank:
+    def __init__(self, rt, n, hidden, inter, seed):
+        self.dev = WL.synth_bank(rt, n_experts=n, hidden=hidden, inter=inter, seed=seed)
+        self.bank = self.dev.bank
+        self.hidden = hidden
+        self.experts = {e: self.dev.expert_host(e) for e in range(n)}
+        self.n = n
+
+
+@pytest.fixture(scope="module")
+def small_bank(rt):
+    return _SmallBank(rt, 16, 256, 128, WL.SEED_BASE + 40)
+
+
+@pytest.mark.parametrize("rows", [1, 7, 64, 200])
+def test_prefill_matches_oracle(rt, small_bank, rows):
+    """Random top-8 of 16 experts: 8 * rows / 16 placements per expert, several 64-slot m-tiles."""
+    import torch
+    rng = np.random.default_rng(100 + rows)
+    x = WL.activations(rows, WL.SEED_BASE + 50 + rows, hidden=256)
+    sel, w = _routes(rng, rows, small_bank.n)
+    got = _prefill(rt, torch, small_bank, x, sel, w)
+    ref = O.moe_layer("b", x, small_bank.experts, small_bank.n, sel, w)
+    assert normwise(got, ref) <= MODE_B_TOL
+    assert rel_l2(got, ref) <= 5e-3
+
+
+def test_prefill_skewed_routes_f32_input(rt, small_bank):
+    """Every token on the same eight experts (count = rows = 300: five m-tiles each), f32 input."""
+    import torch
+    rows = 300
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((rows, 256)).astype(np.float32)
+    sel = np.tile(np.array([3, 1, 4, 15, 9, 2, 6, 5], np.uint32), (rows, 1))
+    w = rng.uniform(0.01, 0.3, (rows, 8)).astype(np.float32)
+    got = _prefill(rt, torch, small_bank, x, sel, w, out_dtype=P.DTYPE_F32, x_f32=True)
+    ref = O.moe_layer("b", x, small_bank.experts, small_bank.n, sel, w)
+    assert normwise(got, ref) <= MODE_B_TOL
+    assert rel_l2(got, ref) <= 5e-3
+
+
+@pytest.fixture(scope="module")
+def full_bank(rt):
+    return WL.synth_bank(rt, n_experts=256, seed=WL.SEED_BASE + 2)
+
+
+def _decode_chunks(rt, torch, bank, x, sel, w, chunk=32):
+    rows = x.shape[0]
+    out = torch.empty((rows, 4096), dtype=torch.int16, device="cuda")
+    xt = _bf16_dev(torch, x)
+    ids = _dev(torch, sel.astype(np.int32))
+    wts = _dev(torch, w.astype(np.float32))
+    stream = torch.cuda.current_stream().cuda_stream
+    for r0 in range(0, rows, chunk):
+        n = min(chunk, rows - r0)
+        rt.moe_layer_device(bank.bank, xt[r0:], n, ids[r0:], wts[r0:], out[r0:], mode=P.MODE_B,
+                            out_dtype=P.DTYPE_BF16, stream=stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    return _from_bf16(out)
+
+
+@pytest.mark.parametrize("zipf", [False, True])
+def test_prefill_2048_tokens_matches_decode_chunks(rt, full_bank, zipf):
+    """2048 tokens, top-8 of 256 experts (16 384 placements): the prefill equals the decode layer
+    run on 32-row chunks (the same mode B numerics per placement) and, on sampled rows, the oracle."""
+    import torch
+    rows = 2048
+    x = WL.activations(rows, WL.SEED_BASE + 4)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
+    sel, w, _ = WL.route_host(x, rw, bias)
+    counts = np.bincount(sel.reshape(-1), minlength=256)
+    assert counts.sum() == rows * 8
+    got = _prefill(rt, torch, full_bank, x, sel, w)
+    dec = _decode_chunks(rt, torch, full_bank, x, sel, w)
+    assert normwise(got, dec) <= MODE_B_TOL
+    assert rel_l2(got, dec) <= 2e-3
+    # oracle on three sampled rows (only their experts are fetched)
+    pick = np.array([0, 1111, 2047])
+    used = sorted(set(sel[pick].reshape(-1).tolist()))
+    experts = {e: full_bank.expert_host(e) for e in used}
+    ref = O.moe_layer("b", x[pick], experts, 256, sel[pick], w[pick])
+    assert normwise(got[pick], ref) <= MODE_B_TOL
+
+
+def test_prefill_rejects_bad_arguments(rt, small_bank):
+    import torch
+    x = torch.zeros((8, 256), dtype=torch.int16, device="cuda")
+    ids = torch.zeros((8, 8), dtype=torch.int32, device="cuda")
+    w = torch.zeros((8, 8), dtype=torch.float32, device="cuda")
+    out = torch.zeros((8, 256), dtype=torch.int16, device="cuda")
+    with pytest.raises(P.PwError, match="ARGUMENT"):
+        rt.moe_prefill_device(small_bank.bank, x, 0, ids, w, out)
+    with pytest.raises(P.PwError, match="ARGUMENT"):
+        rt.moe_prefill_device(small_bank.bank, x, 4097, ids, w, out)
