@@ -210,7 +210,7 @@ int pw_expert_bank_shape(const pw_expert_bank *bank, uint32_t *n_experts, uint32
 
 /* One routed-MoE layer with inputs already in device memory: x [rows x hidden] (x_dtype),
  * route_ids / route_weights [rows x 8] (the reference's RoutingTrace selected/weights,
- * src/text_endpoint.rs:4342-4380), output [rows x hidden] (out_dtype, bf16-rounded). The
+ * src/text_endpoint.rs:4342-4380; 16-byte aligned), output [rows x hidden] (out_dtype, bf16-rounded). The
  * schedule is built on the device in the reference's BTreeMap order. rows <= 32.
  * Asynchronous on stream; kernel error bits accumulate in the runtime's error word. */
 int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
@@ -222,7 +222,7 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
  * slices through WideMetalMoeRuntime::execute (run_layer_major_moe_slice_mode,
  * src/text_endpoint.rs:4951-5287; src/wide_metal_moe.rs:852-1314), here one grouped block-FP8
  * GEMM per projection on the FP8 MFMA (any number of placements per expert). x [rows x hidden]
- * (x_dtype), route_ids / route_weights [rows x 8], output [rows x hidden] (out_dtype,
+ * (x_dtype), route_ids / route_weights [rows x 8] (16-byte aligned), output [rows x hidden] (out_dtype,
  * bf16-rounded). Asynchronous on stream; kernel error bits accumulate in the runtime's word. */
 int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void *x, uint32_t x_dtype,
                           uint32_t rows, const uint32_t *route_ids, const float *route_weights, void *output,

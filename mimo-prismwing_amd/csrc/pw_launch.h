@@ -137,9 +137,9 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
 
 // Routed-MoE prefill (mode B grouped block-FP8 GEMM, pw_prefill.hip) after launch_moe_schedule.
 struct PrefillBuffers {
-    uint2 *tiles;       // [prefill_max_tiles] (schedule entry, first slot of a 64-slot m-tile)
+    uint2 *tiles;       // [prefill_max_tiles] (schedule entry, first slot of a 96-slot m-tile)
     uint32_t *n_tiles;  // [1]
-    uint16_t *hidden;   // [rows * 8][I] bf16 SwiGLU output
+    uint16_t *hidden;   // [rows * 8][2I] bf16 gate and up outputs
     uint16_t *y;        // [rows * 8][H] bf16 expert outputs
 };
 uint32_t prefill_max_tiles(uint32_t rows, uint32_t E);

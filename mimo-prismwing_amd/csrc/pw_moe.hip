@@ -24,18 +24,21 @@ namespace pw {
 // One workgroup (1024 threads, E <= 1024 experts). LDS holds a bit per (expert, token row): the
 // rank of a placement inside its expert is the number of set bits below its row, so placements
 // land in ascending row order without sorting (the reference's BTreeMap<expert, [(position,
-// weight)]>, src/text_endpoint.rs:4767-4775). Counts and offsets come from block-wide scans.
+// weight)]>, src/text_endpoint.rs:4767-4775). Counts and offsets come from block-wide scans; a
+// per-(expert, 32-row word) prefix of the counts (when it fits in LDS) makes each rank O(1).
+// Token rows are handled one per thread: their eight ids and weights are read once.
 __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids,
-    const float *__restrict__ weights, uint32_t rows, uint32_t E, uint32_t max_active,
+    const float *__restrict__ weights, uint32_t rows, uint32_t E, uint32_t max_active, uint32_t with_prefix,
     MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
     ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
     uint32_t *__restrict__ row_slots, uint32_t *flags)
 {
     extern __shared__ uint32_t lds[];
     const uint32_t words = (rows + 31) >> 5;
-    uint32_t *mask = lds;                  // [E][words]
-    uint32_t *offset = mask + E * words;   // [E]
+    uint32_t *mask = lds;                              // [E][words]
+    uint32_t *offset = mask + E * words;               // [E]
+    uint16_t *pref = (uint16_t *)(offset + E);         // [E][words] set bits in earlier words
     __shared__ uint32_t s_bad, s_max, s_scan[48];
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t P = rows * 8;
@@ -46,25 +49,35 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     for (uint32_t i = tid; i < E * words; i += nthr)
         mask[i] = 0;
     __syncthreads();
-    for (uint32_t i = tid; i < P; i += nthr) {
-        const uint32_t e = ids[i];
-        const float w = weights[i];
-        if (e >= E || !finite_f32(w)) {
-            atomicOr(&s_bad, 1u);
-            continue;
+    for (uint32_t p = tid; p < rows; p += nthr) {
+        const uint4 i0 = *(const uint4 *)(ids + (size_t)p * 8), i1 = *(const uint4 *)(ids + (size_t)p * 8 + 4);
+        const float4 w0 = *(const float4 *)(weights + (size_t)p * 8), w1 = *(const float4 *)(weights + (size_t)p * 8 + 4);
+        const uint32_t e8[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+        const float wt8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        bool bad = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t e = e8[j];
+            if (e >= E || !finite_f32(wt8[j])) {
+                bad = true;
+                continue;
+            }
+            const uint32_t old = atomicOr(&mask[e * words + (p >> 5)], 1u << (p & 31));
+            bad |= (old & (1u << (p & 31))) != 0;  // the same expert twice in one token's routes
         }
-        const uint32_t p = i >> 3;
-        const uint32_t old = atomicOr(&mask[e * words + (p >> 5)], 1u << (p & 31));
-        if (old & (1u << (p & 31)))
-            atomicOr(&s_bad, 1u);  // the same expert twice in one token's routes
+        if (bad)
+            atomicOr(&s_bad, 1u);
     }
     __syncthreads();
     // thread e: expert e's count, its slot offset and its index among the routed experts
     const uint32_t e = tid;
     uint32_t c = 0;
     if (e < E)
-        for (uint32_t w = 0; w < words; ++w)
+        for (uint32_t w = 0; w < words; ++w) {
+            if (with_prefix)
+                pref[e * words + w] = (uint16_t)c;
             c += __popc(mask[e * words + w]);
+        }
     uint32_t total, n_active;
     const uint32_t off = block_exclusive_scan(c, s_scan, &total);
     const uint32_t act = block_exclusive_scan(c ? 1u : 0u, s_scan, &n_active);
@@ -96,33 +109,43 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     for (uint32_t a = n_active + tid; a < max_active; a += nthr)
         active[a] = ActiveExpert{};
     // every consumer index starts valid even when the route buffers are rejected
-    for (uint32_t i = tid; i < P; i += nthr) {
-        placement_pos[i] = 0;
-        placement_w[i] = 0.f;
-        row_slots[i] = 0;
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < P; i += nthr) {
-        const uint32_t ei = ids[i];
-        if (ei >= E || !finite_f32(weights[i]))
-            continue;
-        const uint32_t p = i >> 3;
-        uint32_t rank = 0;
-        for (uint32_t w = 0; w < (p >> 5); ++w)
-            rank += __popc(mask[ei * words + w]);
-        rank += __popc(mask[ei * words + (p >> 5)] & ((1u << (p & 31)) - 1u));
-        const uint32_t slot = offset[ei] + rank;
-        if (slot >= P)
-            continue;  // only when the routes were rejected above
-        placement_pos[slot] = p;
-        placement_w[slot] = weights[i];
-        // position of this placement among its token's eight, ordered by expert id
-        uint32_t before = 0;
-        for (uint32_t j = 0; j < 8; ++j) {
-            const uint32_t other = ids[p * 8 + j];
-            before += other < ei ? 1u : 0u;
+    if (s_bad || total != P)
+        for (uint32_t i = tid; i < P; i += nthr) {
+            placement_pos[i] = 0;
+            placement_w[i] = 0.f;
+            row_slots[i] = 0;
         }
-        row_slots[p * 8 + (before & 7)] = slot;
+    __syncthreads();
+    for (uint32_t p = tid; p < rows; p += nthr) {
+        const uint4 i0 = *(const uint4 *)(ids + (size_t)p * 8), i1 = *(const uint4 *)(ids + (size_t)p * 8 + 4);
+        const float4 w0 = *(const float4 *)(weights + (size_t)p * 8), w1 = *(const float4 *)(weights + (size_t)p * 8 + 4);
+        const uint32_t e8[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+        const float wt8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const uint32_t wd = p >> 5, below = (1u << (p & 31)) - 1u;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t ei = e8[j];
+            if (ei >= E || !finite_f32(wt8[j]))
+                continue;
+            uint32_t rank = __popc(mask[ei * words + wd] & below);
+            if (with_prefix) {
+                rank += pref[ei * words + wd];
+            } else {
+                for (uint32_t w = 0; w < wd; ++w)
+                    rank += __popc(mask[ei * words + w]);
+            }
+            const uint32_t slot = offset[ei] + rank;
+            if (slot >= P)
+                continue;  // only when the routes were rejected above
+            placement_pos[slot] = p;
+            placement_w[slot] = wt8[j];
+            // position of this placement among its token's eight, ordered by expert id
+            uint32_t before = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                before += e8[k] < ei ? 1u : 0u;
+            row_slots[(size_t)p * 8 + (before & 7)] = slot;
+        }
     }
     if (tid == 0) {
         plan->n_active = n_active;
@@ -132,7 +155,6 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
             raise_flag(flags, FLAG_SCHEDULE);
     }
 }
-
 
 // --------------------------------------------------------------- shared tile preamble
 struct ExpertTile {
@@ -467,13 +489,17 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
                          uint32_t *flags, hipStream_t stream)
 {
     const uint32_t words = (rows + 31) >> 5;
-    const size_t lds = (size_t)(E * words + E) * sizeof(uint32_t);
+    size_t lds = (size_t)(E * words + E) * sizeof(uint32_t);
+    const size_t with_prefix_lds = lds + (size_t)E * words * sizeof(uint16_t);
+    const uint32_t with_prefix = words > 1 && with_prefix_lds <= 160 * 1024;
+    if (with_prefix)
+        lds = with_prefix_lds;
     if (lds > 65536)  // long prefill batches: up to 160 KB of LDS per workgroup on gfx950
         (void)hipFuncSetAttribute((const void *)moe_schedule_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds);
     const int t = timer_begin(K_MOE_SCHEDULE, stream);
     hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
-                       E, max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active,
+                       E, max_active, with_prefix, mb.plan, mb.active_expert, mb.active_offset, mb.active,
                        mb.placement_pos, mb.placement_w, mb.row_slots, flags);
     timer_end(t, stream);
 }

@@ -13,25 +13,32 @@
 // scales are applied in f32, sequentially over b (the same per-block arithmetic as the decode
 // mode B kernels).
 //
-// Tiles: (64 placement slots of one routed expert = an m-tile) x (64 weight rows = an n-tile). A
-// workgroup of four waves (16 weight rows each) walks K in 128-column steps, double-buffered: the
-// next step's weight bytes (one weight row per lane) and activation codes load into registers
-// while the current step runs on the MFMA; the codes then go to the other LDS buffer (16-byte
-// units XOR-swizzled by token so the B-operand reads spread over the LDS banks), and a barrier
-// that orders LDS only lets the weight prefetch stay in flight. The m-tile's activation scales
-// are staged once, transposed ([block][token]).
-// Epilogues: gate/up -> bf16-staged SwiGLU (bf16_staged_swiglu, kernels/block_fp8_gemv.metal:
-// 139-160) -> hidden as bf16; down -> bf16 expert output (bf16_round_in_place,
-// src/wide_metal_moe.rs:1236-1251). Then the combine sums each token's eight outputs.
+// Tiles: (96 placement slots of one routed expert = an m-tile) x (64 weight rows = an n-tile);
+// 96 slots hold a whole expert's placements at the uniform-routing count (64 on average), so its
+// weights stream once. Gate and up run as one stacked projection (2I output columns per slot),
+// then a SwiGLU + re-quantisation kernel, then down. A workgroup of four waves (16 weight rows
+// each) walks K in 128-column steps. Weight bytes (one row per lane) load straight into a
+// four-slot register ring, four steps ahead of the MFMA; activation codes (cache hits, shared by
+// the expert's n-tiles) load one step ahead into registers and then go to a double-buffered LDS
+// tile (16-byte units XOR-swizzled by token so the B-operand reads spread over the LDS banks).
+// The barriers order LDS only, so the weight stream stays in flight across them. The m-tile's
+// activation scales (transposed, [block][token]) and the tile's weight block scales are staged in
+// LDS once.
+// Epilogues: every projection rounds to bf16 (bf16_round_in_place, src/wide_metal_moe.rs:
+// 1236-1251); bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160) runs on the bf16 gate and
+// up outputs. The combine then sums each token's eight outputs.
 #include "pw_device.h"
 #include "pw_launch.h"
 
 namespace pw {
 
-constexpr uint32_t PF_MT = 64;      // placement slots per m-tile
-constexpr uint32_t PF_UNITS = 8;    // 16-byte units per 128-byte token row of a step
+constexpr uint32_t PF_MT = 96;                    // placement slots per m-tile
+constexpr int PF_TT = (int)PF_MT / 16;            // 16-token MFMA tiles per m-tile
+constexpr uint32_t PF_UNITS = 8;                  // 16-byte units per 128-byte token row of a step
+constexpr int PF_CPW = (int)PF_MT / 8 / 4;        // 8-token code chunks per wave per step
+constexpr int PF_WS = 4;                          // weight register slots: loads run 4 steps ahead
 
-// Tile table: ceil(count / 64) m-tiles per routed expert, ascending expert order. One workgroup of
+// Tile table: ceil(count / 96) m-tiles per routed expert, ascending expert order. One workgroup of
 // 1024 threads, one thread per schedule entry (banks hold at most 1024 experts).
 __global__ __launch_bounds__(1024) void prefill_tiles_kernel(const MoePlan *__restrict__ plan,
                                                              const ActiveExpert *__restrict__ active,
@@ -60,48 +67,54 @@ struct PrefillArgs {
     const ActiveExpert *active;
     const uint2 *tiles;             // [max_tiles] (schedule entry, first slot of the m-tile)
     const uint32_t *n_tiles;
-    const uint32_t *placement_pos;  // gate/up: token row of each placement slot
+    const uint32_t *placement_pos;  // gate/up: token row of each placement slot (down: null)
     const uint8_t *codes;           // activation codes [rows][K] (down: rows = placement slots)
     const float *scales;            // activation scales [rows][K / 128]
-    uint32_t K, R, rows, max_tiles;
-    uint16_t *out;                  // [P][R] bf16: hidden (gate/up) or expert output (down)
+    uint32_t K;                     // columns
+    uint32_t R;                     // output columns per slot: 2I (gate then up) or H
+    uint32_t R1;                    // rows of the first matrix (gate/up: I; down: H)
+    uint32_t rows, max_tiles;
+    uint16_t *out;                  // [P][R] bf16
     uint32_t *flags;
 };
 
-template <int MATS>
-struct PfWeights {
-    uint4 v[MATS][2];
+// One K step's weight bytes of this lane: its row, columns [16q, 16q + 16) and [64 + 16q, 80 + 16q)
+// of the 128-column block (q = lane / 16), so each load instruction reads 64 contiguous bytes of
+// each of 16 rows. The MFMA's K order within the block is permuted alike for the codes, so the
+// block dot product covers the same 128 products.
+struct PfW {
+    uint4 v[2];
 };
 
-template <int MATS>
-__device__ __forceinline__ void pf_load_weights(PfWeights<MATS> &w, const uint8_t *const *wrow, uint32_t k0)
+// This lane's share of one step's activation codes: PF_CPW chunks of 8 tokens x 128 bytes per
+// wave; lane i holds global unit (i % 8) ^ (token % 8) of token 8c + i / 8 and stores it as LDS
+// unit i % 8 of that token (unit index 64c + i: conflict-free writes).
+struct PfC {
+    uint4 v[PF_CPW];
+};
+
+__device__ __forceinline__ void pf_issue_w(PfW &w, const uint8_t *wrow, uint32_t k0)
 {
-#pragma unroll
-    for (int m = 0; m < MATS; ++m) {
-        w.v[m][0] = load_stream16(wrow[m] + k0);
-        w.v[m][1] = load_stream16(wrow[m] + k0 + 16);
-    }
+    w.v[0] = load_stream16(wrow + k0);
+    w.v[1] = load_stream16(wrow + k0 + 64);
 }
 
-// Activation codes of one step, two 16-byte loads per lane: tokens [8c, 8c + 8) of the m-tile
-// for c = 2 * wave + u; lane i holds global unit (i % 8) ^ (token % 8) of token 8c + i / 8 and
-// stores it as LDS unit i % 8 of that token (unit index 64c + i: conflict-free writes).
-__device__ __forceinline__ void pf_load_codes(uint4 (&c)[2], const uint8_t *const *src, uint32_t k0)
+__device__ __forceinline__ void pf_issue_c(PfC &c, const uint8_t *const *csrc, uint32_t k0)
 {
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-        c[u] = load_global16(src[u] + k0);
+    for (int u = 0; u < PF_CPW; ++u)
+        c.v[u] = load_global16(csrc[u] + k0);
 }
 
-__device__ __forceinline__ void pf_store_codes(uint4 *buf, const uint4 (&c)[2], int wave, int lane)
+__device__ __forceinline__ void pf_store_codes(uint4 *buf, const PfC &c, int wave, int lane)
 {
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-        buf[(2 * wave + u) * 64 + lane] = c[u];
+    for (int u = 0; u < PF_CPW; ++u)
+        buf[(PF_CPW * wave + u) * 64 + lane] = c.v[u];
 }
 
-// Workgroup barrier ordering LDS accesses only: outstanding global loads (the next step's
-// prefetch) stay in flight across it, which __syncthreads() would wait for.
+// Workgroup barrier ordering LDS accesses only: outstanding global loads (the prefetched steps)
+// stay in flight across it, which __syncthreads() would wait for.
 __device__ __forceinline__ void lds_barrier()
 {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -109,47 +122,42 @@ __device__ __forceinline__ void lds_barrier()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int MATS>
-__device__ __forceinline__ void pf_compute(f32x4 (&tot)[MATS][4], const PfWeights<MATS> &w, const uint4 *buf,
-                                           const float *lds_scale, const float *lds_wscale, uint32_t blocks,
-                                           uint32_t b, int q, int r16)
+__device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], const PfW &w, const uint4 *buf,
+                                           const float *lds_scale, float sw, uint32_t b, int q, int r16)
 {
-    float sw[MATS];
+    const i32x8 A = {(int)w.v[0].x, (int)w.v[0].y, (int)w.v[0].z, (int)w.v[0].w,
+                     (int)w.v[1].x, (int)w.v[1].y, (int)w.v[1].z, (int)w.v[1].w};
 #pragma unroll
-    for (int m = 0; m < MATS; ++m)
-        sw[m] = lds_wscale[m * blocks + b];
-    i32x8 A[MATS];
-#pragma unroll
-    for (int m = 0; m < MATS; ++m)
-        A[m] = i32x8{(int)w.v[m][0].x, (int)w.v[m][0].y, (int)w.v[m][0].z, (int)w.v[m][0].w,
-                     (int)w.v[m][1].x, (int)w.v[m][1].y, (int)w.v[m][1].z, (int)w.v[m][1].w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < PF_TT; ++j) {
         const uint32_t t = 16 * j + r16;
         const float sa = lds_scale[b * PF_MT + t];
-        const uint4 c0 = buf[t * PF_UNITS + ((2 * q) ^ (t & 7))];
-        const uint4 c1 = buf[t * PF_UNITS + ((2 * q + 1) ^ (t & 7))];
+        const uint4 c0 = buf[t * PF_UNITS + ((q) ^ (t & 7))];
+        const uint4 c1 = buf[t * PF_UNITS + ((q + 4) ^ (t & 7))];
         const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w, (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
+        const f32x4 p = mfma_fp8_16x16x128(A, xb, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int m = 0; m < MATS; ++m) {
-            const f32x4 p = mfma_fp8_16x16x128(A[m], xb, f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                tot[m][j][i] = __builtin_fmaf(p[i] * sw[m], sa, tot[m][j][i]);
-        }
+        for (int i = 0; i < 4; ++i)
+            tot[j][i] = __builtin_fmaf(p[i] * sw, sa, tot[j][i]);
     }
 }
 
-template <int MATS>
-__global__ __launch_bounds__(256) void prefill_b_kernel(const PrefillArgs args)
+// One projection tile: 64 weight rows (of gate, up or down) x one m-tile of placement slots,
+// bf16-rounded outputs (bf16_round_in_place of every projection, src/wide_metal_moe.rs:1236-1251).
+// n-tiles [0, R1 / 64) use the first matrix (gate, or down), the rest the second (up).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_b_kernel(const PrefillArgs args)
 {
-    __shared__ uint4 lds_codes[2][PF_MT * PF_UNITS];  // two 8 KB steps, swizzled
-    extern __shared__ float lds_scale[];              // [K / 128][64] activation, then [MATS][K / 128] weight
-    constexpr int MAXB = 64;                          // K <= 8192
+    __shared__ uint4 lds_codes[2][PF_MT * PF_UNITS];  // two 12 KB steps, swizzled
+    extern __shared__ float lds_scale[];              // [K / 128][96] activation, then [K / 128] weight
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r16 = lane & 15;
-    const uint32_t mt = blockIdx.x % args.max_tiles, ntile = blockIdx.x / args.max_tiles;
+    // XCD-aware order: workgroups go round-robin to the 8 XCDs (blockIdx % 8), so XCD x takes
+    // m-tiles x, x + 8, ... and runs all n-tiles of one m-tile back to back: the m-tile's
+    // activation codes stay in that XCD's L2 while its n-tiles stream their weight rows, and the
+    // m-tiles (counted on the device) spread evenly over the XCDs.
+    const uint32_t n_ntiles = args.R >> 6;
+    const uint32_t local = blockIdx.x >> 3;
+    const uint32_t mt = (blockIdx.x & 7) + 8 * (local / n_ntiles), ntile = local % n_ntiles;
     if (mt >= args.n_tiles[0])
         return;
     const uint2 tl = args.tiles[mt];
@@ -159,142 +167,176 @@ __global__ __launch_bounds__(256) void prefill_b_kernel(const PrefillArgs args)
         return;
     const uint32_t cnt_t = ae.cnt - m0 < PF_MT ? ae.cnt - m0 : PF_MT;
     const uint32_t K = args.K, blocks = K >> 7;
-    const uint32_t row_base = ntile * 64 + wave * 16;
+    const uint32_t col0 = ntile * 64;                    // output column of the tile
+    const bool second = col0 >= args.R1;
+    const uint32_t row_base = (second ? col0 - args.R1 : col0) + wave * 16;  // row in its matrix
     const uint32_t slot0 = ae.off + m0;
+    const bool gather = args.placement_pos != nullptr;
+    const uint8_t *wmat = gather ? (second ? ae.ep.up_w : ae.ep.gate_w) : ae.ep.down_w;
+    const float *smat = gather ? (second ? ae.ep.up_s : ae.ep.gate_s) : ae.ep.down_s;
+    const uint8_t *wrow = wmat + (size_t)(row_base + r16) * K + q * 16;
+    smat += (row_base >> 7) * blocks;
 
-    const uint8_t *wbase[MATS];
-    const float *sbase[MATS];
-    if constexpr (MATS == 2) {
-        wbase[0] = ae.ep.gate_w;
-        wbase[1] = ae.ep.up_w;
-        sbase[0] = ae.ep.gate_s;
-        sbase[1] = ae.ep.up_s;
-    } else {
-        wbase[0] = ae.ep.down_w;
-        sbase[0] = ae.ep.down_s;
-    }
-    const uint8_t *wrow[MATS];
+    // token rows of the m-tile's slots (lane: slots lane and 64 + lane, the second only below 96;
+    // slots past the tile's count repeat its last slot: in-bounds loads whose output columns are
+    // never stored)
+    uint32_t tok[2];
 #pragma unroll
-    for (int m = 0; m < MATS; ++m) {
-        wrow[m] = wbase[m] + (size_t)(row_base + r16) * K + q * 32;
-        sbase[m] += (row_base >> 7) * blocks;
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t t = 64 * h + (h ? lane & 31 : lane);
+        tok[h] = slot0 + (t < cnt_t ? t : cnt_t - 1);
+        if (gather)
+            tok[h] = load_g(args.placement_pos + tok[h]);
     }
-    // step 0's weights first: their addresses depend only on the schedule entry
-    PfWeights<MATS> w0, w1;
-    pf_load_weights<MATS>(w0, wrow, 0);
-
-    // activation row of each slot of the m-tile (lane t: slot t). Slots past the tile's count
-    // repeat its last slot: in-bounds loads whose output columns are never stored.
-    uint32_t tok = slot0 + ((uint32_t)lane < cnt_t ? (uint32_t)lane : cnt_t - 1);
-    if constexpr (MATS == 2)
-        tok = load_g(args.placement_pos + tok);
-    // weight block scales of the workgroup's 64 rows (one 128-row scale block): [m][b]
-    float *lds_wscale = lds_scale + blocks * PF_MT;
-    const uint32_t m_of = (uint32_t)tid / blocks;
-    float wsc = 0.f;
-    if ((uint32_t)tid < MATS * blocks)
-        wsc = load_g(sbase[m_of < MATS ? m_of : 0] + (tid - m_of * blocks));
-    if constexpr (MATS == 2) {
-        if (tok >= args.rows) {
-            raise_flag(args.flags, FLAG_SCHEDULE);
-            tok = args.rows - 1;
+    float wsc = 0.f;  // weight block scales of the workgroup's 64 rows (one 128-row scale block)
+    if ((uint32_t)tid < blocks)
+        wsc = load_g(smat + tid);
+    const uint32_t last = blocks - 1;
+    if (gather) {
+        bool bad = false;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            bad |= tok[h] >= args.rows;
+            tok[h] = tok[h] < args.rows ? tok[h] : args.rows - 1;
         }
+        if (bad)
+            raise_flag(args.flags, FLAG_SCHEDULE);
     }
-    // activation scales of the m-tile, transposed: lds_scale[b * 64 + t] (lane = token); all
-    // loads issued before the first LDS write
-    float asc[MAXB / 4];
-#pragma unroll
-    for (int k = 0; k < MAXB / 4; ++k) {
-        const uint32_t b = wave + 4 * k;
-        asc[k] = b < blocks ? load_g(args.scales + (size_t)tok * blocks + b) : 0.f;
-    }
-    // per-lane sources of this wave's two code loads per step
-    const uint8_t *csrc[2];
+    // per-lane sources of this wave's code chunks: tokens 8c + lane / 8, c = PF_CPW * wave + u
+    const uint8_t *csrc[PF_CPW];
     const uint32_t g = ((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7;  // global unit of LDS unit lane % 8
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const uint32_t t = 8 * (2 * wave + u) + (lane >> 3);
-        const uint32_t row = __shfl(tok, (int)t, 64);
-        csrc[u] = args.codes + (size_t)row * K + g * 16;
+    for (int u = 0; u < PF_CPW; ++u) {
+        const uint32_t t = 8 * (PF_CPW * wave + u) + (lane >> 3);
+        const uint32_t r0 = __shfl(tok[0], (int)(t & 63), 64), r1 = __shfl(tok[1], (int)(t & 63), 64);
+        csrc[u] = args.codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
     }
-    uint4 cr[2];
-    pf_load_codes(cr, csrc, 0);
-    if ((uint32_t)tid < MATS * blocks)
+    // activation scales of the m-tile, transposed (lds_scale[b * 96 + t]), with 4-byte
+    // direct-to-LDS loads (lane = token; a second instruction covers tokens 64..95)
+    float *lds_wscale = lds_scale + blocks * PF_MT;
+    for (uint32_t b = wave; b < blocks; b += 4) {
+        __builtin_amdgcn_global_load_lds(
+            (const __attribute__((address_space(1))) void *)(args.scales + (size_t)tok[0] * blocks + b),
+            (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT), 4, 0, 0);
+        if (lane < 32)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(args.scales + (size_t)tok[1] * blocks + b),
+                (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT + 64), 4, 0, 0);
+    }
+    if ((uint32_t)tid < blocks)
         lds_wscale[tid] = wsc;
-#pragma unroll
-    for (int k = 0; k < MAXB / 4; ++k) {
-        const uint32_t b = wave + 4 * k;
-        if (b < blocks)
-            lds_scale[b * PF_MT + lane] = asc[k];
-    }
-
-    f32x4 tot[MATS][4];
-#pragma unroll
-    for (int m = 0; m < MATS; ++m)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            tot[m][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
+    // step 0's codes to LDS; the weight ring (steps 0..3, clamped to the last step) and step 1's
+    // codes in flight; every load is unconditional, so the compiler's wait counts stay exact
+    PfC cr;
+    pf_issue_c(cr, csrc, 0);
     pf_store_codes(lds_codes[0], cr, wave, lane);
-    lds_barrier();
-    // Step b computes from (w0 | w1, lds_codes[b & 1]) while step b + 1's weights and codes load;
-    // the codes go to the other LDS buffer after the compute, then one barrier. The steady-state
-    // loop has no branches, so the scheduling barrier keeps the store (and its wait for the
-    // prefetched codes) behind the compute; the last one or two steps are peeled.
-    uint32_t b = 0;
-    for (; b + 2 < blocks; b += 2) {
-        pf_load_codes(cr, csrc, (b + 1) << 7);
-        pf_load_weights<MATS>(w1, wrow, (b + 1) << 7);
-        pf_compute<MATS>(tot, w0, lds_codes[0], lds_scale, lds_wscale, blocks, b, q, r16);
-        __builtin_amdgcn_sched_barrier(0);
-        pf_store_codes(lds_codes[1], cr, wave, lane);
-        lds_barrier();
-        pf_load_codes(cr, csrc, (b + 2) << 7);
-        pf_load_weights<MATS>(w0, wrow, (b + 2) << 7);
-        pf_compute<MATS>(tot, w1, lds_codes[1], lds_scale, lds_wscale, blocks, b + 1, q, r16);
-        __builtin_amdgcn_sched_barrier(0);
-        pf_store_codes(lds_codes[0], cr, wave, lane);
-        lds_barrier();
-    }
-    if (b + 1 < blocks) {  // two steps left
-        pf_load_codes(cr, csrc, (b + 1) << 7);
-        pf_load_weights<MATS>(w1, wrow, (b + 1) << 7);
-        pf_compute<MATS>(tot, w0, lds_codes[0], lds_scale, lds_wscale, blocks, b, q, r16);
-        __builtin_amdgcn_sched_barrier(0);
-        pf_store_codes(lds_codes[1], cr, wave, lane);
-        lds_barrier();
-        pf_compute<MATS>(tot, w1, lds_codes[1], lds_scale, lds_wscale, blocks, b + 1, q, r16);
-    } else {  // one step left
-        pf_compute<MATS>(tot, w0, lds_codes[0], lds_scale, lds_wscale, blocks, b, q, r16);
-    }
-
-    // epilogue: lane holds rows row_base + 4q + i of tokens 16j + r16
-    bool bad = false;
-    const uint32_t R = args.R;
+    PfW w[PF_WS];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int i = 0; i < PF_WS; ++i)
+        pf_issue_w(w[i], wrow, ((uint32_t)i < last ? (uint32_t)i : last) << 7);
+    pf_issue_c(cr, csrc, (1 < last ? 1u : last) << 7);
+
+    f32x4 tot[PF_TT];
+#pragma unroll
+    for (int j = 0; j < PF_TT; ++j)
+        tot[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // The scale loads wrote LDS directly: wait for every load issued so far (the ring's first
+    // four steps arrive together with them). Entering the loop with nothing outstanding also lets
+    // the compiler keep its per-register memory-counter waits exact at the loop head.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // Sub-step k: compute step k from weight slot k % 4 and LDS buffer k & 1; store step k + 1's
+    // codes (loaded one sub-step ago) into the other buffer; load step k + 2's codes and step
+    // k + 4's weights into the freed registers; one barrier. Weights stream four steps ahead,
+    // codes (mostly cache hits, shared by the n-tiles of the expert) one step ahead.
+    // Whole groups of four steps run without early exits (so the compiler sees one loop state at
+    // the loop head); the last 0..3 steps are peeled. Load indices are clamped to the last step
+    // (the tail reloads it: cache hits), keeping every load unconditional.
+#define PF_SUBSTEP(W, K, BUF)                                                                 \
+    {                                                                                       \
+        const uint32_t k = (K);                                                             \
+        pf_compute(tot, W, lds_codes[BUF], lds_scale, lds_wscale[k], k, q, r16);            \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        pf_store_codes(lds_codes[(BUF) ^ 1], cr, wave, lane);                               \
+        pf_issue_c(cr, csrc, (k + 2 < last ? k + 2 : last) << 7);                           \
+        pf_issue_w(W, wrow, (k + PF_WS < last ? k + PF_WS : last) << 7);                    \
+        lds_barrier();                                                                      \
+    }
+    const uint32_t nfull = blocks & ~3u;
+    for (uint32_t b = 0; b < nfull; b += PF_WS) {
+        PF_SUBSTEP(w[0], b, 0)
+        PF_SUBSTEP(w[1], b + 1, 1)
+        PF_SUBSTEP(w[2], b + 2, 0)
+        PF_SUBSTEP(w[3], b + 3, 1)
+    }
+    if (nfull < blocks) {
+        PF_SUBSTEP(w[0], nfull, 0)
+        if (nfull + 1 < blocks) {
+            PF_SUBSTEP(w[1], nfull + 1, 1)
+            if (nfull + 2 < blocks)
+                PF_SUBSTEP(w[2], nfull + 2, 0)
+        }
+    }
+#undef PF_SUBSTEP
+
+    // epilogue: lane holds rows row_base + 4q + i of tokens 16j + r16 -> bf16
+    const uint32_t R = args.R;
+    const uint32_t ocol = col0 + wave * 16 + 4 * q;
+#pragma unroll
+    for (int j = 0; j < PF_TT; ++j) {
         const uint32_t t = 16 * j + r16;
         if (t >= cnt_t)
             continue;
         uint16_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if constexpr (MATS == 2) {
-                const float gv = round_bf16(tot[0][j][i]);
-                const float uv = round_bf16(tot[1][j][i]);
-                const float silu = round_bf16(gv / (1.0f + expf(-gv)));
-                const float h = round_bf16(silu * uv);
-                bad |= !finite_f32(gv) || !finite_f32(uv) || !finite_f32(h);
-                o[i] = (uint16_t)(f32_bits(h) >> 16);
-            } else {
-                o[i] = (uint16_t)(f32_bits(round_bf16(tot[0][j][i])) >> 16);
-            }
-        }
-        *(uint2 *)(args.out + (size_t)(slot0 + t) * R + row_base + 4 * q) =
+        for (int i = 0; i < 4; ++i)
+            o[i] = (uint16_t)(f32_bits(round_bf16(tot[j][i])) >> 16);
+        *(uint2 *)(args.out + (size_t)(slot0 + t) * R + ocol) =
             make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
     }
+}
+
+// bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343)
+// on the bf16 gate/up outputs, h = round(round(g / (1 + e^-g)) * u), fused with the dynamic
+// per-(slot, 128-column group) re-quantisation of h for the down projection
+// (dynamic_fp8_quantized_group128, kernels/block_fp8_gemv.metal:84-137). One wave per group,
+// two values per lane; gu [P][2I] bf16 (gate columns, then up).
+__global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_t *__restrict__ gu, uint32_t P,
+                                                                   uint32_t I, uint8_t *__restrict__ codes,
+                                                                   float *__restrict__ scales, uint32_t *flags)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t groups_per_row = I >> 7;
+    const uint32_t group = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (group >= P * groups_per_row)
+        return;
+    const uint32_t slot = group / groups_per_row, c = (group - slot * groups_per_row) * 128 + lane * 2;
+    const uint16_t *row = gu + (size_t)slot * 2 * I;
+    const uint32_t g2 = *(const uint32_t *)(row + c), u2 = *(const uint32_t *)(row + I + c);
+    float h[2];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float gv = f32_from(i ? (g2 & 0xffff0000u) : (g2 << 16));
+        const float uv = f32_from(i ? (u2 & 0xffff0000u) : (u2 << 16));
+        const float silu = round_bf16(gv / (1.0f + expf(-gv)));
+        h[i] = round_bf16(silu * uv);
+        bad |= !finite_f32(gv) || !finite_f32(uv) || !finite_f32(h[i]);
+    }
     if (bad)
-        raise_flag(args.flags, FLAG_SWIGLU_NONFINITE);
+        raise_flag(flags, FLAG_SWIGLU_NONFINITE);
+    const bool f0 = finite_f32(h[0]), f1 = finite_f32(h[1]);
+    float m = fmaxf(f0 ? fabsf(h[0]) : 0.f, f1 ? fabsf(h[1]) : 0.f);
+    m = wave_max(m);
+    const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
+    if (lane == 0)
+        scales[group] = scale;
+    float n0 = h[0] / scale, n1 = h[1] / scale;
+    n0 = n0 < -448.f ? -448.f : (n0 > 448.f ? 448.f : n0);
+    n1 = n1 < -448.f ? -448.f : (n1 > 448.f ? 448.f : n1);
+    *(uint16_t *)(codes + (size_t)slot * I + c) =
+        (uint16_t)encode_e4m3fn_rne(f0 ? n0 : 0.f) | ((uint16_t)encode_e4m3fn_rne(f1 ? n1 : 0.f) << 8);
 }
 
 // route_weighted_scatter_add_f32 + final bf16 round over bf16 expert outputs: each token sums
@@ -345,10 +387,18 @@ uint32_t prefill_max_tiles(uint32_t rows, uint32_t E)
     return max_active + (P + PF_MT - 1) / PF_MT;
 }
 
+static void launch_prefill_projection(const PrefillArgs &a, hipStream_t stream)
+{
+    const size_t lds = (size_t)(a.K / 128) * (PF_MT + 1) * 4;
+    const uint32_t grid = 8 * ((a.max_tiles + 7) / 8) * (a.R >> 6);
+    hipLaunchKernelGGL(prefill_b_kernel, dim3(grid), dim3(256), lds, stream, a);
+}
+
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,
                         uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream)
 {
+    (void)bank;
     const uint32_t P = rows * 8;
     const uint32_t max_active = E < P ? E : P;
     const uint32_t max_tiles = prefill_max_tiles(rows, E);
@@ -356,6 +406,7 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     hipLaunchKernelGGL(prefill_tiles_kernel, dim3(1), dim3(1024), 0, stream, mb.plan, mb.active, max_active,
                        pb.tiles, max_tiles, pb.n_tiles, flags);
 
+    // gate and up as one stacked projection of 2I output columns per slot
     PrefillArgs ga{};
     ga.active = mb.active;
     ga.tiles = pb.tiles;
@@ -364,17 +415,21 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     ga.codes = mb.xq;
     ga.scales = mb.xs;
     ga.K = H;
-    ga.R = I;
+    ga.R = 2 * I;
+    ga.R1 = I;
     ga.rows = rows;
     ga.max_tiles = max_tiles;
     ga.out = pb.hidden;
     ga.flags = flags;
     int t = timer_begin(K_PREFILL_GATEUP, stream);
-    hipLaunchKernelGGL(prefill_b_kernel<2>, dim3(max_tiles * (I / 64)), dim3(256),
-                       (size_t)(H / 128) * (PF_MT + 2) * 4, stream, ga);
+    launch_prefill_projection(ga, stream);
     timer_end(t, stream);
-    // re-quantise the bf16-staged hidden activations per (placement, 128 group)
-    launch_quant_group128(pb.hidden, false, P, I, mb.hq, mb.hs, flags, stream);
+    // bf16-staged SwiGLU + re-quantisation of the hidden per (placement, 128 group)
+    const uint32_t groups = P * (I >> 7);
+    t = timer_begin(K_MOE_SWIGLU, stream);
+    hipLaunchKernelGGL(prefill_swiglu_quant_kernel, dim3((groups + 3) / 4), dim3(256), 0, stream, pb.hidden, P, I,
+                       mb.hq, mb.hs, flags);
+    timer_end(t, stream);
 
     PrefillArgs da = ga;
     da.placement_pos = nullptr;
@@ -382,11 +437,11 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     da.scales = mb.hs;
     da.K = I;
     da.R = H;
+    da.R1 = H;
     da.rows = P;
     da.out = pb.y;
     t = timer_begin(K_PREFILL_DOWN, stream);
-    hipLaunchKernelGGL(prefill_b_kernel<1>, dim3(max_tiles * (H / 64)), dim3(256),
-                       (size_t)(I / 128) * (PF_MT + 1) * 4, stream, da);
+    launch_prefill_projection(da, stream);
     timer_end(t, stream);
 
     const uint32_t n4 = rows * (H >> 2);

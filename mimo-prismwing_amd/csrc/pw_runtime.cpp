@@ -1074,6 +1074,8 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
         return fail(PW_ERR_ARGUMENT, "unknown mode or dtype");
     if (rows < 1 || rows > 32)
         return fail(PW_ERR_ARGUMENT, "device MoE row count must be between one and 32");
+    if (((uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
+        return fail(PW_ERR_ARGUMENT, "route buffers must be 16-byte aligned");
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
@@ -1099,6 +1101,8 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
         return fail(PW_ERR_ARGUMENT, "unknown dtype");
     if (rows < 1 || rows > 4096)
         return fail(PW_ERR_ARGUMENT, "prefill row count must be between one and 4096");
+    if (((uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
+        return fail(PW_ERR_ARGUMENT, "route buffers must be 16-byte aligned");
     const uint32_t E = bank->n_experts, H = bank->hidden, I = bank->intermediate;
     // the device schedule keeps one bit per (expert, row) in LDS (160 KB per workgroup)
     const size_t sched_lds = ((size_t)E * ((rows + 31) / 32) + E) * 4;
