@@ -156,6 +156,22 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
             "max_count": int(np.bincount(sel.reshape(-1), minlength=256).max()), "kernels_us": kt}
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_w8_gateup_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the gate/up kernel on this workload, from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE passes (scaled by the copy-kernel calibration); None if the
+    summary is absent."""
+    import re
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", text)
+    return int(m.group(1)) if m else None
+
+
 def cpu_baseline(WL, bank, batch, budget_s=12.0):
     """The C oracle (mode A, single thread) on a bounded sample of the same layer: the routed
     experts of one width-8 batch, taken in ascending id until ~budget_s of CPU work."""
@@ -188,6 +204,10 @@ def main():
     ap.add_argument("--batches", type=int, default=8, help="token batches cycled over the steps")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="run only the 2048-token prefill leg and print its line (for profiling)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported (the expert path "
@@ -195,12 +215,27 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read": src.numel() * 4,
+                          "bytes_written": dst.numel() * 4, "launches": 5}), flush=True)
+        return
     import prismwing_amd as P
     from prismwing_amd import workloads as WL
 
     rt = P.WideMoeRuntime.compile(0)
     log("synthesising the 256-expert bank (6.4 GB) on the device")
     bank = WL.synth_bank(rt, 256, seed=WL.SEED_BASE + 2)
+    if args.prefill_only:
+        res = prefill_leg(torch, rt, bank, P, WL, zipf=False)
+        print(json.dumps({"workload": "routed-MoE prefill, 2048 tokens, top-8 of 256 experts, mode B",
+                          **res}), flush=True)
+        rt.close()
+        return
     rows = 8
     batches = build_batches(P, WL, args.batches, rows, zipf=False)
     dev_batches = upload(torch, WL, batches)
@@ -218,7 +253,7 @@ def main():
     gu_bytes = float(np.mean([gateup_bytes(sel, rows) for _, sel, _ in batches]))
     achieved = gu_bytes / (gu["avg_us"] * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                 "kernel": "moe_a_split_kernel (gate+up, SwiGLU)", "bytes_per_launch": int(gu_bytes),
                 "avg_us": round(gu["avg_us"], 2)}
 
