@@ -66,6 +66,7 @@ enum { PW_RUNTIME_FUSED_GATE_UP = 1 };
 #define PW_FLAG_FUSED_SWIGLU_NONFINITE 128u
 #define PW_FLAG_SCHEDULE 256u
 #define PW_FLAG_OUTPUT_NONFINITE 512u
+#define PW_FLAG_ROUTE 1024u /* device router: a row's scores, bias or selection were invalid */
 
 typedef struct pw_runtime pw_runtime;
 typedef struct pw_projection pw_projection;
@@ -235,6 +236,20 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
 int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t expert,
                              uint32_t mode, const void *x, uint32_t x_dtype, uint32_t rows,
                              void *output, uint32_t out_dtype, void *stream);
+
+/* ---- routing on the device ------------------------------------------------------------------ */
+/* route_mlp (src/text_endpoint.rs:4342-4380) on device buffers: logits = x [rows x hidden] .
+ * router_weight [experts x hidden]^T (f32 or bf16 each), scores = PyTorch sigmoid (SLEEF
+ * expf_u10), corrected = scores + bias, top 8 in libc++ nth_element order, weights renormalised
+ * (pytorch_noaux_routes, :4394-4473). Writes route_ids / route_weights [rows x 8] (16-byte
+ * aligned; the pw_moe_layer_device / pw_moe_prefill_device inputs), scores [rows x experts] when
+ * not NULL, and adds the number of boundary-tie rows to *tie_rows (a device counter) when not
+ * NULL. Logits sum in a fixed order: 64 lanes of fused multiply-adds over columns l, l + 64, ...,
+ * then a halving tree. An invalid row raises PW_FLAG_ROUTE and gets expert ids = experts (the
+ * layer schedule rejects them). rows 1..4096, experts 9..1024. Asynchronous on stream. */
+int pw_route_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows, uint32_t hidden,
+                    const void *router_weight, uint32_t w_dtype, uint32_t experts, const float *bias,
+                    uint32_t *route_ids, float *route_weights, float *scores, uint32_t *tie_rows, void *stream);
 
 /* ---- routing on the host (src/text_endpoint.rs:4342-4473, src/pytorch_topk.cpp:8-30) -------- */
 /* pw_pytorch_topk_unsorted_f32 with libc++ std::nth_element order: -1 on bad arguments. */

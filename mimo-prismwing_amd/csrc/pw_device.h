@@ -60,6 +60,7 @@ enum : uint32_t {
     FLAG_FUSED_SWIGLU_NONFINITE = 128u,
     FLAG_SCHEDULE = 256u,
     FLAG_OUTPUT_NONFINITE = 512u,
+    FLAG_ROUTE = 1024u,
 };
 
 // A 16-row output tile of a projection: weight rows [w, w + 16*K), one scale row (all 16 rows sit

@@ -135,6 +135,12 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
                       hipStream_t stream);
 
+// Device router (pw_router.hip): x [rows][K] (f32 or bf16) and router weights [E][K] (f32 or bf16)
+// -> scores [rows][E], selected / weights [rows][8]; tie_rows (optional) counts boundary ties.
+void launch_router(const void *x, bool x_f32, const void *w, bool w_f32, const float *bias, uint32_t rows,
+                   uint32_t E, uint32_t K, float *scores, uint32_t *selected, float *weights, uint32_t *tie_rows,
+                   uint32_t *flags, hipStream_t stream);
+
 // Routed-MoE prefill (mode B grouped block-FP8 GEMM, pw_prefill.hip) after launch_moe_schedule.
 struct PrefillBuffers {
     uint2 *tiles;       // [prefill_max_tiles] (schedule entry, first slot of a 96-slot m-tile)

@@ -15,6 +15,7 @@ namespace pw {
 
 PW_HD uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 PW_HD float f32_from(uint32_t u) { return __builtin_bit_cast(float, u); }
+PW_HD bool finite_f32_bits(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
 
 // f32 -> bf16 round-to-nearest-even, returned as the widened f32 value. NaNs keep their sign and
 // high payload and get the quiet bit 0x40 (src/text_endpoint.rs:2960-2971); infinities pass.

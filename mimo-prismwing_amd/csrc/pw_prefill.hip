@@ -300,43 +300,53 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
 // bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343)
 // on the bf16 gate/up outputs, h = round(round(g / (1 + e^-g)) * u), fused with the dynamic
 // per-(slot, 128-column group) re-quantisation of h for the down projection
-// (dynamic_fp8_quantized_group128, kernels/block_fp8_gemv.metal:84-137). One wave per group,
-// two values per lane; gu [P][2I] bf16 (gate columns, then up).
+// (dynamic_fp8_quantized_group128, kernels/block_fp8_gemv.metal:84-137). 16 lanes per group,
+// eight consecutive values per lane (16-byte loads of gate and up), four groups per wave;
+// gu [P][2I] bf16 (gate columns, then up).
 __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_t *__restrict__ gu, uint32_t P,
                                                                    uint32_t I, uint8_t *__restrict__ codes,
                                                                    float *__restrict__ scales, uint32_t *flags)
 {
-    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t lane16 = threadIdx.x & 15;
     const uint32_t groups_per_row = I >> 7;
-    const uint32_t group = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (group >= P * groups_per_row)
+    const uint32_t group = blockIdx.x * 16 + (threadIdx.x >> 4);
+    if (group >= P * groups_per_row)  // whole 16-lane groups leave together
         return;
-    const uint32_t slot = group / groups_per_row, c = (group - slot * groups_per_row) * 128 + lane * 2;
+    const uint32_t slot = group / groups_per_row, c = (group - slot * groups_per_row) * 128 + lane16 * 8;
     const uint16_t *row = gu + (size_t)slot * 2 * I;
-    const uint32_t g2 = *(const uint32_t *)(row + c), u2 = *(const uint32_t *)(row + I + c);
-    float h[2];
+    const uint4 g4 = *(const uint4 *)(row + c), u4 = *(const uint4 *)(row + I + c);
+    const uint32_t gw[4] = {g4.x, g4.y, g4.z, g4.w}, uw[4] = {u4.x, u4.y, u4.z, u4.w};
+    float h[8];
     bool bad = false;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float gv = f32_from(i ? (g2 & 0xffff0000u) : (g2 << 16));
-        const float uv = f32_from(i ? (u2 & 0xffff0000u) : (u2 << 16));
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t gb = gw[i >> 1], ub = uw[i >> 1];
+        const float gv = f32_from((i & 1) ? (gb & 0xffff0000u) : (gb << 16));
+        const float uv = f32_from((i & 1) ? (ub & 0xffff0000u) : (ub << 16));
         const float silu = round_bf16(gv / (1.0f + expf(-gv)));
         h[i] = round_bf16(silu * uv);
         bad |= !finite_f32(gv) || !finite_f32(uv) || !finite_f32(h[i]);
     }
     if (bad)
         raise_flag(flags, FLAG_SWIGLU_NONFINITE);
-    const bool f0 = finite_f32(h[0]), f1 = finite_f32(h[1]);
-    float m = fmaxf(f0 ? fabsf(h[0]) : 0.f, f1 ? fabsf(h[1]) : 0.f);
-    m = wave_max(m);
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        m = fmaxf(m, finite_f32(h[i]) ? fabsf(h[i]) : 0.f);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
+        m = fmaxf(m, __shfl_xor(m, off, 16));
     const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
-    if (lane == 0)
+    if (lane16 == 0)
         scales[group] = scale;
-    float n0 = h[0] / scale, n1 = h[1] / scale;
-    n0 = n0 < -448.f ? -448.f : (n0 > 448.f ? 448.f : n0);
-    n1 = n1 < -448.f ? -448.f : (n1 > 448.f ? 448.f : n1);
-    *(uint16_t *)(codes + (size_t)slot * I + c) =
-        (uint16_t)encode_e4m3fn_rne(f0 ? n0 : 0.f) | ((uint16_t)encode_e4m3fn_rne(f1 ? n1 : 0.f) << 8);
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float n = finite_f32(h[i]) ? h[i] / scale : 0.f;
+        n = n < -448.f ? -448.f : (n > 448.f ? 448.f : n);
+        packed[i >> 2] |= (uint32_t)encode_e4m3fn_rne(n) << (8 * (i & 3));
+    }
+    *(uint2 *)(codes + (size_t)slot * I + c) = make_uint2(packed[0], packed[1]);
 }
 
 // route_weighted_scatter_add_f32 + final bf16 round over bf16 expert outputs: each token sums
@@ -427,8 +437,8 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     // bf16-staged SwiGLU + re-quantisation of the hidden per (placement, 128 group)
     const uint32_t groups = P * (I >> 7);
     t = timer_begin(K_MOE_SWIGLU, stream);
-    hipLaunchKernelGGL(prefill_swiglu_quant_kernel, dim3((groups + 3) / 4), dim3(256), 0, stream, pb.hidden, P, I,
-                       mb.hq, mb.hs, flags);
+    hipLaunchKernelGGL(prefill_swiglu_quant_kernel, dim3((groups + 15) / 16), dim3(256), 0, stream, pb.hidden, P,
+                       I, mb.hq, mb.hs, flags);
     timer_end(t, stream);
 
     PrefillArgs da = ga;

@@ -18,6 +18,7 @@
 
 #include "../../include/pwfp8.h"
 #include "pw_launch.h"
+#include "pw_topk.h"
 #include "pw_numerics.h"
 
 using pw::ExpertPtrs;
@@ -98,7 +99,7 @@ struct pw_runtime {
     // routed-MoE per-layer scratch
     DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
         moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
-        moe_active, moe_partial, pf_tiles;
+        moe_active, moe_partial, pf_tiles, router_scores;
     MoeBuffers mb{};
     pw::KernelTimer timer;
 };
@@ -297,166 +298,8 @@ int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I
     return PW_OK;
 }
 
-// ---- libc++ std::nth_element over (value, index) pairs, greater-by-value ---------------------
-// The reference's top-k (src/pytorch_topk.cpp:8-30) is std::nth_element(first, first + k - 1,
-// last) from the C++ library PyTorch was built with (libc++ for the golden orders). This is that
-// published algorithm: median-of-three, guarded Hoare partition that tracks the pivot, the
-// all-equal fallback partition, the already-partitioned check, selection sort below 8 elements.
-struct Entry {
-    float v;
-    int64_t i;
-};
-
-inline bool greater(const Entry &a, const Entry &b) { return a.v > b.v; }
-
-unsigned sort3(Entry *x, Entry *y, Entry *z)
-{
-    if (!greater(*y, *x)) {
-        if (!greater(*z, *y))
-            return 0;
-        std::swap(*y, *z);
-        if (greater(*y, *x)) {
-            std::swap(*x, *y);
-            return 2;
-        }
-        return 1;
-    }
-    if (greater(*z, *y)) {
-        std::swap(*x, *z);
-        return 1;
-    }
-    std::swap(*x, *y);
-    if (greater(*z, *y)) {
-        std::swap(*y, *z);
-        return 2;
-    }
-    return 1;
-}
-
-void select_sort(Entry *first, Entry *last)
-{
-    for (Entry *lm1 = last - 1; first != lm1; ++first) {
-        Entry *best = first;
-        for (Entry *it = first + 1; it != last; ++it)
-            if (greater(*it, *best))
-                best = it;
-        if (best != first)
-            std::swap(*first, *best);
-    }
-}
-
-void nth_element_cxx(Entry *first, Entry *nth, Entry *last)
-{
-    for (;;) {
-        if (nth == last)
-            return;
-        const ptrdiff_t len = last - first;
-        if (len <= 1)
-            return;
-        if (len == 2) {
-            if (greater(last[-1], *first))
-                std::swap(*first, last[-1]);
-            return;
-        }
-        if (len == 3) {
-            sort3(first, first + 1, last - 1);
-            return;
-        }
-        if (len <= 7) {
-            select_sort(first, last);
-            return;
-        }
-        Entry *m = first + len / 2, *lm1 = last - 1;
-        unsigned swaps = sort3(first, m, lm1);
-        Entry *i = first, *j = lm1;
-        if (!greater(*i, *m)) {
-            bool guard = false;
-            while (!(i == --j)) {
-                if (greater(*j, *m)) {
-                    guard = true;
-                    break;
-                }
-            }
-            if (guard) {
-                std::swap(*i, *j);
-                ++swaps;
-            } else {
-                ++i;
-                j = last;
-                if (!greater(*first, *--j)) {
-                    for (;; ++i) {
-                        if (i == j)
-                            return;
-                        if (greater(*first, *i)) {
-                            std::swap(*i, *j);
-                            ++swaps;
-                            ++i;
-                            break;
-                        }
-                    }
-                }
-                if (i == j)
-                    return;
-                for (;;) {
-                    while (!greater(*first, *i))
-                        ++i;
-                    do
-                        --j;
-                    while (greater(*first, *j));
-                    if (i >= j)
-                        break;
-                    std::swap(*i, *j);
-                    ++swaps;
-                    ++i;
-                }
-                if (nth < i)
-                    return;
-                first = i;
-                continue;
-            }
-        }
-        ++i;
-        if (i < j) {
-            for (;;) {
-                while (greater(*i, *m))
-                    ++i;
-                do
-                    --j;
-                while (!greater(*j, *m));
-                if (i >= j)
-                    break;
-                std::swap(*i, *j);
-                ++swaps;
-                if (m == i)
-                    m = j;
-                ++i;
-            }
-        }
-        if (i != m && greater(*m, *i)) {
-            std::swap(*i, *m);
-            ++swaps;
-        }
-        if (nth == i)
-            return;
-        if (swaps == 0) {
-            Entry *a = nth < i ? first : i, *end = nth < i ? i : last, *prev = a;
-            bool sorted = true;
-            while (++a != end) {
-                if (greater(*a, *prev)) {
-                    sorted = false;
-                    break;
-                }
-                prev = a;
-            }
-            if (sorted)
-                return;
-        }
-        if (nth < i)
-            last = i;
-        else
-            first = i + 1;
-    }
-}
+// The libc++ nth_element top-k and the noaux route row are shared with the device router
+// (pw_topk.h).
 
 }  // namespace
 
@@ -1132,6 +975,32 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
     return PW_OK;
 }
 
+int pw_route_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows, uint32_t hidden,
+                    const void *router_weight, uint32_t w_dtype, uint32_t experts, const float *bias,
+                    uint32_t *route_ids, float *route_weights, float *scores, uint32_t *tie_rows, void *stream)
+{
+    if (!rt || !x || !router_weight || !bias || !route_ids || !route_weights)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (x_dtype > PW_DTYPE_BF16 || w_dtype > PW_DTYPE_BF16)
+        return fail(PW_ERR_ARGUMENT, "unknown dtype");
+    if (rows < 1 || rows > 4096 || hidden == 0 || experts <= 8 || experts > 1024)
+        return fail(PW_ERR_ARGUMENT, "router needs 1..4096 rows, a hidden size and 9..1024 experts");
+    if (((uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
+        return fail(PW_ERR_ARGUMENT, "route buffers must be 16-byte aligned");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    float *sc = scores;
+    if (!sc) {
+        PW_HIP(rt->router_scores.ensure((size_t)rows * experts * 4));
+        sc = (float *)rt->router_scores.p;
+    }
+    pw::launch_router(x, x_dtype == PW_DTYPE_F32, router_weight, w_dtype == PW_DTYPE_F32, bias, rows, experts, hidden,
+                      sc, route_ids, route_weights, tie_rows, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
 int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t expert,
                              uint32_t mode, const void *x, uint32_t x_dtype, uint32_t rows,
                              void *output, uint32_t out_dtype, void *stream)
@@ -1160,13 +1029,13 @@ int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_
 // ----------------------------------------------------------------------------- host routing
 int pw_topk_unsorted_f32(const float *values, size_t count, size_t top_k, uint32_t *selected)
 {
-    if (!values || !selected || top_k == 0 || top_k >= count)
+    if (!values || !selected || top_k == 0 || top_k >= count || count > (size_t)INT32_MAX)
         return -1;
     try {
-        std::vector<Entry> q(count);
+        std::vector<pw::TopkEntry> q(count);
         for (size_t i = 0; i < count; ++i)
-            q[i] = Entry{values[i], (int64_t)i};
-        nth_element_cxx(q.data(), q.data() + top_k - 1, q.data() + count);
+            q[i] = pw::TopkEntry{values[i], (int32_t)i};
+        pw::nth_element_libcxx(q.data(), q.data() + top_k - 1, q.data() + count);
         for (size_t i = 0; i < top_k; ++i)
             selected[i] = (uint32_t)q[i].i;
     } catch (...) {
@@ -1187,52 +1056,19 @@ int pw_noaux_routes(const float *scores, const float *bias, uint32_t rows, uint3
     for (uint32_t e = 0; e < experts; ++e)
         if (!finite(bias[e]))
             return fail(PW_ERR_NONFINITE, "invalid PyTorch noaux-tc inputs");
-    std::vector<float> corrected(experts);
-    std::vector<uint8_t> chosen(experts);
+    std::vector<pw::TopkEntry> scratch(experts);
     uint64_t ties = 0;
     for (uint32_t p = 0; p < rows; ++p) {
-        const float *row = scores + (size_t)p * experts;
-        for (uint32_t e = 0; e < experts; ++e)
-            corrected[e] = row[e] + bias[e];
-        uint32_t sel[K];
-        if (pw_topk_unsorted_f32(corrected.data(), experts, K, sel) != 0)
+        bool tie = false;
+        const int st = pw::noaux_route_row(scores + (size_t)p * experts, bias, experts, scratch.data(),
+                                           selected + (size_t)p * K, weights + (size_t)p * K, &tie);
+        if (st == pw::ROUTE_NONFINITE)
+            return fail(PW_ERR_NONFINITE, "invalid PyTorch noaux-tc inputs");
+        if (st == pw::ROUTE_TOPK)
             return fail(PW_ERR_SCHEDULE, "PyTorch top-k failed at position %u", p);
-        std::fill(chosen.begin(), chosen.end(), 0);
-        for (uint32_t i = 0; i < K; ++i) {
-            if (sel[i] >= experts || chosen[sel[i]])
-                return fail(PW_ERR_SCHEDULE, "PyTorch top-k failed at position %u", p);
-            chosen[sel[i]] = 1;
-        }
-        float boundary = INFINITY, rejected = -INFINITY;
-        for (uint32_t i = 0; i < K; ++i)
-            boundary = std::fmin(boundary, corrected[sel[i]]);
-        for (uint32_t e = 0; e < experts; ++e)
-            if (!chosen[e])
-                rejected = std::fmax(rejected, corrected[e]);
-        if (!finite(boundary) || boundary < rejected)
-            return fail(PW_ERR_SCHEDULE, "top-k selected a value below the rejected boundary at position %u", p);
-        if (boundary == rejected)
-            ++ties;
-        // pytorch_sum_eight (src/text_endpoint.rs:4382-4390) + 1e-20
-        float c[K];
-        for (uint32_t i = 0; i < K; ++i)
-            c[i] = row[sel[i]];
-        const float lanes[4] = {c[0] + c[4], c[1] + c[5], c[2] + c[6], c[3] + c[7]};
-        float sum = 0.0f;
-        for (float l : lanes)
-            sum = sum + l;
-        const float denominator = sum + 1.0e-20f;
-        float wsum = 0.0f;
-        for (uint32_t i = 0; i < K; ++i) {
-            const float w = row[sel[i]] / denominator;
-            if (!finite(w) || w < 0.0f)
-                return fail(PW_ERR_NONFINITE, "PyTorch route weights invalid at position %u", p);
-            weights[(size_t)p * K + i] = w;
-            selected[(size_t)p * K + i] = sel[i];
-            wsum += w;
-        }
-        if (std::fabs(wsum - 1.0f) > 1.0e-6f)
+        if (st == pw::ROUTE_WEIGHTS)
             return fail(PW_ERR_NONFINITE, "PyTorch route weights invalid at position %u", p);
+        ties += tie ? 1 : 0;
     }
     if (tie_rows)
         *tie_rows = ties;

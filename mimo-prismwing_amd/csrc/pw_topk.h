@@ -1,0 +1,244 @@
+// The reference's routing selection, shared by the host routing helpers and the device router
+// so both produce the same routes from the same source.
+//
+// Top-k: src/pytorch_topk.cpp:8-30 calls std::nth_element(first, first + k - 1, last) over
+// (value, index) pairs ordered greater-by-value, from the C++ library PyTorch was built with
+// (libc++ for the reference's golden orders), and returns the first k indices in partition
+// order. This is that published algorithm (libc++ <__algorithm/nth_element.h>): median of three,
+// a guarded partition that tracks the pivot, the all-not-greater fallback partition, the
+// already-partitioned check, and selection sort below 8 elements.
+//
+// Routes: pytorch_noaux_routes (src/text_endpoint.rs:4394-4473): corrected = score + bias, top 8
+// of corrected, boundary check against the best rejected value (equality counts as a tie), and
+// weights score_i / (pytorch_sum_eight(scores) + 1e-20) with pytorch_sum_eight
+// (src/text_endpoint.rs:4382-4390) = fold(0, +) over (s0 + s4, s1 + s5, s2 + s6, s3 + s7).
+#pragma once
+
+#include <stdint.h>
+
+#include "pw_numerics.h"
+
+namespace pw {
+
+struct TopkEntry {
+    float v;
+    int32_t i;
+};
+
+PW_HD bool topk_greater(const TopkEntry &a, const TopkEntry &b) { return a.v > b.v; }
+
+PW_HD void topk_swap(TopkEntry &a, TopkEntry &b)
+{
+    const TopkEntry t = a;
+    a = b;
+    b = t;
+}
+
+PW_HD unsigned topk_sort3(TopkEntry *x, TopkEntry *y, TopkEntry *z)
+{
+    if (!topk_greater(*y, *x)) {
+        if (!topk_greater(*z, *y))
+            return 0;
+        topk_swap(*y, *z);
+        if (topk_greater(*y, *x)) {
+            topk_swap(*x, *y);
+            return 2;
+        }
+        return 1;
+    }
+    if (topk_greater(*z, *y)) {
+        topk_swap(*x, *z);
+        return 1;
+    }
+    topk_swap(*x, *y);
+    if (topk_greater(*z, *y)) {
+        topk_swap(*y, *z);
+        return 2;
+    }
+    return 1;
+}
+
+PW_HD void topk_select_sort(TopkEntry *first, TopkEntry *last)
+{
+    for (TopkEntry *lm1 = last - 1; first != lm1; ++first) {
+        TopkEntry *best = first;
+        for (TopkEntry *it = first + 1; it != last; ++it)
+            if (topk_greater(*it, *best))
+                best = it;
+        if (best != first)
+            topk_swap(*first, *best);
+    }
+}
+
+PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
+{
+    for (;;) {
+        if (nth == last)
+            return;
+        const long len = (long)(last - first);
+        if (len <= 1)
+            return;
+        if (len == 2) {
+            if (topk_greater(last[-1], *first))
+                topk_swap(*first, last[-1]);
+            return;
+        }
+        if (len == 3) {
+            topk_sort3(first, first + 1, last - 1);
+            return;
+        }
+        if (len <= 7) {
+            topk_select_sort(first, last);
+            return;
+        }
+        TopkEntry *m = first + len / 2, *lm1 = last - 1;
+        unsigned swaps = topk_sort3(first, m, lm1);
+        TopkEntry *i = first, *j = lm1;
+        if (!topk_greater(*i, *m)) {
+            bool guard = false;
+            while (!(i == --j)) {
+                if (topk_greater(*j, *m)) {
+                    guard = true;
+                    break;
+                }
+            }
+            if (guard) {
+                topk_swap(*i, *j);
+                ++swaps;
+            } else {
+                ++i;
+                j = last;
+                if (!topk_greater(*first, *--j)) {
+                    for (;; ++i) {
+                        if (i == j)
+                            return;
+                        if (topk_greater(*first, *i)) {
+                            topk_swap(*i, *j);
+                            ++swaps;
+                            ++i;
+                            break;
+                        }
+                    }
+                }
+                if (i == j)
+                    return;
+                for (;;) {
+                    while (!topk_greater(*first, *i))
+                        ++i;
+                    do
+                        --j;
+                    while (topk_greater(*first, *j));
+                    if (i >= j)
+                        break;
+                    topk_swap(*i, *j);
+                    ++swaps;
+                    ++i;
+                }
+                if (nth < i)
+                    return;
+                first = i;
+                continue;
+            }
+        }
+        ++i;
+        if (i < j) {
+            for (;;) {
+                while (topk_greater(*i, *m))
+                    ++i;
+                do
+                    --j;
+                while (!topk_greater(*j, *m));
+                if (i >= j)
+                    break;
+                topk_swap(*i, *j);
+                ++swaps;
+                if (m == i)
+                    m = j;
+                ++i;
+            }
+        }
+        if (i != m && topk_greater(*m, *i)) {
+            topk_swap(*i, *m);
+            ++swaps;
+        }
+        if (nth == i)
+            return;
+        if (swaps == 0) {
+            TopkEntry *a = nth < i ? first : i, *end = nth < i ? i : last, *prev = a;
+            bool sorted = true;
+            while (++a != end) {
+                if (topk_greater(*a, *prev)) {
+                    sorted = false;
+                    break;
+                }
+                prev = a;
+            }
+            if (sorted)
+                return;
+        }
+        if (nth < i)
+            last = i;
+        else
+            first = i + 1;
+    }
+}
+
+// Outcome of one routed row.
+enum RouteStatus : int { ROUTE_OK = 0, ROUTE_NONFINITE = 1, ROUTE_TOPK = 2, ROUTE_WEIGHTS = 3 };
+
+// One row of pytorch_noaux_routes: scores [experts] (sigmoid outputs), bias [experts] ->
+// selected[8], weights[8]; *tie = the boundary value equals the best rejected value. `scratch`
+// holds `experts` entries. Returns a RouteStatus.
+PW_HD int noaux_route_row(const float *scores, const float *bias, uint32_t experts, TopkEntry *scratch,
+                                 uint32_t *selected, float *weights, bool *tie)
+{
+    constexpr uint32_t K = 8;
+    *tie = false;
+    for (uint32_t e = 0; e < experts; ++e) {
+        if (!finite_f32_bits(scores[e]) || !finite_f32_bits(bias[e]))
+            return ROUTE_NONFINITE;
+        scratch[e].v = scores[e] + bias[e];
+        scratch[e].i = (int32_t)e;
+    }
+    nth_element_libcxx(scratch, scratch + K - 1, scratch + experts);
+    uint32_t sel[K];
+    for (uint32_t k = 0; k < K; ++k) {
+        sel[k] = (uint32_t)scratch[k].i;
+        for (uint32_t j = 0; j < k; ++j)
+            if (sel[j] == sel[k])
+                return ROUTE_TOPK;
+    }
+    // boundary check against the best rejected value
+    float boundary = scratch[0].v;
+    for (uint32_t k = 1; k < K; ++k)
+        boundary = scratch[k].v < boundary ? scratch[k].v : boundary;
+    float rejected = -__builtin_inff();
+    for (uint32_t k = K; k < experts; ++k)
+        rejected = scratch[k].v > rejected ? scratch[k].v : rejected;
+    if (!finite_f32_bits(boundary) || boundary < rejected)
+        return ROUTE_TOPK;
+    *tie = boundary == rejected;
+    float c[K];
+    for (uint32_t k = 0; k < K; ++k)
+        c[k] = scores[sel[k]];
+    const float lanes[4] = {c[0] + c[4], c[1] + c[5], c[2] + c[6], c[3] + c[7]};
+    float sum = 0.0f;
+    for (uint32_t l = 0; l < 4; ++l)
+        sum = sum + lanes[l];
+    const float denominator = sum + 1.0e-20f;
+    float wsum = 0.0f;
+    for (uint32_t k = 0; k < K; ++k) {
+        const float w = scores[sel[k]] / denominator;
+        if (!finite_f32_bits(w) || w < 0.0f)
+            return ROUTE_WEIGHTS;
+        weights[k] = w;
+        selected[k] = sel[k];
+        wsum += w;
+    }
+    const float dev = wsum - 1.0f;
+    if ((dev < 0.0f ? -dev : dev) > 1.0e-6f)
+        return ROUTE_WEIGHTS;
+    return ROUTE_OK;
+}
+
+}  // namespace pw

@@ -19,6 +19,9 @@ MODE_A, MODE_B = 0, 1
 DTYPE_F32, DTYPE_BF16, DTYPE_F32_RAW = 0, 1, 2
 LAYOUT_PLAIN, LAYOUT_FULL_QKV_TP4, LAYOUT_SWA_QKV_TP4 = 0, 1, 2
 RUNTIME_FUSED_GATE_UP = 1
+# GPU error bits (include/pwfp8.h PW_FLAG_*)
+FLAG_SCHEDULE = 256
+FLAG_ROUTE = 1024
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
 _f32p = ctypes.POINTER(ctypes.c_float)
@@ -88,6 +91,7 @@ SIGNATURES = {
     "pw_moe_layer_device": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
     "pw_expert_forward_device": (_i, [_vp, _vp, _u32, _u32, _vp, _u32, _u32, _vp, _u32, _vp]),
     "pw_moe_prefill_device": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
+    "pw_route_device": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "pw_topk_unsorted_f32": (_i, [_f32p, _sz, _sz, _u32p]),
     "pw_noaux_routes": (_i, [_f32p, _f32p, _u32, _u32, _u32p, _f32p, _u64p]),
     "pw_route_from_logits": (_i, [_f32p, _f32p, _u32, _u32, _f32p, _u32p, _f32p, _u64p]),

@@ -268,6 +268,15 @@ class WideMoeRuntime:
         check(lib().pw_moe_prefill_device(self.handle, bank.handle, _ptr(x), x_dtype, rows, _ptr(route_ids),
                                           _ptr(route_weights), _ptr(out), out_dtype, stream or 0))
 
+    def route_device(self, x, rows: int, hidden: int, router_weight, experts: int, bias, route_ids, route_weights,
+                     x_dtype: int = DTYPE_BF16, w_dtype: int = DTYPE_BF16, scores=None, tie_rows=None,
+                     stream: Optional[int] = None):
+        """route_mlp on device buffers -> route_ids / route_weights [rows x 8] (and scores)."""
+        check(lib().pw_route_device(self.handle, _ptr(x), x_dtype, rows, hidden, _ptr(router_weight), w_dtype,
+                                    experts, _ptr(bias), _ptr(route_ids), _ptr(route_weights),
+                                    _ptr(scores) if scores is not None else None,
+                                    _ptr(tie_rows) if tie_rows is not None else None, stream or 0))
+
     def expert_forward_device(self, bank: ExpertBank, expert: int, x, rows: int, out, mode: int = MODE_A,
                               x_dtype: int = DTYPE_BF16, out_dtype: int = DTYPE_BF16,
                               stream: Optional[int] = None):

@@ -1,0 +1,125 @@
+"""GPU parity of the on-device router (route_mlp, src/text_endpoint.rs:4342-4473) through the C ABI.
+
+Routes are integer work and must match the C oracle bit for bit: selected expert ids in libc++
+nth_element order, renormalised weights, sigmoid scores and tie counts. The oracle's logits use the
+same declared summation order (64 lanes of fused multiply-adds, then a halving tree), and its
+top-k order is pinned by the reference's golden orders (pw0063, pw0157).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import prismwing_amd as P
+from prismwing_amd import workloads as WL
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_dev(torch, a):
+    return torch.from_numpy(WL.bf16_bits_np(a).view(np.int16)).cuda()
+
+
+def _device_route(rt, torch, x, rw, bias, x_f32=False, w_f32=False):
+    rows, hidden = x.shape
+    experts = rw.shape[0]
+    xt = torch.from_numpy(x.astype(np.float32)).cuda() if x_f32 else _bf16_dev(torch, x)
+    wt = torch.from_numpy(rw.astype(np.float32)).cuda() if w_f32 else _bf16_dev(torch, rw)
+    bt = torch.from_numpy(bias.astype(np.float32)).cuda()
+    ids = torch.zeros((rows, 8), dtype=torch.int32, device="cuda")
+    wts = torch.zeros((rows, 8), dtype=torch.float32, device="cuda")
+    scores = torch.zeros((rows, experts), dtype=torch.float32, device="cuda")
+    ties = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rt.route_device(xt, rows, hidden, wt, experts, bt, ids, wts, x_dtype=P.DTYPE_F32 if x_f32 else P.DTYPE_BF16,
+                    w_dtype=P.DTYPE_F32 if w_f32 else P.DTYPE_BF16, scores=scores, tie_rows=ties,
+                    stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    flags = rt.take_flags()
+    return (ids.cpu().numpy().astype(np.uint32), wts.cpu().numpy(), scores.cpu().numpy(), int(ties.item()), flags)
+
+
+@pytest.mark.parametrize("rows,zipf", [(1, False), (8, False), (8, True), (32, False), (300, True)])
+def test_device_routes_bit_exact(rt, rows, zipf):
+    import torch
+    x = WL.activations(rows, WL.SEED_BASE + 60 + rows)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
+    ids, wts, scores, ties, flags = _device_route(rt, torch, x, rw, bias)
+    assert flags == 0
+    _, ref_scores, ref_sel, ref_w, ref_ties = O.route(x, rw, bias)
+    assert np.array_equal(scores.view(np.uint32), ref_scores.view(np.uint32))
+    assert np.array_equal(ids, ref_sel)
+    assert np.array_equal(wts.view(np.uint32), ref_w.view(np.uint32))
+    assert ties == ref_ties
+
+
+def test_device_routes_f32_inputs(rt):
+    """f32 activations and f32 router weights (the checkpoint stores the router in F32)."""
+    import torch
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((8, 4096)).astype(np.float32)
+    rw = (rng.standard_normal((256, 4096)) * 0.02).astype(np.float32)
+    bias = rng.uniform(-0.01, 0.01, 256).astype(np.float32)
+    ids, wts, scores, ties, flags = _device_route(rt, torch, x, rw, bias, x_f32=True, w_f32=True)
+    assert flags == 0
+    _, ref_scores, ref_sel, ref_w, ref_ties = O.route(x, rw, bias)
+    assert np.array_equal(ids, ref_sel)
+    assert np.array_equal(wts.view(np.uint32), ref_w.view(np.uint32))
+    assert np.array_equal(scores.view(np.uint32), ref_scores.view(np.uint32))
+
+
+def test_device_routes_with_ties(rt):
+    """Logits equal to chosen values (one-hot activation on column 0), with repeated values at the
+    top-8 boundary: the selection order is the libc++ partition order and ties are counted."""
+    import torch
+    rows, hidden, experts = 6, 256, 64
+    rng = np.random.default_rng(5)
+    x = np.zeros((rows, hidden), np.float32)
+    x[:, 0] = 1.0
+    rw = np.zeros((experts, hidden), np.float32)
+    levels = np.array([0.5, 0.25, 0.125, 0.0625, -0.5], np.float32)
+    rw[:, 0] = levels[rng.integers(0, levels.size, experts)]
+    bias = np.zeros(experts, np.float32)
+    ids, wts, scores, ties, flags = _device_route(rt, torch, x, rw, bias, x_f32=True, w_f32=True)
+    _, ref_scores, ref_sel, ref_w, ref_ties = O.route(x, rw, bias)
+    assert flags == 0
+    assert np.array_equal(ids, ref_sel)
+    assert np.array_equal(wts.view(np.uint32), ref_w.view(np.uint32))
+    assert ties == ref_ties and ties == rows
+
+
+def test_device_router_feeds_the_layer(rt):
+    """Device routes drive the decode layer without a host round trip: same output as host routes."""
+    import torch
+    bank = WL.synth_bank(rt, n_experts=16, hidden=256, inter=128, seed=WL.SEED_BASE + 70)
+    rows = 8
+    x = WL.activations(rows, WL.SEED_BASE + 71, hidden=256)
+    rng = np.random.default_rng(12)
+    rw = WL.bf16_round_np((rng.standard_normal((16, 256)) * 0.02).astype(np.float32))
+    bias = rng.uniform(-0.01, 0.01, 16).astype(np.float32)
+    xt = _bf16_dev(torch, x)
+    wt = _bf16_dev(torch, rw)
+    bt = torch.from_numpy(bias).cuda()
+    ids = torch.zeros((rows, 8), dtype=torch.int32, device="cuda")
+    wts = torch.zeros((rows, 8), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    rt.route_device(xt, rows, 256, wt, 16, bt, ids, wts, stream=stream)
+    out_dev = torch.empty((rows, 256), dtype=torch.int16, device="cuda")
+    rt.moe_layer_device(bank.bank, xt, rows, ids, wts, out_dev, mode=P.MODE_A, stream=stream)
+    _, _, sel, w, _ = O.route(x, rw, bias)
+    ids_h = torch.from_numpy(sel.astype(np.int32)).cuda()
+    w_h = torch.from_numpy(w).cuda()
+    out_host = torch.empty((rows, 256), dtype=torch.int16, device="cuda")
+    rt.moe_layer_device(bank.bank, xt, rows, ids_h, w_h, out_host, mode=P.MODE_A, stream=stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    assert torch.equal(out_dev, out_host)
+
+
+def test_device_router_flags_nonfinite_bias(rt):
+    import torch
+    x = WL.activations(4, WL.SEED_BASE + 72)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    bias = bias.copy()
+    bias[17] = np.nan
+    ids, wts, _, _, flags = _device_route(rt, torch, x, rw, bias)
+    assert flags & P.FLAG_ROUTE
+    assert (ids == 256).all() and (wts == 0).all()
