@@ -156,6 +156,105 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
             "max_count": int(np.bincount(sel.reshape(-1), minlength=256).max()), "kernels_us": kt}
 
 
+def _time_calls(torch, rt, run, n_calls, warmup=3):
+    """µs per call of `run(i)` over n_calls back-to-back calls on the runtime's stream."""
+    stream = torch.cuda.ExternalStream(rt.stream)
+    for i in range(warmup):
+        run(i, stream.cuda_stream)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(n_calls):
+        run(i, stream.cuda_stream)
+    end.record(stream)
+    torch.cuda.synchronize()
+    if rt.take_flags():
+        raise RuntimeError("kernels raised error flags")
+    return 1000.0 * start.elapsed_time(end) / n_calls
+
+
+def _bf16_x(torch, WL, rows, hidden, seed):
+    return torch.from_numpy(WL.bf16_bits_np(WL.activations(rows, seed, hidden=hidden)).view(np.int16)).cuda()
+
+
+def projection_legs(torch, rt, bank, P, WL, calls=200):
+    """Configs 0, 1 and 3 (one projection, one complete expert, separate q/k/v segments), mode A,
+    bf16 in and out. HBM-cold: calls rotate over distinct weights well beyond the 256 MB MALL;
+    MALL-warm: one weight copy reused."""
+    out = {}
+    # config 0: W [2048 x 4096] e4m3 + S [16 x 32], x [1 x 4096] -> y [1 x 2048]
+    copies, n, k = 64, 2048, 4096
+    w = torch.empty((copies * n, k), dtype=torch.uint8, device="cuda")
+    s = torch.empty((copies * n // 128, k // 128), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    rt.synth_scales(s, s.numel(), WL.SEED_BASE + 500)
+    rt.synth_fp8(w, s, copies * n, k, WL.SEED_BASE + 501)
+    projs = [rt.bind_projection_device(w[i * n:(i + 1) * n], s[i * n // 128:(i + 1) * n // 128], n, k)
+             for i in range(copies)]
+    x = _bf16_x(torch, WL, 1, k, WL.SEED_BASE + 502)
+    y = torch.empty((1, n), dtype=torch.int16, device="cuda")
+    alg = n * k + (n // 128) * (k // 128) * 4 + k * 2 + n * 2
+    for label, pick in (("hbm_cold", lambda i: projs[i % copies]), ("mall_warm", lambda i: projs[0])):
+        us = _time_calls(torch, rt, lambda i, st: rt.fp8_linear_device(pick(i), x, 1, y, mode=P.MODE_A,
+                                                                     out_dtype=P.DTYPE_BF16, stream=st), calls)
+        out.setdefault("config0_w1", {})[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+    out["config0_w1"]["algorithmic_bytes"] = alg
+    del projs, w, s
+    # config 1: one complete expert (gate/up [2 x 2048 x 4096], down [4096 x 2048]) at widths 1..8
+    for width in (1, 2, 4, 8):
+        x = _bf16_x(torch, WL, width, 4096, WL.SEED_BASE + 510 + width)
+        y = torch.empty((width, 4096), dtype=torch.int16, device="cuda")
+        alg = EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES + width * 4096 * 2 * 2
+        rec = {"algorithmic_bytes": alg}
+        for label, pick in (("hbm_cold", lambda i: i % 256), ("mall_warm", lambda i: 0)):
+            us = _time_calls(torch, rt, lambda i, st: rt.expert_forward_device(
+                bank.bank, pick(i), x, width, y, mode=P.MODE_A, out_dtype=P.DTYPE_BF16, stream=st), calls)
+            rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+        out[f"config1_w{width}"] = rec
+    # config 3: separate q [12288], k [768 or 1000], v [512] x 4096 with their own scale grids
+    for k_rows in (768, 1000):
+        seg_rows = (12288, k_rows, 512)
+        copies = 10
+        hosts = []
+        for c in range(copies):
+            segs = []
+            for j, r in enumerate(seg_rows):
+                ws = torch.empty((r, 4096), dtype=torch.uint8, device="cuda")
+                ss = torch.empty(((r + 127) // 128, 32), dtype=torch.float32, device="cuda")
+                seed = WL.SEED_BASE + 600 + 10 * c + j
+                rt.synth_scales(ss, ss.numel(), seed)
+                rt.synth_fp8(ws, ss, r, 4096, seed + 5)
+                segs.append((ws.cpu().numpy(), ss.cpu().numpy()))
+            hosts.append(segs)
+        projs = [rt.bind_segments(segs, scan_codes=False) for segs in hosts]
+        total = sum(seg_rows)
+        for width in (1, 8):
+            x = _bf16_x(torch, WL, width, 4096, WL.SEED_BASE + 620 + width)
+            y = torch.empty((width, total), dtype=torch.int16, device="cuda")
+            alg = total * 4096 + sum((r + 127) // 128 for r in seg_rows) * 32 * 4 + width * (4096 + total) * 2
+            rec = {"algorithmic_bytes": alg}
+            for label, pick in (("hbm_cold", lambda i: projs[i % copies]), ("mall_warm", lambda i: projs[0])):
+                us = _time_calls(torch, rt, lambda i, st: rt.fp8_linear_device(
+                    pick(i), x, width, y, mode=P.MODE_A, out_dtype=P.DTYPE_BF16, stream=st), calls)
+                rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+            out[f"config3_k{k_rows}_w{width}"] = rec
+        del projs, hosts
+    return out
+
+
+def router_leg(torch, rt, P, WL, rows=8, calls=200):
+    """On-device router (logits, sigmoid, top-8, weights) for one decode batch: x [8 x 4096] bf16,
+    router weights [256 x 4096] bf16."""
+    x = _bf16_x(torch, WL, rows, 4096, WL.SEED_BASE + 700)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    wt = torch.from_numpy(WL.bf16_bits_np(rw).view(np.int16)).cuda()
+    bt = torch.from_numpy(bias).cuda()
+    ids = torch.empty((rows, 8), dtype=torch.int32, device="cuda")
+    wts = torch.empty((rows, 8), dtype=torch.float32, device="cuda")
+    us = _time_calls(torch, rt, lambda i, st: rt.route_device(x, rows, 4096, wt, 256, bt, ids, wts, stream=st), calls)
+    return {"us": round(us, 2), "rows": rows}
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_w8_gateup_hbm_traffic.md")
 
 
@@ -206,6 +305,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="run only the 2048-token prefill leg and print its line (for profiling)")
+    ap.add_argument("--router-only", action="store_true",
+                    help="run only the on-device router leg and print its line (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -228,6 +329,11 @@ def main():
     from prismwing_amd import workloads as WL
 
     rt = P.WideMoeRuntime.compile(0)
+    if args.router_only:
+        print(json.dumps({"workload": "on-device router, 8 token rows, 256 experts, hidden 4096, bf16",
+                          **router_leg(torch, rt, P, WL, calls=args.steps)}), flush=True)
+        rt.close()
+        return
     log("synthesising the 256-expert bank (6.4 GB) on the device")
     bank = WL.synth_bank(rt, 256, seed=WL.SEED_BASE + 2)
     if args.prefill_only:
@@ -279,8 +385,10 @@ def main():
                         "GB/s": round(float(np.mean([b for _, b in s1])) / (ms1 * 1e-3) / 1e9, 1)}
         for zipf in (False, True):
             extras["prefill_t2048" + ("_zipf" if zipf else "")] = prefill_leg(torch, rt, bank, P, WL, zipf)
+        extras["router_w8"] = router_leg(torch, rt, P, WL)
+        extras.update(projection_legs(torch, rt, bank, P, WL))
         for k, v in extras.items():
-            if isinstance(v, dict) and "layer_us" in v:
+            if isinstance(v, dict) and k != "kernels_us":
                 log(f"{k}: {v}")
 
     cpu = None

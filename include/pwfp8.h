@@ -244,9 +244,12 @@ int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_
  * (pytorch_noaux_routes, :4394-4473). Writes route_ids / route_weights [rows x 8] (16-byte
  * aligned; the pw_moe_layer_device / pw_moe_prefill_device inputs), scores [rows x experts] when
  * not NULL, and adds the number of boundary-tie rows to *tie_rows (a device counter) when not
- * NULL. Logits sum in a fixed order: 64 lanes of fused multiply-adds over columns l, l + 64, ...,
- * then a halving tree. An invalid row raises PW_FLAG_ROUTE and gets expert ids = experts (the
- * layer schedule rejects them). rows 1..4096, experts 9..1024. Asynchronous on stream. */
+ * NULL. hidden is a multiple of 8 (at most 65536); x and router_weight are 16-byte aligned.
+ * Logits sum in a fixed order: 256 partial sums of fused multiply-adds, partial g over the 8-column
+ * groups starting at 8g, 8g + 2048, ..., each 64 of them reduced by a halving tree, the four wave
+ * sums added as (w0 + w1) + (w2 + w3). An invalid row raises PW_FLAG_ROUTE and gets expert ids =
+ * experts (the layer schedule rejects them). rows 1..4096, experts 9..1024. Asynchronous on
+ * stream. */
 int pw_route_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows, uint32_t hidden,
                     const void *router_weight, uint32_t w_dtype, uint32_t experts, const float *bias,
                     uint32_t *route_ids, float *route_weights, float *scores, uint32_t *tie_rows, void *stream);

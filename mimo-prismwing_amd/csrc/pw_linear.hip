@@ -63,7 +63,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
                 const uint32_t col = (b << 7) + half * 64 + q * 16;
                 uint4 wv = make_uint4(0, 0, 0, 0);
                 if (row_ok)
-                    wv = load_stream16(wrow + col);
+                    wv = load_global16(wrow + col);
                 const bf16x8 a0 = fp8x8_to_bf16x8(wv.x, wv.y);
                 const bf16x8 a1 = fp8x8_to_bf16x8(wv.z, wv.w);
 #pragma unroll
@@ -157,8 +157,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_b_kernel(
             const uint32_t col = (b << 7) + q * 32;
             uint4 w0 = make_uint4(0, 0, 0, 0), w1 = w0;
             if (row_ok) {
-                w0 = load_stream16(wrow + col);
-                w1 = load_stream16(wrow + col + 16);
+                w0 = load_global16(wrow + col);
+                w1 = load_global16(wrow + col + 16);
             }
             const i32x8 wa = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
                               (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};

@@ -27,6 +27,70 @@ namespace pw {
 // weight)]>, src/text_endpoint.rs:4767-4775). Counts and offsets come from block-wide scans; a
 // per-(expert, 32-row word) prefix of the counts (when it fits in LDS) makes each rank O(1).
 // Token rows are handled one per thread: their eight ids and weights are read once.
+struct RouteRow {
+    uint32_t e[8];
+    float w[8];
+};
+
+__device__ __forceinline__ RouteRow load_route_row(const uint32_t *ids, const float *weights, uint32_t p)
+{
+    const uint4 i0 = *(const uint4 *)(ids + (size_t)p * 8), i1 = *(const uint4 *)(ids + (size_t)p * 8 + 4);
+    const float4 w0 = *(const float4 *)(weights + (size_t)p * 8), w1 = *(const float4 *)(weights + (size_t)p * 8 + 4);
+    return RouteRow{{i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w}, {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w}};
+}
+
+// Sets row p's bit in the mask word of each of its experts; true when a route is invalid (an id
+// out of range, a non-finite weight, the same expert twice in one token's routes).
+__device__ __forceinline__ bool mark_route_row(const RouteRow &rr, uint32_t p, uint32_t E, uint32_t words,
+                                               uint32_t *mask)
+{
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t e = rr.e[j];
+        if (e >= E || !finite_f32(rr.w[j])) {
+            bad = true;
+            continue;
+        }
+        const uint32_t old = atomicOr(&mask[e * words + (p >> 5)], 1u << (p & 31));
+        bad |= (old & (1u << (p & 31))) != 0;
+    }
+    return bad;
+}
+
+// Row p's placements: slot = expert offset + rank of p among the expert's rows.
+__device__ __forceinline__ void place_route_row(const RouteRow &rr, uint32_t p, uint32_t E, uint32_t words,
+                                                uint32_t P, uint32_t with_prefix, const uint32_t *mask,
+                                                const uint16_t *pref, const uint32_t *offset,
+                                                uint32_t *placement_pos, float *placement_w, uint32_t *row_slots)
+{
+    const uint32_t wd = p >> 5, below = (1u << (p & 31)) - 1u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t ei = rr.e[j];
+        if (ei >= E || !finite_f32(rr.w[j]))
+            continue;
+        uint32_t rank = __popc(mask[ei * words + wd] & below);
+        if (with_prefix) {
+            rank += pref[ei * words + wd];
+        } else {
+            for (uint32_t w = 0; w < wd; ++w)
+                rank += __popc(mask[ei * words + w]);
+        }
+        const uint32_t slot = offset[ei] + rank;
+        if (slot >= P)
+            continue;  // only when the routes were rejected
+        placement_pos[slot] = p;
+        placement_w[slot] = rr.w[j];
+        // position of this placement among its token's eight, ordered by expert id
+        uint32_t before = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            before += rr.e[k] < ei ? 1u : 0u;
+        row_slots[(size_t)p * 8 + (before & 7)] = slot;
+    }
+}
+
 __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids,
     const float *__restrict__ weights, uint32_t rows, uint32_t E, uint32_t max_active, uint32_t with_prefix,
@@ -42,6 +106,15 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     __shared__ uint32_t s_bad, s_max, s_scan[48];
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t P = rows * 8;
+    // the loads every later phase waits on go out first: this thread's token row (kept in
+    // registers when every row has its own thread) and its expert's weight pointers
+    const bool one_pass = rows <= nthr;
+    RouteRow mine{};
+    if (one_pass && tid < rows)
+        mine = load_route_row(ids, weights, tid);
+    ExpertPtrs my_ep{};
+    if (tid < E)
+        my_ep = bank[tid];
     if (tid == 0) {
         s_bad = 0;
         s_max = 0;
@@ -49,25 +122,16 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     for (uint32_t i = tid; i < E * words; i += nthr)
         mask[i] = 0;
     __syncthreads();
-    for (uint32_t p = tid; p < rows; p += nthr) {
-        const uint4 i0 = *(const uint4 *)(ids + (size_t)p * 8), i1 = *(const uint4 *)(ids + (size_t)p * 8 + 4);
-        const float4 w0 = *(const float4 *)(weights + (size_t)p * 8), w1 = *(const float4 *)(weights + (size_t)p * 8 + 4);
-        const uint32_t e8[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
-        const float wt8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        bool bad = false;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t e = e8[j];
-            if (e >= E || !finite_f32(wt8[j])) {
-                bad = true;
-                continue;
-            }
-            const uint32_t old = atomicOr(&mask[e * words + (p >> 5)], 1u << (p & 31));
-            bad |= (old & (1u << (p & 31))) != 0;  // the same expert twice in one token's routes
-        }
-        if (bad)
-            atomicOr(&s_bad, 1u);
+    bool bad = false;
+    if (one_pass) {
+        if (tid < rows)
+            bad = mark_route_row(mine, tid, E, words, mask);
+    } else {
+        for (uint32_t p = tid; p < rows; p += nthr)
+            bad |= mark_route_row(load_route_row(ids, weights, p), p, E, words, mask);
     }
+    if (bad)
+        atomicOr(&s_bad, 1u);
     __syncthreads();
     // thread e: expert e's count, its slot offset and its index among the routed experts
     const uint32_t e = tid;
@@ -87,7 +151,7 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
             active_expert[act] = e;
             active_offset[act] = off;
             ActiveExpert ae{};
-            ae.ep = bank[e];
+            ae.ep = my_ep;
             ae.off = off;
             ae.cnt = c;
             uint32_t k = 0;  // token rows of the first 16 slots, ascending
@@ -116,36 +180,14 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
             row_slots[i] = 0;
         }
     __syncthreads();
-    for (uint32_t p = tid; p < rows; p += nthr) {
-        const uint4 i0 = *(const uint4 *)(ids + (size_t)p * 8), i1 = *(const uint4 *)(ids + (size_t)p * 8 + 4);
-        const float4 w0 = *(const float4 *)(weights + (size_t)p * 8), w1 = *(const float4 *)(weights + (size_t)p * 8 + 4);
-        const uint32_t e8[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
-        const float wt8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        const uint32_t wd = p >> 5, below = (1u << (p & 31)) - 1u;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t ei = e8[j];
-            if (ei >= E || !finite_f32(wt8[j]))
-                continue;
-            uint32_t rank = __popc(mask[ei * words + wd] & below);
-            if (with_prefix) {
-                rank += pref[ei * words + wd];
-            } else {
-                for (uint32_t w = 0; w < wd; ++w)
-                    rank += __popc(mask[ei * words + w]);
-            }
-            const uint32_t slot = offset[ei] + rank;
-            if (slot >= P)
-                continue;  // only when the routes were rejected above
-            placement_pos[slot] = p;
-            placement_w[slot] = wt8[j];
-            // position of this placement among its token's eight, ordered by expert id
-            uint32_t before = 0;
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                before += e8[k] < ei ? 1u : 0u;
-            row_slots[(size_t)p * 8 + (before & 7)] = slot;
-        }
+    if (one_pass) {
+        if (tid < rows)
+            place_route_row(mine, tid, E, words, P, with_prefix, mask, pref, offset, placement_pos, placement_w,
+                            row_slots);
+    } else {
+        for (uint32_t p = tid; p < rows; p += nthr)
+            place_route_row(load_route_row(ids, weights, p), p, E, words, P, with_prefix, mask, pref, offset,
+                            placement_pos, placement_w, row_slots);
     }
     if (tid == 0) {
         plan->n_active = n_active;
@@ -251,10 +293,10 @@ __global__ __launch_bounds__(64 * KSPLIT) void moe_b_gateup_kernel(
     const uint32_t b_begin = wave * blocks / KSPLIT, b_end = (wave + 1) * blocks / KSPLIT;
     for (uint32_t b = b_begin; b < b_end; ++b) {
         const uint32_t col = (b << 7) + q * 32;
-        const uint4 g0 = load_stream16(grow + col);
-        const uint4 g1 = load_stream16(grow + col + 16);
-        const uint4 u0 = load_stream16(urow + col);
-        const uint4 u1 = load_stream16(urow + col + 16);
+        const uint4 g0 = load_global16(grow + col);
+        const uint4 g1 = load_global16(grow + col + 16);
+        const uint4 u0 = load_global16(urow + col);
+        const uint4 u1 = load_global16(urow + col + 16);
         const i32x8 ga = {(int)g0.x, (int)g0.y, (int)g0.z, (int)g0.w, (int)g1.x, (int)g1.y, (int)g1.z, (int)g1.w};
         const i32x8 ua = {(int)u0.x, (int)u0.y, (int)u0.z, (int)u0.w, (int)u1.x, (int)u1.y, (int)u1.z, (int)u1.w};
         const float sg = gs[b], su = us[b];
@@ -339,8 +381,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void moe_b_down_kernel(
     const uint32_t b_begin = wave * blocks / KSPLIT, b_end = (wave + 1) * blocks / KSPLIT;
     for (uint32_t b = b_begin; b < b_end; ++b) {
         const uint32_t col = (b << 7) + q * 32;
-        const uint4 d0 = load_stream16(drow + col);
-        const uint4 d1 = load_stream16(drow + col + 16);
+        const uint4 d0 = load_global16(drow + col);
+        const uint4 d1 = load_global16(drow + col + 16);
         const i32x8 da = {(int)d0.x, (int)d0.y, (int)d0.z, (int)d0.w, (int)d1.x, (int)d1.y, (int)d1.z, (int)d1.w};
         const float sd = ds[b];
 #pragma unroll
@@ -393,8 +435,9 @@ __device__ __forceinline__ float4 split_sum4(const float *p, uint32_t ks, size_t
     return v;
 }
 
+template <int KS>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const float *__restrict__ y, uint32_t ks, size_t split_stride, const float *__restrict__ placement_w,
+    const float *__restrict__ y, uint32_t ks_rt, size_t split_stride, const float *__restrict__ placement_w,
     const uint32_t *__restrict__ row_slots, uint32_t rows, uint32_t H, float *__restrict__ out_f32,
     uint16_t *__restrict__ out_bf16, uint32_t raw, uint32_t *flags)
 {
@@ -403,17 +446,46 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     if (idx >= rows * per_row)
         return;
     const uint32_t row = idx / per_row, c4 = idx % per_row;
+    const uint4 s0 = *(const uint4 *)(row_slots + row * 8), s1 = *(const uint4 *)(row_slots + row * 8 + 4);
+    uint32_t slot[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float w[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        slot[j] = slot[j] < rows * 8 ? slot[j] : 0;
+        w[j] = placement_w[slot[j]];
+    }
+    float4 v[8];
+    if constexpr (KS > 0) {
+        // every split partial of the eight slots in flight at once, summed in split order
+        float4 part[8][KS];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+                part[j][s] = *(const float4 *)(y + (size_t)s * split_stride + (size_t)slot[j] * H + c4 * 4);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            v[j] = part[j][0];
+#pragma unroll
+            for (int s = 1; s < KS; ++s) {
+                v[j].x += part[j][s].x;
+                v[j].y += part[j][s].y;
+                v[j].z += part[j][s].z;
+                v[j].w += part[j][s].w;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            v[j] = split_sum4(y + (size_t)slot[j] * H + c4 * 4, ks_rt, split_stride);
+    }
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        uint32_t slot = row_slots[row * 8 + j];
-        slot = slot < rows * 8 ? slot : 0;
-        const float w = placement_w[slot];
-        const float4 v = split_sum4(y + (size_t)slot * H + c4 * 4, ks, split_stride);
-        acc[0] = __fadd_rn(acc[0], __fmul_rn(v.x, w));
-        acc[1] = __fadd_rn(acc[1], __fmul_rn(v.y, w));
-        acc[2] = __fadd_rn(acc[2], __fmul_rn(v.z, w));
-        acc[3] = __fadd_rn(acc[3], __fmul_rn(v.w, w));
+        acc[0] = __fadd_rn(acc[0], __fmul_rn(v[j].x, w[j]));
+        acc[1] = __fadd_rn(acc[1], __fmul_rn(v[j].y, w[j]));
+        acc[2] = __fadd_rn(acc[2], __fmul_rn(v[j].z, w[j]));
+        acc[3] = __fadd_rn(acc[3], __fmul_rn(v[j].w, w[j]));
     }
     bool bad = false;
     const size_t at = (size_t)row * H + c4 * 4;
@@ -592,9 +664,16 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
         launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, max_active, max_count, H, I, flags, stream);
     const uint32_t n4 = rows * (H >> 2);
     const int t = timer_begin(K_MOE_COMBINE, stream);
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((n4 + 255) / 256), dim3(256), 0, stream, eo.y, eo.ks,
-                       eo.stride, mb.placement_w, mb.row_slots, rows, H, out_f32, out_bf16, raw ? 1u : 0u,
-                       flags);
+#define PW_COMBINE(KS)                                                                                         \
+    hipLaunchKernelGGL((moe_combine_kernel<KS>), dim3((n4 + 255) / 256), dim3(256), 0, stream, eo.y, eo.ks, \
+                       eo.stride, mb.placement_w, mb.row_slots, rows, H, out_f32, out_bf16, raw ? 1u : 0u, flags)
+    switch (eo.ks) {
+    case 1: PW_COMBINE(1); break;
+    case 2: PW_COMBINE(2); break;
+    case 4: PW_COMBINE(4); break;
+    default: PW_COMBINE(0); break;
+    }
+#undef PW_COMBINE
     timer_end(t, stream);
 }
 

@@ -10,7 +10,7 @@
 // waves reads each of its 64 rows x KC bytes exactly once. The expert's routed activation rows for
 // the K split go straight from global memory into LDS (global_load_lds, padded rows so the later
 // 16-byte reads are conflict-free) and are shared by the four waves; then every lane issues all of
-// its weight loads (16 bytes per instruction, one weight row per lane, nontemporal), at most eight
+// its weight loads (16 bytes per instruction, one weight row per lane, plain loads), at most eight
 // 128-column blocks per lane, so a wave keeps 16 KB in flight on 64 VGPRs and several waves fit
 // on each SIMD. e4m3 -> bf16 is exact (v_cvt_scalef32_pk_bf16_fp8); activations are bf16 planes
 // (f32 values arrive as three exact planes), so v_mfma_f32_16x16x32_bf16 forms exact products and
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
         for (int j = 0; j < BPW; ++j)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                wv[m][j][h] = load_stream16(wrow + j * 128 + h * 64);
+                wv[m][j][h] = load_global16(wrow + j * 128 + h * 64);
     }
     // block scales of this wave's 16 rows (one 128-row scale block, wave-uniform)
     const uint32_t blocks = K >> 7;
@@ -197,8 +197,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
 
 // Gate/up split sums (in split order 0..KS-1) -> h = (g / (1 + e^-g)) * u in f32 (swiglu_f32,
 // kernels/block_fp8_gemv.metal:241-252; CPU src/lib.rs:5840-5844), written as three exact bf16
-// planes for the down projection's MFMA. One thread per (slot, 4 rows).
-__global__ __launch_bounds__(256) void moe_a_swiglu_kernel(const float *__restrict__ partial, uint32_t KS,
+// planes for the down projection's MFMA. One thread per (slot, 4 rows). With KS known at compile
+// time every partial load is issued before the first add (one memory round trip); KS = 0 is the
+// generic loop.
+template <int KS>
+__global__ __launch_bounds__(256) void moe_a_swiglu_kernel(const float *__restrict__ partial, uint32_t ks_rt,
                                                            uint32_t P, uint32_t R, uint16_t *__restrict__ hidden,
                                                            uint32_t *flags)
 {
@@ -208,17 +211,38 @@ __global__ __launch_bounds__(256) void moe_a_swiglu_kernel(const float *__restri
         return;
     const uint32_t slot = idx / per_slot, row4 = (idx - slot * per_slot) * 4;
     float v[2][4];
+    if constexpr (KS > 0) {
+        float4 part[2][KS];
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-        float4 sum = *(const float4 *)(partial + ((size_t)m * P + slot) * R + row4);
-        for (uint32_t sp = 1; sp < KS; ++sp) {
-            const float4 o = *(const float4 *)(partial + (((size_t)sp * 2 + m) * P + slot) * R + row4);
-            sum.x += o.x;
-            sum.y += o.y;
-            sum.z += o.z;
-            sum.w += o.w;
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int sp = 0; sp < KS; ++sp)
+                part[m][sp] = *(const float4 *)(partial + (((size_t)sp * 2 + m) * P + slot) * R + row4);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            float4 sum = part[m][0];
+#pragma unroll
+            for (int sp = 1; sp < KS; ++sp) {
+                sum.x += part[m][sp].x;
+                sum.y += part[m][sp].y;
+                sum.z += part[m][sp].z;
+                sum.w += part[m][sp].w;
+            }
+            v[m][0] = sum.x; v[m][1] = sum.y; v[m][2] = sum.z; v[m][3] = sum.w;
         }
-        v[m][0] = sum.x; v[m][1] = sum.y; v[m][2] = sum.z; v[m][3] = sum.w;
+    } else {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            float4 sum = *(const float4 *)(partial + ((size_t)m * P + slot) * R + row4);
+            for (uint32_t sp = 1; sp < ks_rt; ++sp) {
+                const float4 o = *(const float4 *)(partial + (((size_t)sp * 2 + m) * P + slot) * R + row4);
+                sum.x += o.x;
+                sum.y += o.y;
+                sum.z += o.z;
+                sum.w += o.w;
+            }
+            v[m][0] = sum.x; v[m][1] = sum.y; v[m][2] = sum.z; v[m][3] = sum.w;
+        }
     }
     uint16_t hp[3][4];
     bool bad = false;
@@ -243,8 +267,17 @@ void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t
                          uint32_t *flags, hipStream_t stream)
 {
     const uint32_t n = P * (I >> 2);
-    hipLaunchKernelGGL(moe_a_swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, partial, ks, P, I,
-                       hidden_planes, flags);
+    const dim3 grid((n + 255) / 256), block(256);
+#define PW_SWIGLU(KS) hipLaunchKernelGGL((moe_a_swiglu_kernel<KS>), grid, block, 0, stream, partial, ks, P, I, \
+                                         hidden_planes, flags)
+    switch (ks) {
+    case 1: PW_SWIGLU(1); break;
+    case 2: PW_SWIGLU(2); break;
+    case 4: PW_SWIGLU(4); break;
+    case 8: PW_SWIGLU(8); break;
+    default: PW_SWIGLU(0); break;
+    }
+#undef PW_SWIGLU
 }
 
 // LDS bytes of a split: NS planes x cnt rows x (KC/8 + 1) 16-byte units.

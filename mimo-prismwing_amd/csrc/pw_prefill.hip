@@ -95,8 +95,8 @@ struct PfC {
 
 __device__ __forceinline__ void pf_issue_w(PfW &w, const uint8_t *wrow, uint32_t k0)
 {
-    w.v[0] = load_stream16(wrow + k0);
-    w.v[1] = load_stream16(wrow + k0 + 64);
+    w.v[0] = load_global16(wrow + k0);
+    w.v[1] = load_global16(wrow + k0 + 64);
 }
 
 __device__ __forceinline__ void pf_issue_c(PfC &c, const uint8_t *const *csrc, uint32_t k0)

@@ -985,6 +985,10 @@ int pw_route_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t ro
         return fail(PW_ERR_ARGUMENT, "unknown dtype");
     if (rows < 1 || rows > 4096 || hidden == 0 || experts <= 8 || experts > 1024)
         return fail(PW_ERR_ARGUMENT, "router needs 1..4096 rows, a hidden size and 9..1024 experts");
+    // rows are read as 8-column groups with 16-byte loads
+    if (hidden % 8 || hidden > 65536 || (((uintptr_t)x | (uintptr_t)router_weight) & 15))
+        return fail(PW_ERR_ARGUMENT, "router hidden size must be a multiple of 8 (at most 65536) with 16-byte "
+                                     "aligned activations and router weights");
     if (((uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
         return fail(PW_ERR_ARGUMENT, "route buffers must be 16-byte aligned");
     PW_HIP(set_device(rt));

@@ -70,27 +70,72 @@ PW_HD void topk_select_sort(TopkEntry *first, TopkEntry *last)
     }
 }
 
+// The ranges of at most 7 elements nth_element finishes directly; returns false for longer ones.
+PW_HD bool topk_small(TopkEntry *first, TopkEntry *last)
+{
+    const long len = (long)(last - first);
+    if (len <= 1)
+        return true;
+    if (len == 2) {
+        if (topk_greater(last[-1], *first))
+            topk_swap(*first, last[-1]);
+        return true;
+    }
+    if (len == 3) {
+        topk_sort3(first, first + 1, last - 1);
+        return true;
+    }
+    if (len <= 7) {
+        topk_select_sort(first, last);
+        return true;
+    }
+    return false;
+}
+
+// The partition nth_element falls back to when no element of (first, last - 1) is greater than the
+// pivot and *first equals it: partitions around *first. Returns true when nth is placed; otherwise
+// *next is the new start of the range.
+PW_HD bool topk_fallback_partition(TopkEntry *first, TopkEntry *nth, TopkEntry *last, TopkEntry **next)
+{
+    TopkEntry *i = first + 1, *j = last;
+    if (!topk_greater(*first, *--j)) {
+        for (;; ++i) {
+            if (i == j)
+                return true;
+            if (topk_greater(*first, *i)) {
+                topk_swap(*i, *j);
+                ++i;
+                break;
+            }
+        }
+    }
+    if (i == j)
+        return true;
+    for (;;) {
+        while (!topk_greater(*first, *i))
+            ++i;
+        do
+            --j;
+        while (topk_greater(*first, *j));
+        if (i >= j)
+            break;
+        topk_swap(*i, *j);
+        ++i;
+    }
+    if (nth < i)
+        return true;
+    *next = i;
+    return false;
+}
+
 PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
 {
     for (;;) {
         if (nth == last)
             return;
+        if (topk_small(first, last))
+            return;
         const long len = (long)(last - first);
-        if (len <= 1)
-            return;
-        if (len == 2) {
-            if (topk_greater(last[-1], *first))
-                topk_swap(*first, last[-1]);
-            return;
-        }
-        if (len == 3) {
-            topk_sort3(first, first + 1, last - 1);
-            return;
-        }
-        if (len <= 7) {
-            topk_select_sort(first, last);
-            return;
-        }
         TopkEntry *m = first + len / 2, *lm1 = last - 1;
         unsigned swaps = topk_sort3(first, m, lm1);
         TopkEntry *i = first, *j = lm1;
@@ -106,37 +151,10 @@ PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
                 topk_swap(*i, *j);
                 ++swaps;
             } else {
-                ++i;
-                j = last;
-                if (!topk_greater(*first, *--j)) {
-                    for (;; ++i) {
-                        if (i == j)
-                            return;
-                        if (topk_greater(*first, *i)) {
-                            topk_swap(*i, *j);
-                            ++swaps;
-                            ++i;
-                            break;
-                        }
-                    }
-                }
-                if (i == j)
+                TopkEntry *next;
+                if (topk_fallback_partition(first, nth, last, &next))
                     return;
-                for (;;) {
-                    while (!topk_greater(*first, *i))
-                        ++i;
-                    do
-                        --j;
-                    while (topk_greater(*first, *j));
-                    if (i >= j)
-                        break;
-                    topk_swap(*i, *j);
-                    ++swaps;
-                    ++i;
-                }
-                if (nth < i)
-                    return;
-                first = i;
+                first = next;
                 continue;
             }
         }
@@ -186,21 +204,13 @@ PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
 // Outcome of one routed row.
 enum RouteStatus : int { ROUTE_OK = 0, ROUTE_NONFINITE = 1, ROUTE_TOPK = 2, ROUTE_WEIGHTS = 3 };
 
-// One row of pytorch_noaux_routes: scores [experts] (sigmoid outputs), bias [experts] ->
-// selected[8], weights[8]; *tie = the boundary value equals the best rejected value. `scratch`
-// holds `experts` entries. Returns a RouteStatus.
-PW_HD int noaux_route_row(const float *scores, const float *bias, uint32_t experts, TopkEntry *scratch,
-                                 uint32_t *selected, float *weights, bool *tie)
+// The end of one row after the top-k partition: scratch[0..8) holds the selected (corrected, id)
+// entries in partition order and `rejected` is the largest corrected value of the rest. Checks the
+// boundary (equality counts as a tie) and writes selected[8], weights[8].
+PW_HD int noaux_finish_row(const float *scores, const TopkEntry *scratch, float rejected, uint32_t *selected,
+                           float *weights, bool *tie)
 {
     constexpr uint32_t K = 8;
-    *tie = false;
-    for (uint32_t e = 0; e < experts; ++e) {
-        if (!finite_f32_bits(scores[e]) || !finite_f32_bits(bias[e]))
-            return ROUTE_NONFINITE;
-        scratch[e].v = scores[e] + bias[e];
-        scratch[e].i = (int32_t)e;
-    }
-    nth_element_libcxx(scratch, scratch + K - 1, scratch + experts);
     uint32_t sel[K];
     for (uint32_t k = 0; k < K; ++k) {
         sel[k] = (uint32_t)scratch[k].i;
@@ -208,13 +218,9 @@ PW_HD int noaux_route_row(const float *scores, const float *bias, uint32_t exper
             if (sel[j] == sel[k])
                 return ROUTE_TOPK;
     }
-    // boundary check against the best rejected value
     float boundary = scratch[0].v;
     for (uint32_t k = 1; k < K; ++k)
         boundary = scratch[k].v < boundary ? scratch[k].v : boundary;
-    float rejected = -__builtin_inff();
-    for (uint32_t k = K; k < experts; ++k)
-        rejected = scratch[k].v > rejected ? scratch[k].v : rejected;
     if (!finite_f32_bits(boundary) || boundary < rejected)
         return ROUTE_TOPK;
     *tie = boundary == rejected;
@@ -239,6 +245,26 @@ PW_HD int noaux_route_row(const float *scores, const float *bias, uint32_t exper
     if ((dev < 0.0f ? -dev : dev) > 1.0e-6f)
         return ROUTE_WEIGHTS;
     return ROUTE_OK;
+}
+
+// One row of pytorch_noaux_routes: scores [experts] (sigmoid outputs), bias [experts] ->
+// selected[8], weights[8]; *tie = the boundary value equals the best rejected value. `scratch`
+// holds `experts` entries. Returns a RouteStatus.
+PW_HD int noaux_route_row(const float *scores, const float *bias, uint32_t experts, TopkEntry *scratch,
+                          uint32_t *selected, float *weights, bool *tie)
+{
+    *tie = false;
+    for (uint32_t e = 0; e < experts; ++e) {
+        if (!finite_f32_bits(scores[e]) || !finite_f32_bits(bias[e]))
+            return ROUTE_NONFINITE;
+        scratch[e].v = scores[e] + bias[e];
+        scratch[e].i = (int32_t)e;
+    }
+    nth_element_libcxx(scratch, scratch + 7, scratch + experts);
+    float rejected = -__builtin_inff();
+    for (uint32_t k = 8; k < experts; ++k)
+        rejected = scratch[k].v > rejected ? scratch[k].v : rejected;
+    return noaux_finish_row(scores, scratch, rejected, selected, weights, tie);
 }
 
 }  // namespace pw

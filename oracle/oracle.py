@@ -60,8 +60,8 @@ def lib():
         L.pwo_swiglu_bf16_staged.restype = None
         L.pwo_topk_unsorted.argtypes = [_f32p, _sz, _sz, _u32p]
         L.pwo_noaux_routes.argtypes = [_f32p, _f32p, _sz, _sz, _u32p, _f32p, _u64p]
-        L.pwo_router_logits_lane64.argtypes = [_f32p, _sz, _f32p, _sz, _sz, _f32p]
-        L.pwo_router_logits_lane64.restype = None
+        L.pwo_router_logits_t256.argtypes = [_f32p, _sz, _f32p, _sz, _sz, _f32p]
+        L.pwo_router_logits_t256.restype = None
         L.pwo_route.argtypes = [_f32p, _sz, _f32p, _f32p, _sz, _sz, _f32p, _f32p, _u32p, _f32p, _u64p]
         for name in ("pwo_moe_layer_mode_a", "pwo_moe_layer_mode_b"):
             getattr(L, name).argtypes = [_f32p, _sz, _sz, _sz, ctypes.POINTER(PwoExpert), _sz,
@@ -183,10 +183,10 @@ def noaux_routes(scores, bias):
     return sel, w, ties.value
 
 
-def router_logits_lane64(x, router_w):
+def router_logits_t256(x, router_w):
     x = _c(np.atleast_2d(x), np.float32); r = _c(router_w, np.float32)
     out = np.zeros((x.shape[0], r.shape[0]), np.float32)
-    lib().pwo_router_logits_lane64(_p(x, _f32p), x.shape[0], _p(r, _f32p), r.shape[0], r.shape[1], _p(out, _f32p))
+    lib().pwo_router_logits_t256(_p(x, _f32p), x.shape[0], _p(r, _f32p), r.shape[0], r.shape[1], _p(out, _f32p))
     return out
 
 

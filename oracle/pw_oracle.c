@@ -570,22 +570,28 @@ int pwo_noaux_routes(const float *scores, const float *bias, size_t rows, size_t
     return status;
 }
 
-void pwo_router_logits_lane64(const float *x, size_t rows, const float *router_w, size_t experts,
-                              size_t k, float *logits)
+void pwo_router_logits_t256(const float *x, size_t rows, const float *router_w, size_t experts,
+                            size_t k, float *logits)
 {
     for (size_t p = 0; p < rows; ++p) {
         for (size_t e = 0; e < experts; ++e) {
-            float partial[64];
-            for (size_t l = 0; l < 64; ++l) {
+            float partial[256];
+            for (size_t g = 0; g < 256; ++g) {
                 float acc = 0.0f;
-                for (size_t c = l; c < k; c += 64)
-                    acc = fmaf(x[p * k + c], router_w[e * k + c], acc);
-                partial[l] = acc;
+                for (size_t c0 = 8 * g; c0 < k; c0 += 2048)
+                    for (size_t j = 0; j < 8; ++j)
+                        acc = fmaf(x[p * k + c0 + j], router_w[e * k + c0 + j], acc);
+                partial[g] = acc;
             }
-            for (size_t offset = 32; offset > 0; offset /= 2)
-                for (size_t l = 0; l < offset; ++l)
-                    partial[l] = partial[l] + partial[l + offset];
-            logits[p * experts + e] = partial[0];
+            float wave[4];
+            for (size_t w = 0; w < 4; ++w) {
+                float *lane = partial + 64 * w;
+                for (size_t offset = 32; offset > 0; offset /= 2)
+                    for (size_t l = 0; l < offset; ++l)
+                        lane[l] = lane[l] + lane[l + offset];
+                wave[w] = lane[0];
+            }
+            logits[p * experts + e] = (wave[0] + wave[1]) + (wave[2] + wave[3]);
         }
     }
 }
@@ -595,7 +601,7 @@ int pwo_route(const float *x, size_t rows, const float *router_w, const float *b
               size_t experts, size_t k, float *logits, float *scores, uint32_t *selected,
               float *weights, uint64_t *tie_rows)
 {
-    pwo_router_logits_lane64(x, rows, router_w, experts, k, logits);
+    pwo_router_logits_t256(x, rows, router_w, experts, k, logits);
     for (size_t i = 0; i < rows * experts; ++i)
         scores[i] = pwo_sigmoid_f32(logits[i]);
     return pwo_noaux_routes(scores, bias, rows, experts, selected, weights, tie_rows);

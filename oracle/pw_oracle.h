@@ -23,8 +23,10 @@
  *   pwo_sigmoid_f32          golden pw0062-router-sigmoid.json, pw0068
  *   pwo_topk_unsorted        golden pw0063-topk-order.json + 5 tie cases of pw0157 (order and set)
  *   pwo_noaux_routes         pw0157 tie counting; weights sum to 1 within 1e-6; tiny-MoE fixture set
- *   pwo_router_logits_lane64 f64 brute force (tolerance) — summation order is this build's declared
- *                            order; the reference's (Apple Accelerate SGEMM) is unknowable
+ *   pwo_router_logits_t256   known-answer sums whose f32 value fixes the fma, the column order, the
+ *                            lane tree and the wave order; f64 brute force (tolerance). The order is
+ *                            this build's declared one; the reference's (Apple Accelerate SGEMM) is
+ *                            closed
  *   pwo_moe_layer_mode_a/_b  schedule bijection + exact reconstruction with one-hot weights; f64
  *                            brute force on tiny shapes; moe-noaux-tc-swiglu.json structure
  *   pwo_full/swa_qkv_*       known-answer row/scale maps of src/text_endpoint.rs:13686-13732
@@ -78,10 +80,12 @@ int pwo_topk_unsorted(const float *values, size_t count, size_t top_k, uint32_t 
  * weights [rows x 8]; *tie_rows counts rows whose selected boundary equals the best rejected. */
 int pwo_noaux_routes(const float *scores, const float *bias, size_t rows, size_t experts,
                      uint32_t *selected, float *weights, uint64_t *tie_rows);
-/* Router logits in the declared lane-64 order: for each (p, e) 64 partial sums, partial l
- * accumulating k = l, l+64, ... with fmaf, then the halving tree 32,16,8,4,2,1. */
-void pwo_router_logits_lane64(const float *x, size_t rows, const float *router_w, size_t experts,
-                              size_t k, float *logits);
+/* Router logits in the declared 256-thread order (k a multiple of 8): for each (p, e) 256 partial
+ * sums, partial g accumulating with fmaf over the 8-column groups c0 = 8g, 8g + 2048, ... (columns
+ * c0 .. c0 + 7 in order); each 64-partial wave reduced by the halving tree 32,16,8,4,2,1 into
+ * w0..w3; logit = (w0 + w1) + (w2 + w3). */
+void pwo_router_logits_t256(const float *x, size_t rows, const float *router_w, size_t experts,
+                            size_t k, float *logits);
 /* Full route: logits (lane-64) -> sigmoid -> noaux routes. */
 int pwo_route(const float *x, size_t rows, const float *router_w, const float *bias,
               size_t experts, size_t k, float *logits, float *scores, uint32_t *selected,

@@ -2,8 +2,10 @@
 
 Routes are integer work and must match the C oracle bit for bit: selected expert ids in libc++
 nth_element order, renormalised weights, sigmoid scores and tie counts. The oracle's logits use the
-same declared summation order (64 lanes of fused multiply-adds, then a halving tree), and its
-top-k order is pinned by the reference's golden orders (pw0063, pw0157).
+same declared summation order (256 partial fused multiply-add sums over 8-column groups, halving
+trees per wave, then (w0 + w1) + (w2 + w3)), and its top-k order is pinned by the reference's
+golden orders (pw0063, pw0157). The device splits nth_element's partitions across a wave; the
+pattern tests drive its guard, fallback and already-sorted branches.
 """
 import numpy as np
 import pytest
@@ -84,6 +86,77 @@ def test_device_routes_with_ties(rt):
     assert np.array_equal(ids, ref_sel)
     assert np.array_equal(wts.view(np.uint32), ref_w.view(np.uint32))
     assert ties == ref_ties and ties == rows
+
+
+def _pattern(kind, experts, rng):
+    if kind == "random":
+        return rng.standard_normal(experts).astype(np.float32)
+    if kind == "levels":
+        return np.array([0.5, 0.25, -0.125, 1.0], np.float32)[rng.integers(0, 4, experts)]
+    if kind == "equal":
+        return np.full(experts, 0.75, np.float32)
+    if kind == "ascending":
+        return np.linspace(-2, 2, experts).astype(np.float32)
+    if kind == "descending":
+        return np.linspace(2, -2, experts).astype(np.float32)
+    if kind == "one_high":
+        v = np.full(experts, -1.0, np.float32)
+        v[experts // 2] = 3.0
+        return v
+    raise ValueError(kind)
+
+
+KINDS = ["random", "levels", "equal", "ascending", "descending", "one_high"]
+
+
+@pytest.mark.parametrize("experts", [9, 100, 257, 1024])
+@pytest.mark.parametrize("hidden", [8, 2056])
+def test_device_routes_patterns(rt, experts, hidden):
+    """Row r has logits = pattern r exactly (x one-hot on column r): ties everywhere, all-equal rows,
+    sorted rows, expert counts that are not multiples of the wave, hidden sizes off the 2048 stride."""
+    import torch
+    rng = np.random.default_rng(experts * 7 + hidden)
+    rows = len(KINDS)
+    x = np.zeros((rows, hidden), np.float32)
+    rw = np.zeros((experts, hidden), np.float32)
+    for r, kind in enumerate(KINDS):
+        x[r, r] = 1.0
+        rw[:, r] = _pattern(kind, experts, rng)
+    bias = np.zeros(experts, np.float32)
+    ids, wts, scores, ties, flags = _device_route(rt, torch, x, rw, bias, x_f32=True, w_f32=True)
+    assert flags == 0
+    _, ref_scores, ref_sel, ref_w, ref_ties = O.route(x, rw, bias)
+    assert np.array_equal(scores.view(np.uint32), ref_scores.view(np.uint32))
+    assert np.array_equal(ids, ref_sel)
+    assert np.array_equal(wts.view(np.uint32), ref_w.view(np.uint32))
+    assert ties == ref_ties
+
+
+def test_device_routes_many_rows_ragged(rt):
+    """1000 rows (125 row chunks), 300 experts, bf16, hidden 4104 (not a multiple of 2048)."""
+    import torch
+    rng = np.random.default_rng(21)
+    x = WL.bf16_round_np(rng.standard_normal((1000, 4104)).astype(np.float32))
+    rw = WL.bf16_round_np((rng.standard_normal((300, 4104)) * 0.02).astype(np.float32))
+    bias = rng.uniform(-0.01, 0.01, 300).astype(np.float32)
+    ids, wts, scores, ties, flags = _device_route(rt, torch, x, rw, bias)
+    assert flags == 0
+    _, ref_scores, ref_sel, ref_w, ref_ties = O.route(x, rw, bias)
+    assert np.array_equal(scores.view(np.uint32), ref_scores.view(np.uint32))
+    assert np.array_equal(ids, ref_sel)
+    assert np.array_equal(wts.view(np.uint32), ref_w.view(np.uint32))
+    assert ties == ref_ties
+
+
+def test_device_router_rejects_bad_hidden(rt):
+    import torch
+    x = torch.zeros((4, 260), dtype=torch.int16, device="cuda")
+    wt = torch.zeros((16, 260), dtype=torch.int16, device="cuda")
+    bt = torch.zeros(16, dtype=torch.float32, device="cuda")
+    ids = torch.zeros((4, 8), dtype=torch.int32, device="cuda")
+    wts = torch.zeros((4, 8), dtype=torch.float32, device="cuda")
+    with pytest.raises(P.PwError, match="ARGUMENT"):
+        rt.route_device(x, 4, 260, wt, 16, bt, ids, wts)
 
 
 def test_device_router_feeds_the_layer(rt):

@@ -329,13 +329,37 @@ def test_noaux_weights_and_rejection():
         O.noaux_routes(np.full((1, 256), np.nan, np.float32), bias)
 
 
-def test_router_logits_lane64_brute_force():
+def test_router_logits_t256_brute_force():
     rng = np.random.default_rng(4)
     x = rng.standard_normal((3, 4096)).astype(np.float32)
     r = (rng.standard_normal((16, 4096)) * 0.02).astype(np.float32)
-    got = O.router_logits_lane64(x, r)
+    got = O.router_logits_t256(x, r)
     want = x.astype(np.float64) @ r.T.astype(np.float64)
     assert np.max(np.abs(got - want)) < 1e-5
+
+
+def _one_logit(entries, k=4096):
+    """Logit of one row against one expert with x[c] = a, w[c] = b for (c, a, b) in entries."""
+    x = np.zeros((1, k), np.float32)
+    r = np.zeros((1, k), np.float32)
+    for c, a, b in entries:
+        x[0, c], r[0, c] = a, b
+    return float(O.router_logits_t256(x, r)[0, 0])
+
+
+def test_router_logits_t256_order_known_answers():
+    """Sums whose f32 value is fixed by the declared order (2^24 + 1 rounds to 2^24)."""
+    big = float(2 ** 24)
+    # fused multiply-add: -(1 + 2^-11) + (1 + 2^-12)^2 = 2^-24 exactly; a rounded product gives 0
+    assert _one_logit([(0, 1.0, -(1 + 2 ** -11)), (1, 1 + 2 ** -12, 1 + 2 ** -12)]) == 2 ** -24
+    # one thread: columns 0, 1 of the first group, then column 2048 of its next group -> 0
+    assert _one_logit([(0, 1.0, big), (1, 1.0, 1.0), (2048, 1.0, -big)]) == 0.0
+    # halving tree: threads 0 and 32 meet first, thread 1 joins at offset 1 -> 1 (a lane-serial sum gives 0)
+    assert _one_logit([(0, 1.0, big), (8, 1.0, 1.0), (256, 1.0, -big)]) == 1.0
+    # waves: (w0 + w1) + (w2 + w3) with w = 2^24, 1, 1, -2^24 -> 1 (serial 0, exact 2)
+    assert _one_logit([(0, 1.0, big), (512, 1.0, 1.0), (1024, 1.0, 1.0), (1536, 1.0, -big)]) == 1.0
+    # a hidden size that is not a multiple of 2048: thread 1's second group starts at 2056
+    assert _one_logit([(8, 1.0, big), (2056, 1.0, 1.0), (2057, 1.0, -big)], k=2064) == 0.0
 
 
 # ---------------------------------------------------------------- a12 QKV maps
