@@ -44,6 +44,25 @@ __device__ __forceinline__ void lds_load16(const void *src_lane, void *lds_wave_
                                      (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
 }
 
+// Waits until at most N vector-memory operations of this wave are outstanding (gfx9 s_waitcnt
+// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt at their no-wait maxima). Loads
+// complete in issue order, so this is "everything but the last N loads".
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt has six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier ordering LDS accesses only: outstanding global loads stay in flight across it,
+// which __syncthreads() would wait for.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Error bits raised by kernels into the runtime's device error word. The low bits keep the
 // meaning of the reference's Metal error word (kernels/block_fp8_gemv.metal, bits 1..128).
 enum : uint32_t {

@@ -101,6 +101,10 @@ SplitPlan plan_split(uint32_t K, int mats, int ns, uint32_t max_cnt);
 void launch_moe_a_split(int mats, int ns, int nt, const SplitArgs &args, const SplitPlan &sp,
                         uint32_t max_active, hipStream_t stream);
 // gate/up split sums -> SwiGLU -> hidden as three bf16 planes [3][P][I]
+// Gate/up with the SwiGLU fused and no split partials (pw_moe_a.hip), when the routed rows fit the
+// LDS stage; returns false (nothing launched) otherwise.
+bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_active, uint16_t *hidden_planes,
+                               hipStream_t stream);
 void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t I, uint16_t *hidden_planes,
                          uint32_t *flags, hipStream_t stream);
 

@@ -112,9 +112,15 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     RouteRow mine{};
     if (one_pass && tid < rows)
         mine = load_route_row(ids, weights, tid);
-    ExpertPtrs my_ep{};
-    if (tid < E)
-        my_ep = bank[tid];
+    // this thread's expert's ExpertPtrs (48 bytes) in three native vectors (a struct or array copy
+    // held across the barriers below would be kept in scratch memory)
+    u32x4 ep0 = {0u, 0u, 0u, 0u}, ep1 = ep0, ep2 = ep0;
+    if (tid < E) {
+        const u32x4 *src = (const u32x4 *)(bank + tid);
+        ep0 = src[0];
+        ep1 = src[1];
+        ep2 = src[2];
+    }
     if (tid == 0) {
         s_bad = 0;
         s_max = 0;
@@ -150,28 +156,40 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
         if (c) {
             active_expert[act] = e;
             active_offset[act] = off;
-            ActiveExpert ae{};
-            ae.ep = my_ep;
-            ae.off = off;
-            ae.cnt = c;
-            uint32_t k = 0;  // token rows of the first 16 slots, ascending
-            for (uint32_t w = 0; w < words && k < 16; ++w) {
-                uint32_t bits = mask[e * words + w];
-                while (bits && k < 16) {
-                    ae.tok[k++] = (uint16_t)(w * 32 + __builtin_ctz(bits));
-                    bits &= bits - 1;
-                }
+            // token rows of the first 16 slots, ascending, packed two per word (static indices
+            // only: a dynamically indexed register array would move to scratch memory)
+            uint32_t tw[8] = {};
+            uint32_t w = 0, bits = mask[e * words];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                while (!bits && w + 1 < words)
+                    bits = mask[e * words + ++w];
+                const uint32_t t = bits ? w * 32 + __builtin_ctz(bits) : 0u;
+                tw[k >> 1] |= t << (16 * (k & 1));
+                bits &= bits - 1;
             }
-            if (act < max_active)
-                active[act] = ae;
+            if (act < max_active) {
+                // ActiveExpert: ExpertPtrs, off, cnt, tok[16], pad[2] as six 16-byte stores
+                u32x4 *dst = (u32x4 *)(active + act);
+                dst[0] = ep0;
+                dst[1] = ep1;
+                dst[2] = ep2;
+                dst[3] = u32x4{off, c, tw[0], tw[1]};
+                dst[4] = u32x4{tw[2], tw[3], tw[4], tw[5]};
+                dst[5] = u32x4{tw[6], tw[7], 0u, 0u};
+            }
             atomicMax(&s_max, c);
         }
     }
     if (tid == 0)
         active_offset[n_active] = total;
     // entries past the last routed expert: cnt = 0, the projection workgroups exit at once
-    for (uint32_t a = n_active + tid; a < max_active; a += nthr)
-        active[a] = ActiveExpert{};
+    for (uint32_t a = n_active + tid; a < max_active; a += nthr) {
+        uint4 *dst = (uint4 *)(active + a);
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+            dst[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
     // every consumer index starts valid even when the route buffers are rejected
     if (s_bad || total != P)
         for (uint32_t i = tid; i < P; i += nthr) {
@@ -603,11 +621,15 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     const SplitPlan gp = plan_split(H, 2, x_f32 ? 3 : 1, cnt);
     ga.KS = gp.ks;
     int t = timer_begin(K_MOE_GATEUP, stream);
-    launch_moe_a_split(2, x_f32 ? 3 : 1, nt, ga, gp, max_active, stream);
+    const bool fused = nt == 1 && launch_moe_a_gateup_fused(x_f32 ? 3 : 1, ga, max_active, mb.hidden_planes, stream);
+    if (!fused)
+        launch_moe_a_split(2, x_f32 ? 3 : 1, nt, ga, gp, max_active, stream);
     timer_end(t, stream);
-    t = timer_begin(K_MOE_SWIGLU, stream);
-    launch_moe_a_swiglu(mb.partial, gp.ks, placements, I, mb.hidden_planes, flags, stream);
-    timer_end(t, stream);
+    if (!fused) {
+        t = timer_begin(K_MOE_SWIGLU, stream);
+        launch_moe_a_swiglu(mb.partial, gp.ks, placements, I, mb.hidden_planes, flags, stream);
+        timer_end(t, stream);
+    }
 
     SplitArgs da = ga;
     da.placement_pos = nullptr;

@@ -195,6 +195,192 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
         }
 }
 
+// Gate/up over the whole K in one workgroup, SwiGLU fused: the decode fast path when the expert's
+// routed rows fit LDS (NS * cnt <= 8). Work item: (routed expert, 16 weight rows of gate and of
+// up). Eight waves split K (wave w: blocks [w * BPW, (w + 1) * BPW)), each issuing all of its
+// weight loads at once (the same per-lane stream as the split kernel); the expert's routed
+// activation rows for the whole K go straight into LDS; the eight partial sums meet in LDS and
+// are added in split order 0..7 -- the same order and the same arithmetic as the split kernel
+// followed by moe_a_swiglu_kernel, so the hidden planes are bit-identical -- and the SwiGLU is
+// written as three exact bf16 planes. No split partials go through memory.
+template <int NS, int BPW>
+__global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs args, uint16_t *__restrict__ hidden)
+{
+    extern __shared__ uint4 lds_x[];  // [NS * cnt][K/8 + 1]; then the split partials [8][2][64]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // split index, wave-uniform
+    const int q = lane >> 4, r16 = lane & 15;
+    const uint32_t G = args.R >> 4;
+    const uint32_t g = blockIdx.x % G, a = blockIdx.x / G;
+    const ActiveExpert ae = args.active[a];
+    if (ae.cnt == 0)
+        return;
+    if (ae.cnt > 16u || ae.cnt > args.cap) {
+        if (tid == 0)
+            raise_flag(args.flags, FLAG_SCHEDULE);
+        return;
+    }
+    const uint32_t K = args.K;
+    constexpr uint32_t KC = BPW * 128;
+    const uint32_t k0 = wave * KC;
+    const uint32_t row0 = g * 16;
+
+    // 1. this wave's weight bytes of gate and up, all in flight at once
+    const uint8_t *wbase[2] = {ae.ep.gate_w, ae.ep.up_w};
+    const float *sbase[2] = {ae.ep.gate_s, ae.ep.up_s};
+    uint4 wv[2][BPW][2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const uint8_t *wrow = wbase[m] + (size_t)(row0 + r16) * K + k0 + q * 16;
+#pragma unroll
+        for (int j = 0; j < BPW; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                wv[m][j][h] = load_global16(wrow + j * 128 + h * 64);
+    }
+    const uint32_t blocks = K >> 7;
+    float sc[2][BPW];
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int j = 0; j < BPW; ++j)
+            sc[m][j] = load_g(sbase[m] + (row0 >> 7) * blocks + (k0 >> 7) + j);
+
+    // 2. the routed activation rows, whole K (= 8 * KC), planes -> LDS: wave w copies the 64
+    //    16-byte units of its own K split of every row and plane, fully unrolled (one instruction
+    //    per row and plane, since KC / 8 = 64 units)
+    static_assert(KC / 8 == 64, "one 64-lane copy per row and split");
+    constexpr uint32_t per_row = 8 * KC / 8, stride = per_row + 1;
+    bool bad_row = false;
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; ++t) {
+        if (t < ae.cnt) {
+            uint32_t src = ae.tok[t];
+            if (src >= args.rows) {
+                bad_row = true;
+                src = args.rows - 1;
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < (uint32_t)NS; ++p)
+                lds_load16(args.x + p * args.x_plane + (size_t)src * K + k0 + lane * 8,
+                           lds_x + (p * ae.cnt + t) * stride + wave * 64);
+        }
+    }
+    if (bad_row && tid == 0)
+        raise_flag(args.flags, FLAG_SCHEDULE);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // 3. block partials on the MFMA, block scale in registers (as moe_a_split_kernel)
+    f32x4 tot[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const bool ok = (uint32_t)r16 < ae.cnt;
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            bf16x8 A[2][2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                A[m][0] = fp8x8_to_bf16x8(wv[m][j][h].x, wv[m][j][h].y);
+                A[m][1] = fp8x8_to_bf16x8(wv[m][j][h].z, wv[m][j][h].w);
+            }
+            const uint32_t cu = (k0 >> 3) + j * 16 + h * 8 + q * 2;
+#pragma unroll
+            for (int p = 0; p < NS; ++p) {
+                uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+                if (ok) {
+                    const uint4 *xp = lds_x + (p * ae.cnt + r16) * stride + cu;
+                    x0 = xp[0];
+                    x1 = xp[1];
+                }
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    acc[m] = mfma_bf16_16x16x32(A[m][0], bf16x8_from_u4(x0), acc[m]);
+                    acc[m] = mfma_bf16_16x16x32(A[m][1], bf16x8_from_u4(x1), acc[m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                tot[m][i] = __builtin_fmaf(sc[m][j], acc[m][i], tot[m][i]);
+    }
+
+    // 4. the eight split partials meet in LDS (after every wave is done with the activations)
+    __syncthreads();
+    f32x4 *red = (f32x4 *)lds_x;  // [8 splits][2 mats][64 lanes]
+    red[(wave * 2 + 0) * 64 + lane] = tot[0];
+    red[(wave * 2 + 1) * 64 + lane] = tot[1];
+    __syncthreads();
+    if (wave != 0 || !ok)
+        return;
+    // lane: rows 4q .. 4q + 3 of the 16, token r16; split sums in order 0..7, then the SwiGLU
+    float v[2][4];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        f32x4 sum = red[m * 64 + lane];
+#pragma unroll
+        for (int sp = 1; sp < 8; ++sp) {
+            const f32x4 o = red[(sp * 2 + m) * 64 + lane];
+            sum[0] += o[0];
+            sum[1] += o[1];
+            sum[2] += o[2];
+            sum[3] += o[3];
+        }
+        v[m][0] = sum[0]; v[m][1] = sum[1]; v[m][2] = sum[2]; v[m][3] = sum[3];
+    }
+    uint16_t hp[3][4];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float gv = v[0][i];
+        const float hv = (gv / (1.0f + expf(-gv))) * v[1][i];
+        bad |= !finite_f32(hv);
+        split3_bf16(hv, hp[0][i], hp[1][i], hp[2][i]);
+    }
+    const size_t plane = (size_t)args.P * args.R;
+    uint16_t *dst = hidden + (size_t)(ae.off + r16) * args.R + row0 + q * 4;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+        *(uint2 *)(dst + pl * plane) = make_uint2((uint32_t)hp[pl][0] | ((uint32_t)hp[pl][1] << 16),
+                                                  (uint32_t)hp[pl][2] | ((uint32_t)hp[pl][3] << 16));
+    if (bad)
+        raise_flag(args.flags, FLAG_SWIGLU_NONFINITE);
+}
+
+// LDS bytes of the fused gate/up stage: NS planes x cnt rows x (K/8 + 1) 16-byte units, at least
+// the eight split partials.
+static size_t fused_lds(int ns, uint32_t cnt, uint32_t K)
+{
+    const size_t stage = (size_t)ns * cnt * (K / 8 + 1) * 16, red = (size_t)8 * 2 * 64 * 16;
+    return stage > red ? stage : red;
+}
+
+bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_active, uint16_t *hidden_planes,
+                               hipStream_t stream)
+{
+    // four 128-column blocks per wave and split (the split kernel's gate/up stream), eight splits
+    if (args.K != 8 * 4 * 128 || args.R % 16 != 0 || (uint32_t)ns * args.cap > 8)
+        return false;
+    const size_t lds = fused_lds(ns, args.cap, args.K);
+    const dim3 grid(max_active * (args.R >> 4)), block(512);
+    if (ns == 3) {
+        if (lds > 65536)
+            (void)hipFuncSetAttribute((const void *)moe_a_gateup_fused_kernel<3, 4>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL((moe_a_gateup_fused_kernel<3, 4>), grid, block, lds, stream, args, hidden_planes);
+    } else {
+        if (lds > 65536)
+            (void)hipFuncSetAttribute((const void *)moe_a_gateup_fused_kernel<1, 4>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL((moe_a_gateup_fused_kernel<1, 4>), grid, block, lds, stream, args, hidden_planes);
+    }
+    return true;
+}
+
 // Gate/up split sums (in split order 0..KS-1) -> h = (g / (1 + e^-g)) * u in f32 (swiglu_f32,
 // kernels/block_fp8_gemv.metal:241-252; CPU src/lib.rs:5840-5844), written as three exact bf16
 // planes for the down projection's MFMA. One thread per (slot, 4 rows). With KS known at compile

@@ -13,17 +13,18 @@
 // scales are applied in f32, sequentially over b (the same per-block arithmetic as the decode
 // mode B kernels).
 //
-// Tiles: (96 placement slots of one routed expert = an m-tile) x (64 weight rows = an n-tile);
+// Tiles: (96 placement slots of one routed expert = an m-tile) x (128 weight rows = an n-tile);
 // 96 slots hold a whole expert's placements at the uniform-routing count (64 on average), so its
 // weights stream once. Gate and up run as one stacked projection (2I output columns per slot),
-// then a SwiGLU + re-quantisation kernel, then down. A workgroup of four waves (16 weight rows
-// each) walks K in 128-column steps. Weight bytes (one row per lane) load straight into a
-// four-slot register ring, four steps ahead of the MFMA; activation codes (cache hits, shared by
-// the expert's n-tiles) load one step ahead into registers and then go to a double-buffered LDS
-// tile (16-byte units XOR-swizzled by token so the B-operand reads spread over the LDS banks).
-// The barriers order LDS only, so the weight stream stays in flight across them. The m-tile's
-// activation scales (transposed, [block][token]) and the tile's weight block scales are staged in
-// LDS once.
+// then a SwiGLU + re-quantisation kernel, then down. A workgroup walks K in 128-column steps with
+// two kinds of waves, so the two streams never wait on each other in the in-order memory counter:
+// eight consumer waves (16 weight rows each) load their weight bytes (one row per lane) into a
+// four-step register ring and run the MFMAs; one producer wave copies the m-tile's activation
+// codes (cache hits, shared by the expert's n-tiles) with direct-to-LDS loads into a four-step LDS
+// ring (16-byte units XOR-swizzled by token so the B-operand reads spread over the LDS banks).
+// One LDS-only barrier per step publishes a ring slot and frees the previous one; the weight
+// stream stays in flight across it. The m-tile's activation scales (transposed, [block][token])
+// and the tile's weight block scales are staged in LDS once.
 // Epilogues: every projection rounds to bf16 (bf16_round_in_place, src/wide_metal_moe.rs:
 // 1236-1251); bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160) runs on the bf16 gate and
 // up outputs. The combine then sums each token's eight outputs.
@@ -35,8 +36,24 @@ namespace pw {
 constexpr uint32_t PF_MT = 96;                    // placement slots per m-tile
 constexpr int PF_TT = (int)PF_MT / 16;            // 16-token MFMA tiles per m-tile
 constexpr uint32_t PF_UNITS = 8;                  // 16-byte units per 128-byte token row of a step
-constexpr int PF_CPW = (int)PF_MT / 8 / 4;        // 8-token code chunks per wave per step
-constexpr int PF_WS = 4;                          // weight register slots: loads run 4 steps ahead
+constexpr int PF_CONS = 8;                        // consumer waves per workgroup, 16 weight rows each
+constexpr uint32_t PF_NROWS = 16 * PF_CONS;       // weight rows per n-tile
+constexpr uint32_t PF_BLK = PF_MT * PF_UNITS;     // 16-byte code units per 128-column block
+constexpr int PF_DMA = (int)(PF_BLK / 64);        // producer copy instructions per block
+static_assert(PF_BLK % 64 == 0, "a block's codes are whole 64-lane copies");
+
+// K-step shape: SB 128-column blocks per step, WS weight steps in flight per consumer lane, D code
+// steps in the LDS ring. Two-block steps ask for 256 contiguous bytes of every weight row at once
+// (more DRAM page hits than 128-byte pieces); one-block steps cover an odd number of blocks.
+template <int SB_, int WS_, int D_>
+struct PfCfg {
+    static constexpr int SB = SB_, WS = WS_, D = D_;
+    static constexpr int G = WS > D ? WS : D;              // steps per unrolled group
+    static constexpr uint32_t STEP = SB * PF_BLK;          // 16-byte code units per step
+    static_assert(G % WS == 0 && G % D == 0, "ring sizes divide the unrolled group");
+};
+using PfWide = PfCfg<2, 2, 2>;
+using PfNarrow = PfCfg<1, 4, 4>;
 
 // Tile table: ceil(count / 96) m-tiles per routed expert, ascending expert order. One workgroup of
 // 1024 threads, one thread per schedule entry (banks hold at most 1024 experts).
@@ -78,76 +95,81 @@ struct PrefillArgs {
     uint32_t *flags;
 };
 
-// One K step's weight bytes of this lane: its row, columns [16q, 16q + 16) and [64 + 16q, 80 + 16q)
-// of the 128-column block (q = lane / 16), so each load instruction reads 64 contiguous bytes of
-// each of 16 rows. The MFMA's K order within the block is permuted alike for the codes, so the
-// block dot product covers the same 128 products.
+// One K step's weight bytes of this lane: for each of the step's blocks, its row's columns
+// [16q, 16q + 16) and [64 + 16q, 80 + 16q) of the 128-column block (q = lane / 16), so each load
+// instruction reads 64 contiguous bytes of each of 16 rows and a step asks for SB * 128
+// contiguous bytes of every row at once. The MFMA's K order within a block is permuted alike for
+// the codes, so the block dot product covers the same 128 products.
+template <class C>
 struct PfW {
-    uint4 v[2];
+    uint4 v[2 * C::SB];
 };
 
-// This lane's share of one step's activation codes: PF_CPW chunks of 8 tokens x 128 bytes per
-// wave; lane i holds global unit (i % 8) ^ (token % 8) of token 8c + i / 8 and stores it as LDS
-// unit i % 8 of that token (unit index 64c + i: conflict-free writes).
-struct PfC {
-    uint4 v[PF_CPW];
-};
-
-__device__ __forceinline__ void pf_issue_w(PfW &w, const uint8_t *wrow, uint32_t k0)
-{
-    w.v[0] = load_global16(wrow + k0);
-    w.v[1] = load_global16(wrow + k0 + 64);
-}
-
-__device__ __forceinline__ void pf_issue_c(PfC &c, const uint8_t *const *csrc, uint32_t k0)
+template <class C>
+__device__ __forceinline__ void pf_issue_w(PfW<C> &w, const uint8_t *wrow, uint32_t k0)
 {
 #pragma unroll
-    for (int u = 0; u < PF_CPW; ++u)
-        c.v[u] = load_global16(csrc[u] + k0);
-}
-
-__device__ __forceinline__ void pf_store_codes(uint4 *buf, const PfC &c, int wave, int lane)
-{
-#pragma unroll
-    for (int u = 0; u < PF_CPW; ++u)
-        buf[(PF_CPW * wave + u) * 64 + lane] = c.v[u];
-}
-
-// Workgroup barrier ordering LDS accesses only: outstanding global loads (the prefetched steps)
-// stay in flight across it, which __syncthreads() would wait for.
-__device__ __forceinline__ void lds_barrier()
-{
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-__device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], const PfW &w, const uint4 *buf,
-                                           const float *lds_scale, float sw, uint32_t b, int q, int r16)
-{
-    const i32x8 A = {(int)w.v[0].x, (int)w.v[0].y, (int)w.v[0].z, (int)w.v[0].w,
-                     (int)w.v[1].x, (int)w.v[1].y, (int)w.v[1].z, (int)w.v[1].w};
-#pragma unroll
-    for (int j = 0; j < PF_TT; ++j) {
-        const uint32_t t = 16 * j + r16;
-        const float sa = lds_scale[b * PF_MT + t];
-        const uint4 c0 = buf[t * PF_UNITS + ((q) ^ (t & 7))];
-        const uint4 c1 = buf[t * PF_UNITS + ((q + 4) ^ (t & 7))];
-        const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w, (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
-        const f32x4 p = mfma_fp8_16x16x128(A, xb, f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            tot[j][i] = __builtin_fmaf(p[i] * sw, sa, tot[j][i]);
+    for (int h = 0; h < C::SB; ++h) {
+        w.v[2 * h] = load_global16(wrow + k0 + 128 * h);
+        w.v[2 * h + 1] = load_global16(wrow + k0 + 128 * h + 64);
     }
 }
 
-// One projection tile: 64 weight rows (of gate, up or down) x one m-tile of placement slots,
-// bf16-rounded outputs (bf16_round_in_place of every projection, src/wide_metal_moe.rs:1236-1251).
-// n-tiles [0, R1 / 64) use the first matrix (gate, or down), the rest the second (up).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void prefill_b_kernel(const PrefillArgs args)
+// The producer's copy of one step's codes into a ring slot (one block after another): instruction
+// c of a block covers tokens 8c .. 8c + 7; lane i reads global unit (i % 8) ^ (token % 8) of token
+// 8c + i / 8 and lands at LDS unit 64c + i (unit i % 8 of that token).
+template <class C>
+__device__ __forceinline__ void pf_copy_codes(uint4 *slot, const uint8_t *const *csrc, uint32_t k0)
 {
-    __shared__ uint4 lds_codes[2][PF_MT * PF_UNITS];  // two 12 KB steps, swizzled
-    extern __shared__ float lds_scale[];              // [K / 128][96] activation, then [K / 128] weight
+#pragma unroll
+    for (int h = 0; h < C::SB; ++h)
+#pragma unroll
+        for (int c = 0; c < PF_DMA; ++c)
+            lds_load16(csrc[c] + k0 + 128 * h, slot + h * PF_BLK + c * 64);
+}
+
+// One step: its blocks in ascending order, each block's FP8 products from one MFMA per 16-token
+// tile, then tot += (p * S_w) * a in f32.
+template <class C>
+__device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], const PfW<C> &w, const uint4 *slot,
+                                           const float *lds_scale, const float *lds_wscale, uint32_t k, int q,
+                                           int r16)
+{
+#pragma unroll
+    for (int h = 0; h < C::SB; ++h) {
+        const uint32_t b = k * C::SB + h;
+        const float sw = lds_wscale[b];
+        const uint4 *buf = slot + h * PF_BLK;
+        const i32x8 A = {(int)w.v[2 * h].x,     (int)w.v[2 * h].y,     (int)w.v[2 * h].z,     (int)w.v[2 * h].w,
+                         (int)w.v[2 * h + 1].x, (int)w.v[2 * h + 1].y, (int)w.v[2 * h + 1].z, (int)w.v[2 * h + 1].w};
+#pragma unroll
+        for (int j = 0; j < PF_TT; ++j) {
+            const uint32_t t = 16 * j + r16;
+            const float sa = lds_scale[b * PF_MT + t];
+            const uint4 c0 = buf[t * PF_UNITS + ((q) ^ (t & 7))];
+            const uint4 c1 = buf[t * PF_UNITS + ((q + 4) ^ (t & 7))];
+            const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
+                              (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
+            const f32x4 p = mfma_fp8_16x16x128(A, xb, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                tot[j][i] = __builtin_fmaf(p[i] * sw, sa, tot[j][i]);
+        }
+    }
+}
+
+// One projection tile: 128 weight rows (of gate, up or down) x one m-tile of placement slots,
+// bf16-rounded outputs (bf16_round_in_place of every projection, src/wide_metal_moe.rs:1236-1251).
+// n-tiles [0, R1 / 128) use the first matrix (gate, or down), the rest the second (up).
+template <class C>
+__global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per_eu(C::SB == 2 ? 5 : 4))) void prefill_b_kernel(const PrefillArgs args)
+{
+    extern __shared__ uint4 lds_pf[];
+    const uint32_t K = args.K, blocks = K >> 7;
+    const uint32_t nsteps = blocks / C::SB, last = nsteps - 1;  // the launcher checks blocks % SB
+    uint4 *ring = lds_pf;                                   // [D][STEP] code units, swizzled
+    float *lds_scale = (float *)(ring + C::D * C::STEP);    // [blocks][96] activation scales
+    float *lds_wscale = lds_scale + blocks * PF_MT;       // [blocks] weight block scales
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r16 = lane & 15;
@@ -155,7 +177,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     // m-tiles x, x + 8, ... and runs all n-tiles of one m-tile back to back: the m-tile's
     // activation codes stay in that XCD's L2 while its n-tiles stream their weight rows, and the
     // m-tiles (counted on the device) spread evenly over the XCDs.
-    const uint32_t n_ntiles = args.R >> 6;
+    const uint32_t n_ntiles = args.R / PF_NROWS;
     const uint32_t local = blockIdx.x >> 3;
     const uint32_t mt = (blockIdx.x & 7) + 8 * (local / n_ntiles), ntile = local % n_ntiles;
     if (mt >= args.n_tiles[0])
@@ -166,16 +188,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
     if (m0 >= ae.cnt)
         return;
     const uint32_t cnt_t = ae.cnt - m0 < PF_MT ? ae.cnt - m0 : PF_MT;
-    const uint32_t K = args.K, blocks = K >> 7;
-    const uint32_t col0 = ntile * 64;                    // output column of the tile
+    const uint32_t col0 = ntile * PF_NROWS;               // output column of the tile
     const bool second = col0 >= args.R1;
-    const uint32_t row_base = (second ? col0 - args.R1 : col0) + wave * 16;  // row in its matrix
+    const uint32_t mrow0 = second ? col0 - args.R1 : col0;  // first weight row in its matrix
     const uint32_t slot0 = ae.off + m0;
     const bool gather = args.placement_pos != nullptr;
-    const uint8_t *wmat = gather ? (second ? ae.ep.up_w : ae.ep.gate_w) : ae.ep.down_w;
-    const float *smat = gather ? (second ? ae.ep.up_s : ae.ep.gate_s) : ae.ep.down_s;
-    const uint8_t *wrow = wmat + (size_t)(row_base + r16) * K + q * 16;
-    smat += (row_base >> 7) * blocks;
 
     // token rows of the m-tile's slots (lane: slots lane and 64 + lane, the second only below 96;
     // slots past the tile's count repeat its last slot: in-bounds loads whose output columns are
@@ -188,10 +205,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         if (gather)
             tok[h] = load_g(args.placement_pos + tok[h]);
     }
-    float wsc = 0.f;  // weight block scales of the workgroup's 64 rows (one 128-row scale block)
-    if ((uint32_t)tid < blocks)
-        wsc = load_g(smat + tid);
-    const uint32_t last = blocks - 1;
     if (gather) {
         bool bad = false;
 #pragma unroll
@@ -202,19 +215,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
         if (bad)
             raise_flag(args.flags, FLAG_SCHEDULE);
     }
-    // per-lane sources of this wave's code chunks: tokens 8c + lane / 8, c = PF_CPW * wave + u
-    const uint8_t *csrc[PF_CPW];
-    const uint32_t g = ((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7;  // global unit of LDS unit lane % 8
-#pragma unroll
-    for (int u = 0; u < PF_CPW; ++u) {
-        const uint32_t t = 8 * (PF_CPW * wave + u) + (lane >> 3);
-        const uint32_t r0 = __shfl(tok[0], (int)(t & 63), 64), r1 = __shfl(tok[1], (int)(t & 63), 64);
-        csrc[u] = args.codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
+    // weight block scales of the n-tile (one 128-row scale block) and the m-tile's activation
+    // scales, transposed (lds_scale[b * 96 + t]) with 4-byte direct-to-LDS loads (lane = token; a
+    // second instruction covers tokens 64..95), spread over all waves
+    {
+        const float *smat = gather ? (second ? ae.ep.up_s : ae.ep.gate_s) : ae.ep.down_s;
+        if ((uint32_t)tid < blocks)
+            lds_wscale[tid] = load_g(smat + (mrow0 >> 7) * blocks + tid);
     }
-    // activation scales of the m-tile, transposed (lds_scale[b * 96 + t]), with 4-byte
-    // direct-to-LDS loads (lane = token; a second instruction covers tokens 64..95)
-    float *lds_wscale = lds_scale + blocks * PF_MT;
-    for (uint32_t b = wave; b < blocks; b += 4) {
+    for (uint32_t b = wave; b < blocks; b += PF_CONS + 1) {
         __builtin_amdgcn_global_load_lds(
             (const __attribute__((address_space(1))) void *)(args.scales + (size_t)tok[0] * blocks + b),
             (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT), 4, 0, 0);
@@ -223,64 +232,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void p
                 (const __attribute__((address_space(1))) void *)(args.scales + (size_t)tok[1] * blocks + b),
                 (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT + 64), 4, 0, 0);
     }
-    if ((uint32_t)tid < blocks)
-        lds_wscale[tid] = wsc;
-    // step 0's codes to LDS; the weight ring (steps 0..3, clamped to the last step) and step 1's
-    // codes in flight; every load is unconditional, so the compiler's wait counts stay exact
-    PfC cr;
-    pf_issue_c(cr, csrc, 0);
-    pf_store_codes(lds_codes[0], cr, wave, lane);
-    PfW w[PF_WS];
-#pragma unroll
-    for (int i = 0; i < PF_WS; ++i)
-        pf_issue_w(w[i], wrow, ((uint32_t)i < last ? (uint32_t)i : last) << 7);
-    pf_issue_c(cr, csrc, (1 < last ? 1u : last) << 7);
 
+    if (wave == PF_CONS) {
+        // ---- producer: the codes ring. Per-lane sources of the step's copy instructions.
+        const uint8_t *csrc[PF_DMA];
+        const uint32_t g = ((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7;
+#pragma unroll
+        for (int c = 0; c < PF_DMA; ++c) {
+            const uint32_t t = 8 * c + (lane >> 3);
+            const uint32_t r0 = __shfl(tok[0], (int)(t & 63), 64), r1 = __shfl(tok[1], (int)(t & 63), 64);
+            csrc[c] = args.codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
+        }
+        // steps 0 .. C::D - 2 into slots 0 .. C::D - 2 (indices clamped to the last step)
+#pragma unroll
+        for (int s = 0; s < C::D - 1; ++s)
+            pf_copy_codes<C>(ring + s * C::STEP, csrc, ((uint32_t)s < last ? (uint32_t)s : last) * (128 * C::SB));
+        for (uint32_t k = 0; k < nsteps; ++k) {
+            // step k's copy (and every older one) is complete; C::D - 2 younger steps stay in flight
+            wait_vmcnt<(C::D - 2) * PF_DMA * C::SB>();
+            lds_barrier();  // publishes slot k % C::D; every consumer is done with step k - 1
+            const uint32_t s = k + C::D - 1;
+            pf_copy_codes<C>(ring + (s % C::D) * C::STEP, csrc, (s < last ? s : last) * (128 * C::SB));
+        }
+        wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
+        return;
+    }
+
+    // ---- consumers: 16 weight rows each, the weight ring in registers
+    const uint8_t *wmat = gather ? (second ? ae.ep.up_w : ae.ep.gate_w) : ae.ep.down_w;
+    const uint8_t *wrow = wmat + (size_t)(mrow0 + wave * 16 + r16) * K + q * 16;
+    PfW<C> w[C::WS];
+#pragma unroll
+    for (int i = 0; i < C::WS; ++i)
+        pf_issue_w<C>(w[i], wrow, ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB));
     f32x4 tot[PF_TT];
 #pragma unroll
     for (int j = 0; j < PF_TT; ++j)
         tot[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // The scale loads wrote LDS directly: wait for every load issued so far (the ring's first
-    // four steps arrive together with them). Entering the loop with nothing outstanding also lets
-    // the compiler keep its per-register memory-counter waits exact at the loop head.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // this wave's scale copies (issued before the weights) are complete before the first barrier
+    wait_vmcnt<2 * C::SB * C::WS>();
 
-    // Sub-step k: compute step k from weight slot k % 4 and LDS buffer k & 1; store step k + 1's
-    // codes (loaded one sub-step ago) into the other buffer; load step k + 2's codes and step
-    // k + 4's weights into the freed registers; one barrier. Weights stream four steps ahead,
-    // codes (mostly cache hits, shared by the n-tiles of the expert) one step ahead.
-    // Whole groups of four steps run without early exits (so the compiler sees one loop state at
-    // the loop head); the last 0..3 steps are peeled. Load indices are clamped to the last step
-    // (the tail reloads it: cache hits), keeping every load unconditional.
-#define PF_SUBSTEP(W, K, BUF)                                                                 \
-    {                                                                                       \
-        const uint32_t k = (K);                                                             \
-        pf_compute(tot, W, lds_codes[BUF], lds_scale, lds_wscale[k], k, q, r16);            \
-        __builtin_amdgcn_sched_barrier(0);                                                  \
-        pf_store_codes(lds_codes[(BUF) ^ 1], cr, wave, lane);                               \
-        pf_issue_c(cr, csrc, (k + 2 < last ? k + 2 : last) << 7);                           \
-        pf_issue_w(W, wrow, (k + PF_WS < last ? k + PF_WS : last) << 7);                    \
-        lds_barrier();                                                                      \
-    }
-    const uint32_t nfull = blocks & ~3u;
-    for (uint32_t b = 0; b < nfull; b += PF_WS) {
-        PF_SUBSTEP(w[0], b, 0)
-        PF_SUBSTEP(w[1], b + 1, 1)
-        PF_SUBSTEP(w[2], b + 2, 0)
-        PF_SUBSTEP(w[3], b + 3, 1)
-    }
-    if (nfull < blocks) {
-        PF_SUBSTEP(w[0], nfull, 0)
-        if (nfull + 1 < blocks) {
-            PF_SUBSTEP(w[1], nfull + 1, 1)
-            if (nfull + 2 < blocks)
-                PF_SUBSTEP(w[2], nfull + 2, 0)
+    // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, then load
+    // step k + C::WS's weights into that slot. Whole groups of C::G steps run without early exits
+    // (static ring indices, one loop state at the loop head); the last steps are peeled. Load
+    // indices are clamped to the last step (the tail reloads it: cache hits), keeping every load
+    // unconditional.
+    const uint32_t nfull = nsteps - nsteps % C::G;
+    for (uint32_t b = 0; b < nfull; b += C::G) {
+#pragma unroll
+        for (int i = 0; i < C::G; ++i) {
+            const uint32_t k = b + i;
+            lds_barrier();
+            pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, q, r16);
+            pf_issue_w<C>(w[i % C::WS], wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB));
         }
     }
-#undef PF_SUBSTEP
+#pragma unroll
+    for (int i = 0; i < C::G - 1; ++i) {
+        const uint32_t k = nfull + i;
+        if (k >= nsteps)
+            break;
+        lds_barrier();
+        pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, q, r16);
+        pf_issue_w<C>(w[i % C::WS], wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB));
+    }
 
-    // epilogue: lane holds rows row_base + 4q + i of tokens 16j + r16 -> bf16
+    // epilogue: lane holds rows 4q + i of the wave's 16 for tokens 16j + r16 -> bf16
     const uint32_t R = args.R;
     const uint32_t ocol = col0 + wave * 16 + 4 * q;
 #pragma unroll
@@ -397,11 +414,23 @@ uint32_t prefill_max_tiles(uint32_t rows, uint32_t E)
     return max_active + (P + PF_MT - 1) / PF_MT;
 }
 
+template <class C>
+static void launch_prefill_cfg(const PrefillArgs &a, hipStream_t stream)
+{
+    const size_t lds = (size_t)C::D * C::STEP * 16 + (size_t)(a.K / 128) * (PF_MT + 1) * 4;
+    if (lds > 65536)  // wide K: up to 160 KB of LDS per workgroup on gfx950
+        (void)hipFuncSetAttribute((const void *)prefill_b_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds);
+    const uint32_t grid = 8 * ((a.max_tiles + 7) / 8) * (a.R / PF_NROWS);
+    hipLaunchKernelGGL((prefill_b_kernel<C>), dim3(grid), dim3(64 * (PF_CONS + 1)), lds, stream, a);
+}
+
 static void launch_prefill_projection(const PrefillArgs &a, hipStream_t stream)
 {
-    const size_t lds = (size_t)(a.K / 128) * (PF_MT + 1) * 4;
-    const uint32_t grid = 8 * ((a.max_tiles + 7) / 8) * (a.R >> 6);
-    hipLaunchKernelGGL(prefill_b_kernel, dim3(grid), dim3(256), lds, stream, a);
+    if ((a.K / 128) % PfWide::SB == 0)
+        launch_prefill_cfg<PfWide>(a, stream);
+    else
+        launch_prefill_cfg<PfNarrow>(a, stream);
 }
 
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
