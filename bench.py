@@ -239,6 +239,20 @@ def projection_legs(torch, rt, bank, P, WL, calls=200):
                 rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
             out[f"config3_k{k_rows}_w{width}"] = rec
         del projs, hosts
+    # BF16 wide linear: attention o_proj [4096 x 8192] (64 MB), widths 1 and 8, f32 in, bf16-rounded f32 out
+    copies, n, k = 10, 4096, 8192
+    wb = torch.randn((copies, n, k), dtype=torch.bfloat16, device="cuda").view(torch.int16)
+    bprojs = [rt.bind_bf16_device(wb[i], n, k) for i in range(copies)]
+    for width in (1, 8):
+        x = torch.randn((width, k), dtype=torch.float32, device="cuda")
+        y = torch.empty((width, n), dtype=torch.float32, device="cuda")
+        alg = n * k * 2 + width * k * 4 + width * n * 4
+        rec = {"algorithmic_bytes": alg}
+        for label, pick in (("hbm_cold", lambda i: bprojs[i % copies]), ("mall_warm", lambda i: bprojs[0])):
+            us = _time_calls(torch, rt, lambda i, st: rt.bf16_linear_device(pick(i), x, width, y, stream=st), calls)
+            rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+        out[f"bf16_o_proj_w{width}"] = rec
+    del bprojs, wb
     return out
 
 

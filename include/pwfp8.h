@@ -145,7 +145,7 @@ int pw_runtime_take_flags(pw_runtime *rt, uint32_t *flags);
  * command buffer, src/staged_metal_expert.rs:1763-1771): when enabled, every timed launch records
  * a start and a stop event on the stream it runs on, up to max_launches (0 disables). Kernel
  * names: linear_a, linear_b, quant, moe_schedule, moe_gateup, moe_swiglu, moe_down, moe_combine,
- * prefill_gateup, prefill_down, router. */
+ * prefill_gateup, prefill_down, router, bf16_linear. */
 int pw_runtime_enable_timing(pw_runtime *rt, uint32_t max_launches);
 /* Synchronise the device; report the recorded launches of `kernel` and their summed duration. */
 int pw_runtime_timing_summary(pw_runtime *rt, const char *kernel, uint32_t *launches,
@@ -182,6 +182,29 @@ int pw_fp8_linear(pw_runtime *rt, uint32_t mode, const float *input, uint32_t ro
 int pw_fp8_linear_device(pw_runtime *rt, uint32_t mode, const void *input, uint32_t input_dtype,
                          uint32_t rows, const pw_projection *proj, void *output,
                          uint32_t output_dtype, uint32_t round_output, void *stream);
+
+/* ---- BF16 wide linear ---------------------------------------------------------------------- */
+/* Binds a checkpoint BF16 weight view [rows x columns] (o_proj, LM head) and copies it into HBM once
+ * (the reference maps the region no-copy per call in execute_bf16_linear,
+ * src/wide_metal_moe.rs:728-760, and checks tensor_bytes == rows * columns * 2: a mismatch is
+ * PW_ERR_LAYOUT "wide BF16 linear layout mismatch"). columns % 128 == 0. The handle is released
+ * with pw_projection_release and reports its shape through pw_projection_shape. */
+int pw_bf16_bind(pw_runtime *rt, const pw_region *weight, uint32_t rows, uint32_t columns, pw_projection **out);
+/* No-copy binding of BF16 weights already resident in device memory (16-byte aligned). */
+int pw_bf16_bind_device(pw_runtime *rt, const void *weight, uint32_t rows, uint32_t columns,
+                        pw_projection **out);
+/* WideMetalMoeRuntime::execute_bf16_linear (src/wide_metal_moe.rs:728-834; CPU twin bf16_linear,
+ * src/text_endpoint.rs:3347-3380): input f32 [rows x columns] (rows 1..32; the reference allows
+ * 1..8), output f32 [rows x proj_rows] = round_bf16(sum_c bf16(W[r, c]) * x[p, c]) with f32
+ * accumulation. Non-finite input -> PW_ERR_NONFINITE; a non-finite output raises the reference's
+ * error bit 32 (PW_FLAG_ROUND_NONFINITE) -> PW_ERR_GPU_FLAGS. Synchronous. */
+int pw_bf16_linear(pw_runtime *rt, const float *input, uint32_t rows, const pw_projection *proj, float *output,
+                   pw_linear_stats *stats);
+/* Device-resident form (input 16-byte aligned, input_dtype F32 or BF16; output_dtype as for
+ * pw_fp8_linear_device), enqueued on stream. */
+int pw_bf16_linear_device(pw_runtime *rt, const void *input, uint32_t input_dtype, uint32_t rows,
+                          const pw_projection *proj, void *output, uint32_t output_dtype, uint32_t round_output,
+                          void *stream);
 
 /* Dynamic per-(row, 128-column group) FP8 activation quantiser on device rows
  * (dynamic_fp8_quantized_group128, kernels/block_fp8_gemv.metal:84-137; CPU authority

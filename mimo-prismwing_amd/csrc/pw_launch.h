@@ -22,6 +22,7 @@ enum KernelId : uint32_t {
     K_PREFILL_GATEUP,
     K_PREFILL_DOWN,
     K_ROUTER,
+    K_BF16_LINEAR,
     K_COUNT
 };
 
@@ -101,6 +102,21 @@ SplitPlan plan_split(uint32_t K, int mats, int ns, uint32_t max_cnt);
 void launch_moe_a_split(int mats, int ns, int nt, const SplitArgs &args, const SplitPlan &sp,
                         uint32_t max_active, hipStream_t stream);
 // gate/up split sums -> SwiGLU -> hidden as three bf16 planes [3][P][I]
+// BF16 wide linear (pw_bf16.hip): w bf16 [R][K] (K a multiple of 128), x bf16 planes [NS][W][K],
+// split-K partials [KS][W][R] f32 summed in split order by the reduce kernel.
+struct Bf16Args {
+    const uint16_t *w;
+    const uint16_t *x;
+    size_t x_plane;
+    uint32_t K, R, W, KS;
+    float *partial;
+};
+// 128-column blocks per wave for K (the K split is 128 * that); at most `lds_cap` bytes of LDS
+// for NS planes of W activation rows.
+int bf16_blocks_per_wave(uint32_t K, int planes, uint32_t W, size_t lds_cap);
+void launch_bf16_linear(const Bf16Args &a, int planes, int bpw, float *y32, uint16_t *y16, uint32_t round_f32,
+                        uint32_t *flags, hipStream_t stream);
+
 // Gate/up with the SwiGLU fused and no split partials (pw_moe_a.hip), when the routed rows fit the
 // LDS stage; returns false (nothing launched) otherwise.
 bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_active, uint16_t *hidden_planes,

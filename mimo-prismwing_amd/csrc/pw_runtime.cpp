@@ -33,7 +33,7 @@ namespace {
 
 const char *const kKernelNames[pw::K_COUNT] = {
     "linear_a", "linear_b", "quant", "moe_schedule", "moe_gateup", "moe_swiglu", "moe_down",
-    "moe_combine", "prefill_gateup", "prefill_down", "router"};
+    "moe_combine", "prefill_gateup", "prefill_down", "router", "bf16_linear"};
 
 thread_local std::string g_error;
 
@@ -99,7 +99,7 @@ struct pw_runtime {
     // routed-MoE per-layer scratch
     DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
         moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
-        moe_active, moe_partial, pf_tiles, router_scores;
+        moe_active, moe_partial, pf_tiles, router_scores, bf16_partial;
     MoeBuffers mb{};
     pw::KernelTimer timer;
 };
@@ -127,6 +127,7 @@ void free_timer(pw::KernelTimer &t)
 
 struct pw_projection {
     pw_runtime *rt = nullptr;
+    bool bf16 = false;          // BF16 weights [rows][columns] (no scales, no tile table)
     uint8_t *w = nullptr;       // device weight base
     float *s = nullptr;         // device scale base
     bool owns = false;
@@ -234,9 +235,12 @@ int reset_flags(pw_runtime *rt)
     return PW_OK;
 }
 
+// A synchronous host call owns the error word for its duration (like the reference's per-call
+// error buffer): it is cleared before the call's kernels and read and cleared after them.
 int read_flags(pw_runtime *rt, uint32_t &flags)
 {
     PW_HIP(hipMemcpyAsync(&flags, rt->d_flags, sizeof(uint32_t), hipMemcpyDeviceToHost, rt->stream));
+    PW_HIP(hipMemsetAsync(rt->d_flags, 0, sizeof(uint32_t), rt->stream));
     PW_HIP(hipStreamSynchronize(rt->stream));
     return PW_OK;
 }
@@ -676,6 +680,8 @@ int pw_fp8_linear(pw_runtime *rt, uint32_t mode, const float *input, uint32_t ro
     const double t0 = now_ms();
     if (!rt || !input || !p || !output)
         return fail(PW_ERR_ARGUMENT, "null argument");
+    if (p->bf16)
+        return fail(PW_ERR_ARGUMENT, "a BF16 projection runs through pw_bf16_linear");
     if (rows < 1 || rows > 32)
         return fail(PW_ERR_ARGUMENT, "wide row count must be between one and 32");
     const size_t n_in = (size_t)rows * p->columns, n_out = (size_t)rows * p->rows;
@@ -712,6 +718,8 @@ int pw_fp8_linear_device(pw_runtime *rt, uint32_t mode, const void *input, uint3
 {
     if (!rt || !input || !p || !output)
         return fail(PW_ERR_ARGUMENT, "null argument");
+    if (p->bf16)
+        return fail(PW_ERR_ARGUMENT, "a BF16 projection runs through pw_bf16_linear_device");
     if (rows < 1 || rows > 32)
         return fail(PW_ERR_ARGUMENT, "wide row count must be between one and 32");
     if (input_dtype > PW_DTYPE_BF16 || output_dtype > PW_DTYPE_F32_RAW)
@@ -723,6 +731,147 @@ int pw_fp8_linear_device(pw_runtime *rt, uint32_t mode, const void *input, uint3
     uint16_t *y16 = output_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr;
     const uint32_t round_f32 = output_dtype == PW_DTYPE_F32 && round_output ? 1u : 0u;
     return enqueue_linear(rt, mode, input, input_dtype == PW_DTYPE_F32, rows, p, y32, y16, round_f32, s);
+}
+
+// ---- BF16 wide linear ------------------------------------------------------------------------
+static int bf16_bind_common(pw_runtime *rt, uint32_t rows, uint32_t columns, pw_projection **out)
+{
+    if (!rt || !out)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    *out = nullptr;
+    if (rows == 0 || columns == 0 || columns % 128 != 0)
+        return fail(PW_ERR_LAYOUT, "BF16 linear dimensions must be nonzero, columns a multiple of 128");
+    return PW_OK;
+}
+
+int pw_bf16_bind(pw_runtime *rt, const pw_region *weight, uint32_t rows, uint32_t columns, pw_projection **out)
+{
+    PW_TRY(bf16_bind_common(rt, rows, columns, out));
+    if (!weight || !weight->bytes)
+        return fail(PW_ERR_ARGUMENT, "null weight region");
+    const size_t bytes = (size_t)rows * columns * 2;
+    if (weight->tensor_bytes != bytes || weight->tensor_offset + bytes > weight->region_bytes)
+        return fail(PW_ERR_LAYOUT, "wide BF16 linear layout mismatch");
+    PW_HIP(set_device(rt));
+    pw_projection *p = new pw_projection;
+    p->rt = rt;
+    p->bf16 = true;
+    p->owns = true;
+    p->rows = rows;
+    p->columns = columns;
+    p->weight_bytes = bytes;
+    hipError_t e = hipMalloc(&p->w, bytes);
+    if (e == hipSuccess)
+        e = hipMemcpy(p->w, (const uint8_t *)weight->bytes + weight->tensor_offset, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        pw_projection_release(p);
+        return fail(PW_ERR_DEVICE, "BF16 weight upload: %s", hipGetErrorString(e));
+    }
+    *out = p;
+    return PW_OK;
+}
+
+int pw_bf16_bind_device(pw_runtime *rt, const void *weight, uint32_t rows, uint32_t columns, pw_projection **out)
+{
+    PW_TRY(bf16_bind_common(rt, rows, columns, out));
+    if (!weight)
+        return fail(PW_ERR_ARGUMENT, "null weight");
+    if ((uintptr_t)weight & 15)
+        return fail(PW_ERR_ARGUMENT, "BF16 weights must be 16-byte aligned");
+    pw_projection *p = new pw_projection;
+    p->rt = rt;
+    p->bf16 = true;
+    p->w = (uint8_t *)weight;
+    p->rows = rows;
+    p->columns = columns;
+    p->weight_bytes = (uint64_t)rows * columns * 2;
+    *out = p;
+    return PW_OK;
+}
+
+static int enqueue_bf16_linear(pw_runtime *rt, const void *x, bool x_f32, uint32_t rows, const pw_projection *p,
+                               float *y32, uint16_t *y16, uint32_t round_f32, hipStream_t stream)
+{
+    const int planes = x_f32 ? 3 : 1;
+    const uint16_t *xp = (const uint16_t *)x;
+    if (x_f32) {
+        const size_t n = (size_t)rows * p->columns;
+        PW_HIP(rt->lin_planes.ensure(3 * n * 2));
+        pw::launch_split_planes((const float *)x, (uint32_t)n, (uint16_t *)rt->lin_planes.p, stream);
+        xp = (const uint16_t *)rt->lin_planes.p;
+    }
+    const int bpw = pw::bf16_blocks_per_wave(p->columns, planes, rows, 65536);
+    pw::Bf16Args a{};
+    a.w = (const uint16_t *)p->w;
+    a.x = xp;
+    a.x_plane = (size_t)rows * p->columns;
+    a.K = p->columns;
+    a.R = p->rows;
+    a.W = rows;
+    a.KS = p->columns / (128u * bpw);
+    PW_HIP(rt->bf16_partial.ensure((size_t)a.KS * rows * p->rows * 4));
+    a.partial = (float *)rt->bf16_partial.p;
+    pw::launch_bf16_linear(a, planes, bpw, y32, y16, round_f32, rt->d_flags, stream);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_bf16_linear(pw_runtime *rt, const float *input, uint32_t rows, const pw_projection *p, float *output,
+                   pw_linear_stats *stats)
+{
+    const double t0 = now_ms();
+    if (!rt || !input || !p || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (!p->bf16)
+        return fail(PW_ERR_ARGUMENT, "not a BF16 projection");
+    if (rows < 1 || rows > 32)
+        return fail(PW_ERR_ARGUMENT, "wide row count must be between one and 32");
+    const size_t n_in = (size_t)rows * p->columns, n_out = (size_t)rows * p->rows;
+    for (size_t i = 0; i < n_in; ++i)
+        if (!finite(input[i]))
+            return fail(PW_ERR_NONFINITE, "wide BF16 linear layout mismatch (non-finite input)");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    PW_TRY(reset_flags(rt));
+    bool x_f32;
+    PW_TRY(stage_input(rt, input, n_in, x_f32));
+    PW_HIP(rt->out.ensure(n_out * 4));
+    PW_TRY(enqueue_bf16_linear(rt, rt->in.p, x_f32, rows, p, (float *)rt->out.p, nullptr, 1, rt->stream));
+    PW_HIP(hipMemcpyAsync(output, rt->out.p, n_out * 4, hipMemcpyDeviceToHost, rt->stream));
+    uint32_t flags = 0;
+    PW_TRY(read_flags(rt, flags));
+    if (stats) {
+        stats->wall_ms = now_ms() - t0;
+        stats->mapped_source_bytes = 0;
+        stats->resident_source_bytes = p->weight_bytes;
+        stats->gpu_flags = flags;
+    }
+    if (flags)
+        return fail(PW_ERR_GPU_FLAGS, "wide BF16 linear Metal transaction failed (flags %u)", flags);
+    return PW_OK;
+}
+
+int pw_bf16_linear_device(pw_runtime *rt, const void *input, uint32_t input_dtype, uint32_t rows,
+                          const pw_projection *p, void *output, uint32_t output_dtype, uint32_t round_output,
+                          void *stream)
+{
+    if (!rt || !input || !p || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (!p->bf16)
+        return fail(PW_ERR_ARGUMENT, "not a BF16 projection");
+    if (rows < 1 || rows > 32)
+        return fail(PW_ERR_ARGUMENT, "wide row count must be between one and 32");
+    if (input_dtype > PW_DTYPE_BF16 || output_dtype > PW_DTYPE_F32_RAW)
+        return fail(PW_ERR_ARGUMENT, "unknown dtype");
+    if ((uintptr_t)input & 15)
+        return fail(PW_ERR_ARGUMENT, "input must be 16-byte aligned");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    float *y32 = output_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr;
+    uint16_t *y16 = output_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr;
+    const uint32_t round_f32 = output_dtype == PW_DTYPE_F32 && round_output ? 1u : 0u;
+    return enqueue_bf16_linear(rt, input, input_dtype == PW_DTYPE_F32, rows, p, y32, y16, round_f32, s);
 }
 
 int pw_quantize_fp8_group128_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows,

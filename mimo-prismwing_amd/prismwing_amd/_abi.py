@@ -82,6 +82,10 @@ SIGNATURES = {
     "pw_fp8_linear": (_i, [_vp, _u32, _f32p, _u32, _vp, _f32p, ctypes.POINTER(LinearStats)]),
     "pw_fp8_linear_device": (_i, [_vp, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp]),
     "pw_quantize_fp8_group128_device": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "pw_bf16_bind": (_i, [_vp, ctypes.POINTER(Region), _u32, _u32, ctypes.POINTER(_vp)]),
+    "pw_bf16_bind_device": (_i, [_vp, _vp, _u32, _u32, ctypes.POINTER(_vp)]),
+    "pw_bf16_linear": (_i, [_vp, _f32p, _u32, _vp, _f32p, ctypes.POINTER(LinearStats)]),
+    "pw_bf16_linear_device": (_i, [_vp, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp]),
     "pw_moe_execute": (_i, [_vp, _u32, _u32, _f32p, _u32, ctypes.POINTER(ExpertBindingC), _u32, _f32p,
                             ctypes.POINTER(MoeStats)]),
     "pw_expert_bank_create": (_i, [_vp, _u32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),

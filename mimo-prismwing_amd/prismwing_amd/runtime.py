@@ -182,6 +182,20 @@ class WideMoeRuntime:
                                               ctypes.byref(h)))
         return Projection(h.value, rows, columns)
 
+    def bind_bf16(self, weight: np.ndarray) -> Projection:
+        """A checkpoint BF16 weight [rows, columns] (uint16 bits) copied into HBM once."""
+        w = np.ascontiguousarray(weight, dtype=np.uint16)
+        if w.ndim != 2:
+            raise ValueError("weight must be [rows, columns]")
+        h = ctypes.c_void_p()
+        check(lib().pw_bf16_bind(self.handle, ctypes.byref(_region(w)), w.shape[0], w.shape[1], ctypes.byref(h)))
+        return Projection(h.value, w.shape[0], w.shape[1])
+
+    def bind_bf16_device(self, weight, rows: int, columns: int) -> Projection:
+        h = ctypes.c_void_p()
+        check(lib().pw_bf16_bind_device(self.handle, _ptr(weight), rows, columns, ctypes.byref(h)))
+        return Projection(h.value, rows, columns)
+
     def expert_bank(self, gates: Sequence[Projection], ups: Sequence[Projection],
                     downs: Sequence[Projection]) -> ExpertBank:
         n = len(gates)
@@ -208,6 +222,20 @@ class WideMoeRuntime:
         st = _abi.LinearStats()
         check(lib().pw_fp8_linear(self.handle, mode, x.ctypes.data_as(_abi._f32p), rows, binding.handle,
                                   out.ctypes.data_as(_abi._f32p), ctypes.byref(st)))
+        return WideLinearExecution(out, st.wall_ms, st.mapped_source_bytes, st.resident_source_bytes)
+
+    def execute_bf16_linear(self, input: np.ndarray, binding: Projection) -> WideLinearExecution:
+        """execute_bf16_linear (src/wide_metal_moe.rs:728-834): f32 rows -> bf16-rounded f32."""
+        x = np.ascontiguousarray(input, dtype=np.float32)
+        if x.ndim == 1:
+            x = x.reshape(1, -1)
+        if x.shape[1] != binding.columns:
+            raise _abi.PwError(-1, "wide row shape mismatch")
+        rows = x.shape[0]
+        out = np.zeros((rows, binding.rows), np.float32)
+        st = _abi.LinearStats()
+        check(lib().pw_bf16_linear(self.handle, x.ctypes.data_as(_abi._f32p), rows, binding.handle,
+                                   out.ctypes.data_as(_abi._f32p), ctypes.byref(st)))
         return WideLinearExecution(out, st.wall_ms, st.mapped_source_bytes, st.resident_source_bytes)
 
     def execute(self, input: np.ndarray, experts: Sequence[WideExpertBinding],
@@ -248,6 +276,11 @@ class WideMoeRuntime:
                           stream: Optional[int] = None):
         check(lib().pw_fp8_linear_device(self.handle, mode, _ptr(x), x_dtype, rows, proj.handle, _ptr(out),
                                          out_dtype, int(round_output), stream or 0))
+
+    def bf16_linear_device(self, proj: Projection, x, rows: int, out, x_dtype: int = DTYPE_F32,
+                           out_dtype: int = DTYPE_F32, round_output: bool = True, stream: Optional[int] = None):
+        check(lib().pw_bf16_linear_device(self.handle, _ptr(x), x_dtype, rows, proj.handle, _ptr(out), out_dtype,
+                                          int(round_output), stream or 0))
 
     def quantize_fp8_group128_device(self, x, rows: int, cols: int, codes, scales,
                                      x_dtype: int = DTYPE_F32, stream: Optional[int] = None):

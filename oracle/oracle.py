@@ -16,6 +16,7 @@ _LIB_PATH = os.path.join(_HERE, "libpw_oracle.so")
 _lib = None
 
 _u8p = ctypes.POINTER(ctypes.c_uint8)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
 _f32p = ctypes.POINTER(ctypes.c_float)
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 _u64p = ctypes.POINTER(ctypes.c_uint64)
@@ -54,6 +55,7 @@ def lib():
         L.pwo_gemm_mode_a.argtypes = [_u8p, _f32p, _sz, _sz, _f32p, _sz, _f32p]
         L.pwo_gemm_mode_b_equation.argtypes = [_u8p, _f32p, _sz, _sz, _u8p, _f32p, _sz, _f32p]
         L.pwo_fp8_linear_mode_b.argtypes = [_u8p, _f32p, _sz, _sz, _f32p, _sz, _f32p]
+        L.pwo_bf16_linear.argtypes = [_u16p, _sz, _sz, _f32p, _sz, _f32p, _f32p]
         L.pwo_swiglu_f32.argtypes = [_f32p, _f32p, _f32p, _sz]
         L.pwo_swiglu_f32.restype = None
         L.pwo_swiglu_bf16_staged.argtypes = [_f32p, _f32p, _f32p, _sz]
@@ -124,6 +126,18 @@ def gemm_mode_a(w: np.ndarray, s: np.ndarray, x: np.ndarray) -> np.ndarray:
     if rc != 0:
         raise ValueError(f"gemm_mode_a failed: {rc}")
     return y
+
+
+def bf16_linear(w_bits: np.ndarray, x: np.ndarray, raw: bool = False):
+    """W [n, k] bf16 bits (uint16), x [rows, k] f32 -> bf16-rounded y [rows, n] (and the raw sums)."""
+    w = _c(w_bits, np.uint16); x = _c(np.atleast_2d(x), np.float32)
+    n, k = w.shape
+    y = np.zeros((x.shape[0], n), np.float32)
+    y_raw = np.zeros_like(y)
+    rc = lib().pwo_bf16_linear(_p(w, _u16p), n, k, _p(x, _f32p), x.shape[0], _p(y, _f32p), _p(y_raw, _f32p))
+    if rc != 0:
+        raise ValueError(f"bf16_linear failed: {rc}")
+    return (y, y_raw) if raw else y
 
 
 def gemm_mode_b_equation(w, s, q, a) -> np.ndarray:

@@ -117,6 +117,41 @@ static int weights_finite(const uint8_t *w, size_t count)
     return 1;
 }
 
+/* bf16_linear (src/text_endpoint.rs:3347-3380): decode the BF16 tensor (bits << 16, exact), f32
+ * GEMM, round every output to bf16; the GPU form execute_bf16_linear (src/wide_metal_moe.rs:
+ * 728-834) checks the input is finite. The reference's SGEMM order is closed; this restatement
+ * sums sequentially over columns with separate multiply and add (like mapped_fp8_gemv).
+ * y_raw (optional) receives the sums before rounding. */
+int pwo_bf16_linear(const uint16_t *w, size_t n, size_t k, const float *x, size_t rows, float *y,
+                    float *y_raw)
+{
+    if (w == NULL || x == NULL || y == NULL || n == 0 || k == 0 || rows == 0)
+        return -1;
+    for (size_t i = 0; i < rows * k; ++i)
+        if (!isfinite(x[i]))
+            return -2;
+    for (size_t p = 0; p < rows; ++p) {
+        const float *input = x + p * k;
+        for (size_t r = 0; r < n; ++r) {
+            const uint16_t *row = w + r * k;
+            float sum = 0.0f;
+            for (size_t c = 0; c < k; ++c) {
+                const uint32_t bits = (uint32_t)row[c] << 16;
+                float wv;
+                memcpy(&wv, &bits, 4);
+                sum += wv * input[c];
+            }
+            if (y_raw)
+                y_raw[p * n + r] = sum;
+            const float rounded = pwo_round_bf16(sum);
+            if (!isfinite(rounded))
+                return -3;
+            y[p * n + r] = rounded;
+        }
+    }
+    return 0;
+}
+
 /* src/lib.rs:1272-1309 (mapped_fp8_gemv; fixture form block_fp8_gemv :7469-7493) generalised to
  * `rows` activation rows and a partial trailing 128-row block: sequential over columns,
  * sum += decoded * scale * activation, f32, no fused multiply-add. Validation follows

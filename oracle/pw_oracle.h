@@ -15,6 +15,8 @@
  *   pwo_encode_e4m3fn        golden pw0053 codes; brute-force nearest search near every midpoint
  *   pwo_dynamic_fp8          golden pw0053-dynamic-fp8-activation.json (scales, codes, dequant bits)
  *   pwo_gemm_mode_a          real mtp-gate-fp8-gemv.json (abs 2e-7), closed form 384/896, f64 brute force
+ *   pwo_bf16_linear          closed forms (exact sums of powers of two, bf16 rounding of a tie), f64
+ *                            brute force, equality with pwo_gemm_mode_a on e4m3 values with unit scales
  *   pwo_gemm_mode_b_equation closed-form probe inputs vs f64 brute force; equals mode A when the
  *                            activation codes are exact and scales are 1
  *   pwo_fp8_linear_mode_b    f64 brute force on tiny shapes; bf16-rounding idempotence
@@ -60,6 +62,11 @@ int pwo_dynamic_fp8(const float *input, size_t rows, size_t cols, uint8_t *codes
  * Returns -1 on shape error, -2 on non-finite input/scale/weight (0x7f/0xff), -3 non-finite out. */
 int pwo_gemm_mode_a(const uint8_t *w, const float *s, size_t n, size_t k, const float *x,
                     size_t rows, float *y);
+/* BF16 linear: y[p, r] = round_bf16(sum_c bf16(W[r, c]) * x[p, c]), f32, sequential over c.
+ * W [n x k] bf16 bits, x [rows x k] f32 -> y [rows x n]; y_raw (may be NULL) gets the sums.
+ * Returns -1 on shape error, -2 on non-finite input, -3 on a non-finite output. */
+int pwo_bf16_linear(const uint16_t *w, size_t n, size_t k, const float *x, size_t rows, float *y,
+                    float *y_raw);
 /* Block-scaled equation of the GPU mode-B kernels:
  * y[p, r] = sum_b (sum_{c in b} dec(W) * dec(q[p, c])) * S[r/128, b] * a[p, b], blocks ascending. */
 int pwo_gemm_mode_b_equation(const uint8_t *w, const float *s, size_t n, size_t k,

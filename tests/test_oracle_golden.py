@@ -383,3 +383,54 @@ def test_swa_qkv_maps_known_answers():
     for r, want in src.items():
         assert O.swa_qkv_source_row(r) == want
     assert O.swa_qkv_source_row(14848) == -1
+
+
+# ---------------------------------------------------------------- f3 BF16 linear
+def _bf16_bits(values):
+    return (np.asarray(values, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def test_bf16_linear_sequential_unfused_known_answers():
+    """Sums whose f32 value fixes the restatement: separate multiply and add, sequential columns."""
+    a = 1 + 2 ** -7
+    b = 1 + 2 ** -17
+    # (1 + 2^-7)(1 + 2^-17) = 1 + 2^-7 + 2^-17 + 2^-24 rounds (tie to even) to 1 + 2^-7 + 2^-17, so the
+    # unfused sum is exactly 0; a fused multiply-add would leave 2^-24
+    w = _bf16_bits([[1.0, a]])
+    x = np.array([[-(1 + 2 ** -7 + 2 ** -17), b]], np.float32)
+    y, raw = O.bf16_linear(w, x, raw=True)
+    assert raw[0, 0] == 0.0 and y[0, 0] == 0.0
+    # sequential order: 2^24 + 1 rounds back to 2^24 twice (exact sum 2^24 + 2)
+    w = _bf16_bits([[1.0, 1.0, 1.0]])
+    y, raw = O.bf16_linear(w, np.array([[2.0 ** 24, 1.0, 1.0]], np.float32), raw=True)
+    assert raw[0, 0] == 2.0 ** 24
+    # output rounding to bf16, ties to even: 1 + 2^-8 -> 1, 1 + 3 * 2^-8 -> 1 + 2^-6
+    w = _bf16_bits([[1.0, 1.0]])
+    y = O.bf16_linear(w, np.array([[1.0, 2.0 ** -8], [1.0, 3 * 2.0 ** -8]], np.float32))
+    assert y[0, 0] == 1.0 and y[1, 0] == 1 + 2 ** -6
+
+
+def test_bf16_linear_equals_mode_a_on_e4m3_values_with_unit_scales():
+    """bf16 weights holding e4m3 values are the mode A projection with unit scales, bit for bit."""
+    rng = np.random.default_rng(8)
+    n, k = 130, 256
+    codes = rng.integers(0, 256, (n, k)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x3C
+    dec = np.vectorize(O.decode_e4m3fn, otypes=[np.float32])(codes)
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    ya = O.gemm_mode_a(codes, np.ones((2, 2), np.float32), x)
+    _, raw = O.bf16_linear(_bf16_bits(dec), x, raw=True)
+    assert np.array_equal(ya.view(np.uint32), raw.view(np.uint32))
+
+
+def test_bf16_linear_f64_brute_force():
+    rng = np.random.default_rng(9)
+    w = _bf16_bits(rng.standard_normal((70, 384)).astype(np.float32) * 0.05)
+    x = rng.standard_normal((4, 384)).astype(np.float32)
+    y, raw = O.bf16_linear(w, x, raw=True)
+    wf = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    want = x.astype(np.float64) @ wf.T
+    assert np.max(np.abs(raw - want)) <= 1e-5 * np.max(np.abs(want))
+    assert np.array_equal(y.view(np.uint32), np.vectorize(O.round_bf16, otypes=[np.float32])(raw).view(np.uint32))
+    with pytest.raises(ValueError):
+        O.bf16_linear(w, np.full((1, 384), np.nan, np.float32))
