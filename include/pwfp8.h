@@ -71,6 +71,7 @@ enum { PW_RUNTIME_FUSED_GATE_UP = 1 };
 typedef struct pw_runtime pw_runtime;
 typedef struct pw_projection pw_projection;
 typedef struct pw_expert_bank pw_expert_bank;
+typedef struct pw_safetensors pw_safetensors;
 
 /* WideSourceRegion (src/wide_metal_moe.rs:38-78): a tensor inside a larger (e.g. mmapped,
  * page-rounded) host region. */
@@ -213,6 +214,36 @@ int pw_bf16_linear_device(pw_runtime *rt, const void *input, uint32_t input_dtyp
  * scales [rows x cols/128]. Non-finite inputs raise PW_FLAG_QUANT_NONFINITE. */
 int pw_quantize_fp8_group128_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows,
                                     uint32_t cols, uint8_t *codes, float *scales, void *stream);
+
+/* ---- checkpoint files ------------------------------------------------------------------------ */
+/* One tensor of a safetensors file: dtype string ("F8_E4M3", "F32", "BF16", ...), shape, and a
+ * region over its bytes inside the read-only file mapping (valid until pw_safetensors_close). */
+typedef struct {
+    char dtype[16];
+    uint32_t rank;
+    uint64_t shape[8];
+    pw_region region;
+} pw_tensor_info;
+
+/* MappedSafetensors::open (src/lib.rs:783-905): maps the file read-only and parses its header:
+ * 8-byte little-endian length (nonzero, <= 256 MiB, a multiple of 8, inside the file), a JSON object
+ * of {dtype, shape, data_offsets} per tensor plus an optional __metadata__ object; rejects unknown
+ * dtypes, empty or zero shapes, sizes that disagree with shape x dtype, payloads past the file,
+ * overlapping payloads, duplicate names and files without tensors (PW_ERR_LAYOUT). */
+int pw_safetensors_open(const char *path, pw_safetensors **out);
+void pw_safetensors_close(pw_safetensors *st);
+uint32_t pw_safetensors_count(const pw_safetensors *st);
+/* MappedSafetensors::tensor (src/lib.rs:907-930): PW_ERR_ARGUMENT "tensor is absent" if missing. */
+int pw_safetensors_tensor(const pw_safetensors *st, const char *name, pw_tensor_info *info);
+/* A layer's routed experts from checkpoint files into one HBM allocation the bank owns: for each
+ * expert e < n_experts, model.layers.{layer}.mlp.experts.{e}.{gate,up,down}_proj.weight and
+ * ..._scale_inv (the names of src/text_endpoint.rs:4785-4845), looked up across the files in order,
+ * validated like validate_fp8_views_internal (src/lib.rs:1217-1270: F8_E4M3 rank two of shape
+ * [intermediate x hidden] / [hidden x intermediate], F32 scale grids [rows/128 x cols/128], finite
+ * scales, and with scan_codes no 0x7f/0xff code), then copied once. */
+int pw_expert_bank_from_safetensors(pw_runtime *rt, const pw_safetensors *const *files, uint32_t n_files,
+                                    uint32_t layer, uint32_t n_experts, uint32_t hidden, uint32_t intermediate,
+                                    int scan_codes, pw_expert_bank **out);
 
 /* ---- routed MoE ---------------------------------------------------------------------------- */
 /* WideMetalMoeRuntime::execute / execute_fused_gate_up (src/wide_metal_moe.rs:836-1314): input

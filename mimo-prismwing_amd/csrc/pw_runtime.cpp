@@ -18,6 +18,7 @@
 
 #include "../../include/pwfp8.h"
 #include "pw_launch.h"
+#include "pw_internal.h"
 #include "pw_topk.h"
 #include "pw_numerics.h"
 
@@ -37,7 +38,9 @@ const char *const kKernelNames[pw::K_COUNT] = {
 
 thread_local std::string g_error;
 
-int fail(int code, const char *fmt, ...)
+}  // namespace
+
+int pw::fail(int code, const char *fmt, ...)
 {
     char buf[512];
     va_list ap;
@@ -47,6 +50,10 @@ int fail(int code, const char *fmt, ...)
     g_error = buf;
     return code;
 }
+
+using pw::fail;
+
+namespace {
 
 #define PW_HIP(call)                                                                            \
     do {                                                                                        \
@@ -141,6 +148,8 @@ struct pw_expert_bank {
     pw_runtime *rt = nullptr;
     ExpertPtrs *table = nullptr;  // device [E]
     uint32_t n_experts = 0, hidden = 0, intermediate = 0;
+    void *owned = nullptr;        // weights and scales the bank owns (checkpoint banks)
+    uint64_t owned_bytes = 0;
 };
 
 namespace {
@@ -1043,8 +1052,41 @@ void pw_expert_bank_release(pw_expert_bank *b)
         (void)hipSetDevice(b->rt->device);
     if (b->table)
         (void)hipFree(b->table);
+    if (b->owned)
+        (void)hipFree(b->owned);
     delete b;
 }
+
+}  // extern "C"
+
+int pw::set_device_of(pw_runtime *rt)
+{
+    const hipError_t e = hipSetDevice(rt->device);
+    return e == hipSuccess ? PW_OK : fail(PW_ERR_DEVICE, "hipSetDevice: %s", hipGetErrorString(e));
+}
+
+int pw::make_owned_bank(pw_runtime *rt, const std::vector<ExpertPtrs> &table, uint32_t hidden, uint32_t intermediate,
+                        void *owned, uint64_t owned_bytes, pw_expert_bank **out)
+{
+    pw_expert_bank *b = new pw_expert_bank;
+    b->rt = rt;
+    b->n_experts = (uint32_t)table.size();
+    b->hidden = hidden;
+    b->intermediate = intermediate;
+    b->owned = owned;
+    b->owned_bytes = owned_bytes;
+    hipError_t e = hipMalloc(&b->table, table.size() * sizeof(ExpertPtrs));
+    if (e == hipSuccess)
+        e = hipMemcpy(b->table, table.data(), table.size() * sizeof(ExpertPtrs), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        pw_expert_bank_release(b);
+        return fail(PW_ERR_DEVICE, "bank upload failed: %s", hipGetErrorString(e));
+    }
+    *out = b;
+    return PW_OK;
+}
+
+extern "C" {
 
 int pw_expert_bank_shape(const pw_expert_bank *b, uint32_t *n, uint32_t *h, uint32_t *i)
 {

@@ -8,14 +8,14 @@ of src/text_endpoint.rs:4342-4473. Errors raise ``PwError`` (the reference retur
 """
 from ._abi import (DTYPE_BF16, DTYPE_F32, DTYPE_F32_RAW, FLAG_ROUTE, FLAG_SCHEDULE, LAYOUT_FULL_QKV_TP4,
                    LAYOUT_PLAIN, LAYOUT_SWA_QKV_TP4, MODE_A, MODE_B, PwError, lib)
-from .runtime import (ExpertBank, Projection, WideExpertBinding, WideLinearExecution,
+from .runtime import (ExpertBank, Projection, Safetensors, WideExpertBinding, WideLinearExecution,
                       WideMoeExecution, WideMoeRuntime, full_qkv_scale_row, full_qkv_source_row,
                       noaux_routes, route_from_logits, swa_qkv_source_row, topk_unsorted)
 
 __all__ = [
     "DTYPE_BF16", "DTYPE_F32", "DTYPE_F32_RAW", "FLAG_ROUTE", "FLAG_SCHEDULE", "LAYOUT_FULL_QKV_TP4",
     "LAYOUT_PLAIN", "LAYOUT_SWA_QKV_TP4",
-    "MODE_A", "MODE_B", "PwError", "lib", "ExpertBank", "Projection", "WideExpertBinding",
+    "MODE_A", "MODE_B", "PwError", "lib", "ExpertBank", "Projection", "Safetensors", "WideExpertBinding",
     "WideLinearExecution", "WideMoeExecution", "WideMoeRuntime", "full_qkv_scale_row",
     "full_qkv_source_row", "noaux_routes", "route_from_logits", "swa_qkv_source_row",
     "topk_unsorted",

@@ -52,6 +52,10 @@ class ExpertBindingC(ctypes.Structure):
                 ("gate", _vp), ("up", _vp), ("down", _vp)]
 
 
+class TensorInfo(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_char * 16), ("rank", _u32), ("shape", ctypes.c_uint64 * 8), ("region", Region)]
+
+
 class LinearStats(ctypes.Structure):
     _fields_ = [("wall_ms", ctypes.c_double), ("mapped_source_bytes", ctypes.c_uint64),
                 ("resident_source_bytes", ctypes.c_uint64), ("gpu_flags", _u32)]
@@ -82,6 +86,12 @@ SIGNATURES = {
     "pw_fp8_linear": (_i, [_vp, _u32, _f32p, _u32, _vp, _f32p, ctypes.POINTER(LinearStats)]),
     "pw_fp8_linear_device": (_i, [_vp, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp]),
     "pw_quantize_fp8_group128_device": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "pw_safetensors_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "pw_safetensors_close": (None, [_vp]),
+    "pw_safetensors_count": (_u32, [_vp]),
+    "pw_safetensors_tensor": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(TensorInfo)]),
+    "pw_expert_bank_from_safetensors": (_i, [_vp, ctypes.POINTER(_vp), _u32, _u32, _u32, _u32, _u32, _i,
+                                             ctypes.POINTER(_vp)]),
     "pw_bf16_bind": (_i, [_vp, ctypes.POINTER(Region), _u32, _u32, ctypes.POINTER(_vp)]),
     "pw_bf16_bind_device": (_i, [_vp, _vp, _u32, _u32, ctypes.POINTER(_vp)]),
     "pw_bf16_linear": (_i, [_vp, _f32p, _u32, _vp, _f32p, ctypes.POINTER(LinearStats)]),

@@ -100,6 +100,44 @@ class ExpertBank:
             pass
 
 
+class Safetensors:
+    """A safetensors file mapped read-only with its header parsed (MappedSafetensors, src/lib.rs:783-972)."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(lib().pw_safetensors_open(str(path).encode(), ctypes.byref(h)))
+        self.handle = h.value
+        self.path = str(path)
+
+    def __len__(self) -> int:
+        return int(lib().pw_safetensors_count(self.handle))
+
+    def tensor(self, name: str):
+        """(dtype, shape, bytes) of one tensor; the bytes are a copy of the mapped payload."""
+        info = _abi.TensorInfo()
+        check(lib().pw_safetensors_tensor(self.handle, name.encode(), ctypes.byref(info)))
+        shape = tuple(int(info.shape[i]) for i in range(info.rank))
+        data = ctypes.string_at(info.region.bytes, info.region.tensor_bytes)
+        return info.dtype.decode(), shape, data
+
+    def close(self):
+        if self.handle:
+            lib().pw_safetensors_close(self.handle)
+            self.handle = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class WideMoeRuntime:
     """One runtime per device; calls are serialised by the caller like the reference's &self."""
 
@@ -181,6 +219,15 @@ class WideMoeRuntime:
         check(lib().pw_projection_bind_device(self.handle, _ptr(weight), _ptr(scale), rows, columns,
                                               ctypes.byref(h)))
         return Projection(h.value, rows, columns)
+
+    def expert_bank_from_safetensors(self, files: Sequence["Safetensors"], layer: int, n_experts: int,
+                                     hidden: int, intermediate: int, scan_codes: bool = True) -> ExpertBank:
+        """One layer's routed experts from checkpoint files, copied once into a device bank it owns."""
+        arr = (ctypes.c_void_p * len(files))(*[f.handle for f in files])
+        h = ctypes.c_void_p()
+        check(lib().pw_expert_bank_from_safetensors(self.handle, arr, len(files), layer, n_experts, hidden,
+                                                    intermediate, int(scan_codes), ctypes.byref(h)))
+        return ExpertBank(h.value, n_experts, hidden, intermediate)
 
     def bind_bf16(self, weight: np.ndarray) -> Projection:
         """A checkpoint BF16 weight [rows, columns] (uint16 bits) copied into HBM once."""

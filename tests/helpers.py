@@ -93,3 +93,24 @@ def within_one_bf16_ulp(got: np.ndarray, ref: np.ndarray) -> bool:
     """bf16 outputs differ from the reference's bf16 outputs by at most one rounding step."""
     d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
     return bool(np.all(d <= bf16_ulp(np.maximum(np.abs(got), np.abs(ref))) * 1.0000001))
+
+
+def write_safetensors(path, tensors, metadata=None, header_pad=True, raw_header=None):
+    """Writes a safetensors file: tensors maps name -> (dtype string, shape, bytes), payloads packed in
+    the given order. raw_header replaces the JSON header text (for malformed-file tests)."""
+    import json
+    import struct
+    header, payload, off = {}, b"", 0
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    for name, (dtype, shape, data) in tensors.items():
+        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [off, off + len(data)]}
+        payload += data
+        off += len(data)
+    text = raw_header if raw_header is not None else json.dumps(header, separators=(",", ":"))
+    hb = text.encode()
+    if header_pad:
+        hb += b" " * ((-len(hb)) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(hb)) + hb + payload)
+    return path
