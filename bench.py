@@ -253,6 +253,34 @@ def projection_legs(torch, rt, bank, P, WL, calls=200):
             rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
         out[f"bf16_o_proj_w{width}"] = rec
     del bprojs, wb
+    # dense layer-0 FP8 MLP: gate/up [16384 x 4096], down [4096 x 16384] as one-expert banks, 3 copies
+    dh, di, copies = 4096, 16384, 3
+    keep, banks = [], []
+    for c in range(copies):
+        projs = []
+        for j, (rows_, cols_) in enumerate(((di, dh), (di, dh), (dh, di))):
+            w = torch.empty((rows_, cols_), dtype=torch.uint8, device="cuda")
+            sc = torch.empty((rows_ // 128, cols_ // 128), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            rt.synth_scales(sc, sc.numel(), WL.SEED_BASE + 700 + 10 * c + 2 * j)
+            rt.synth_fp8(w, sc, rows_, cols_, WL.SEED_BASE + 701 + 10 * c + 2 * j)
+            keep += [w, sc]
+            projs.append(rt.bind_projection_device(w, sc, rows_, cols_))
+        banks.append(rt.expert_bank([projs[0]], [projs[1]], [projs[2]]))
+        keep.append(projs)
+    weight_bytes = 3 * dh * di + 3 * (dh // 128) * (di // 128) * 4
+    for mode, tag in ((P.MODE_A, "a"), (P.MODE_B, "b")):
+        for width in (1, 8):
+            x = _bf16_x(torch, WL, width, dh, WL.SEED_BASE + 720 + width)
+            y = torch.empty((width, dh), dtype=torch.int16, device="cuda")
+            alg = weight_bytes + width * dh * 2 * 2
+            rec = {"algorithmic_bytes": alg}
+            for label, pick in (("hbm_cold", lambda i: banks[i % copies]), ("mall_warm", lambda i: banks[0])):
+                us = _time_calls(torch, rt, lambda i, st: rt.expert_forward_device(
+                    pick(i), 0, x, width, y, mode=mode, out_dtype=P.DTYPE_BF16, stream=st), calls // 2)
+                rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+            out[f"dense_mlp_mode_{tag}_w{width}"] = rec
+    del banks, keep
     return out
 
 
