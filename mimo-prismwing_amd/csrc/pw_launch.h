@@ -134,8 +134,6 @@ inline void timer_end(int slot, hipStream_t s)
         tl_timer->end(slot, s);
 }
 
-int pick_ksplit(uint32_t n_tiles, uint32_t blocks);
-
 // x: `planes` bf16 planes [planes][W][K] (1: bf16 activations, 3: f32 split by launch_split_planes)
 void launch_linear_a(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, int planes,
                      uint32_t W, uint32_t K, float *y32, uint16_t *y16, uint32_t N,

@@ -31,63 +31,84 @@ struct Acc {
 // ------------------------------------------------------------------------------------ mode A
 // Activations arrive as NS bf16 planes [NS][W][K] (NS = 1: bf16 input; NS = 3: an f32 input split
 // exactly into hi + mid + lo), so the inner loop does no conversion work on them.
-template <int NS, int KSPLIT, int NT>
+template <int NS, int KSPLIT, int NT, int BPW>
 __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
     const ProjTile *__restrict__ tiles, uint32_t n_tiles, const uint16_t *__restrict__ x, uint32_t W,
     uint32_t K, float *__restrict__ y_f32, uint16_t *__restrict__ y_bf16, uint32_t N,
     uint32_t round_f32)
 {
     const size_t plane = (size_t)W * K;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r16 = lane & 15;
     __shared__ f32x4 red[KSPLIT > 1 ? KSPLIT : 1][NT][64];
     const uint32_t blocks = K >> 7;
-    const uint32_t b_begin = wave * blocks / KSPLIT, b_end = (wave + 1) * blocks / KSPLIT;
 
     for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
         const ProjTile tile = tiles[t];
         const bool row_ok = (uint32_t)r16 < tile.valid;
-        const uint8_t *wrow = tile.w + (size_t)r16 * K;
+        const uint8_t *wrow = tile.w + (size_t)r16 * K + q * 16;
         f32x4 total[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
             total[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-        for (uint32_t b = b_begin; b < b_end; ++b) {
-            f32x4 acc[NT];
+        // K in rounds of KSPLIT * BPW blocks (one round whenever K <= 128 * KSPLIT * BPW): wave w
+        // takes blocks [round + w * BPW, round + (w + 1) * BPW), and issues every weight load and
+        // block scale of them before its first MFMA
+        for (uint32_t round = 0; round < blocks; round += KSPLIT * BPW) {
+            const uint32_t b0 = round + (uint32_t)wave * BPW;
+            uint4 wv[BPW][2];
+            float sc[BPW];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-                acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const uint32_t col = (b << 7) + half * 64 + q * 16;
-                uint4 wv = make_uint4(0, 0, 0, 0);
-                if (row_ok)
-                    wv = load_global16(wrow + col);
-                const bf16x8 a0 = fp8x8_to_bf16x8(wv.x, wv.y);
-                const bf16x8 a1 = fp8x8_to_bf16x8(wv.z, wv.w);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    const uint32_t token = nt * 16 + r16;
-#pragma unroll
-                    for (int s = 0; s < NS; ++s) {
-                        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
-                        if (token < W) {
-                            const uint4 *xp = (const uint4 *)(x + s * plane + (size_t)token * K + col);
-                            x0 = xp[0];
-                            x1 = xp[1];
-                        }
-                        acc[nt] = mfma_bf16_16x16x32(a0, bf16x8_from_u4(x0), acc[nt]);
-                        acc[nt] = mfma_bf16_16x16x32(a1, bf16x8_from_u4(x1), acc[nt]);
+            for (int j = 0; j < BPW; ++j) {
+                const uint32_t b = b0 + j;
+                wv[j][0] = make_uint4(0, 0, 0, 0);
+                wv[j][1] = wv[j][0];
+                sc[j] = 0.f;
+                if (b < blocks) {
+                    if (row_ok) {
+                        wv[j][0] = load_global16(wrow + ((size_t)b << 7));
+                        wv[j][1] = load_global16(wrow + ((size_t)b << 7) + 64);
                     }
+                    sc[j] = tile.s[b];
                 }
             }
-            const float sc = tile.s[b];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
+            for (int j = 0; j < BPW; ++j) {
+                const uint32_t b = b0 + j;
+                if (b >= blocks)
+                    break;
+                f32x4 acc[NT];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    total[nt][i] = __builtin_fmaf(sc, acc[nt][i], total[nt][i]);
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const uint32_t col = (b << 7) + half * 64 + q * 16;
+                    const bf16x8 a0 = fp8x8_to_bf16x8(wv[j][half].x, wv[j][half].y);
+                    const bf16x8 a1 = fp8x8_to_bf16x8(wv[j][half].z, wv[j][half].w);
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const uint32_t token = nt * 16 + r16;
+#pragma unroll
+                        for (int s = 0; s < NS; ++s) {
+                            uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+                            if (token < W) {
+                                const uint4 *xp = (const uint4 *)(x + s * plane + (size_t)token * K + col);
+                                x0 = xp[0];
+                                x1 = xp[1];
+                            }
+                            acc[nt] = mfma_bf16_16x16x32(a0, bf16x8_from_u4(x0), acc[nt]);
+                            acc[nt] = mfma_bf16_16x16x32(a1, bf16x8_from_u4(x1), acc[nt]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        total[nt][i] = __builtin_fmaf(sc[j], acc[nt][i], total[nt][i]);
+            }
         }
 
         if constexpr (KSPLIT > 1) {
@@ -133,53 +154,72 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
 }
 
 // ------------------------------------------------------------------------------------ mode B
-template <int KSPLIT, int NT>
+template <int KSPLIT, int NT, int BPW>
 __global__ __launch_bounds__(64 * KSPLIT) void linear_b_kernel(
     const ProjTile *__restrict__ tiles, uint32_t n_tiles, const uint8_t *__restrict__ codes,
     const float *__restrict__ act_scales, uint32_t W, uint32_t K, float *__restrict__ y_f32,
     uint16_t *__restrict__ y_bf16, uint32_t N, uint32_t round_f32)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r16 = lane & 15;
     __shared__ f32x4 red[KSPLIT > 1 ? KSPLIT : 1][NT][64];
     const uint32_t blocks = K >> 7;
-    const uint32_t b_begin = wave * blocks / KSPLIT, b_end = (wave + 1) * blocks / KSPLIT;
 
     for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
         const ProjTile tile = tiles[t];
         const bool row_ok = (uint32_t)r16 < tile.valid;
-        const uint8_t *wrow = tile.w + (size_t)r16 * K;
+        const uint8_t *wrow = tile.w + (size_t)r16 * K + q * 32;
         f32x4 total[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
             total[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (uint32_t b = b_begin; b < b_end; ++b) {
-            const uint32_t col = (b << 7) + q * 32;
-            uint4 w0 = make_uint4(0, 0, 0, 0), w1 = w0;
-            if (row_ok) {
-                w0 = load_global16(wrow + col);
-                w1 = load_global16(wrow + col + 16);
-            }
-            const i32x8 wa = {(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
-                              (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
-            const float sw = tile.s[b];
+        // K in rounds of KSPLIT * BPW blocks, every weight load of a wave's blocks issued first
+        // (as in linear_a_kernel)
+        for (uint32_t round = 0; round < blocks; round += KSPLIT * BPW) {
+            const uint32_t b0 = round + (uint32_t)wave * BPW;
+            uint4 wv[BPW][2];
+            float sw[BPW];
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const uint32_t token = nt * 16 + r16;
-                uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
-                float sa = 0.f;
-                if (token < W) {
-                    const uint4 *cp = (const uint4 *)(codes + (size_t)token * K + col);
-                    c0 = cp[0];
-                    c1 = cp[1];
-                    sa = act_scales[(size_t)token * blocks + b];
+            for (int j = 0; j < BPW; ++j) {
+                const uint32_t b = b0 + j;
+                wv[j][0] = make_uint4(0, 0, 0, 0);
+                wv[j][1] = wv[j][0];
+                sw[j] = 0.f;
+                if (b < blocks) {
+                    if (row_ok) {
+                        wv[j][0] = load_global16(wrow + ((size_t)b << 7));
+                        wv[j][1] = load_global16(wrow + ((size_t)b << 7) + 16);
+                    }
+                    sw[j] = tile.s[b];
                 }
-                const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
-                                  (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
-                const f32x4 p = mfma_fp8_16x16x128(wa, xb, f32x4{0.f, 0.f, 0.f, 0.f});
+            }
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    total[nt][i] = __builtin_fmaf(p[i] * sw, sa, total[nt][i]);
+            for (int j = 0; j < BPW; ++j) {
+                const uint32_t b = b0 + j;
+                if (b >= blocks)
+                    break;
+                const uint32_t col = (b << 7) + q * 32;
+                const i32x8 wa = {(int)wv[j][0].x, (int)wv[j][0].y, (int)wv[j][0].z, (int)wv[j][0].w,
+                                  (int)wv[j][1].x, (int)wv[j][1].y, (int)wv[j][1].z, (int)wv[j][1].w};
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const uint32_t token = nt * 16 + r16;
+                    uint4 c0 = make_uint4(0, 0, 0, 0), c1 = c0;
+                    float sa = 0.f;
+                    if (token < W) {
+                        const uint4 *cp = (const uint4 *)(codes + (size_t)token * K + col);
+                        c0 = cp[0];
+                        c1 = cp[1];
+                        sa = act_scales[(size_t)token * blocks + b];
+                    }
+                    const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
+                                      (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
+                    const f32x4 p = mfma_fp8_16x16x128(wa, xb, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        total[nt][i] = __builtin_fmaf(p[i] * sw[j], sa, total[nt][i]);
+                }
             }
         }
         if constexpr (KSPLIT > 1) {
@@ -293,72 +333,107 @@ void launch_split_planes(const float *x, uint32_t n, uint16_t *planes, hipStream
     hipLaunchKernelGGL(split_planes_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, x, n, planes);
 }
 
-template <int NS, int KSPLIT>
-static void launch_a_ks(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, uint32_t W,
-                        uint32_t K, float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32,
-                        hipStream_t stream)
+// K split of a 16-row tile: KSPLIT waves x BPW 128-column blocks per wave, every weight byte of a
+// wave requested before its first MFMA. KSPLIT grows until the launch has about eight waves per
+// CU (2048 on 256 CUs) and until eight blocks per wave cover K in one round; a wave keeps at least
+// one block. At most 16 waves (8 for batches of more than 16 rows, whose two token tiles need more
+// than the 128 registers a 1024-thread workgroup leaves).
+struct LinearSplit {
+    int ks, bpw;
+};
+
+static LinearSplit pick_split(uint32_t blocks, uint32_t W, uint32_t n_tiles)
 {
-    const int grid = grid_for(n_tiles, 65535);
-    if (W <= 16)
-        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1>), dim3(grid), dim3(64 * KSPLIT), 0,
-                           stream, tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
-    else
-        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 2>), dim3(grid), dim3(64 * KSPLIT), 0,
-                           stream, tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+    const uint32_t max_ks = W <= 16 ? 16u : 8u;
+    uint32_t ks = 1;
+    while (ks < max_ks && ((uint64_t)ks * n_tiles < 2048 || ks * 8 < blocks))
+        ks *= 2;
+    while (ks > 1 && ks / 2 >= blocks)
+        ks /= 2;
+    uint32_t bpw = 1;
+    while (ks * bpw < blocks && bpw < 8)
+        bpw *= 2;
+    return LinearSplit{(int)ks, (int)bpw};
 }
 
-int pick_ksplit(uint32_t n_tiles, uint32_t blocks)
+template <int NS, int KSPLIT, int BPW>
+static void launch_a_split(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, uint32_t W, uint32_t K,
+                           float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32, hipStream_t stream)
 {
-    // enough waves to cover 256 CUs several times over; every wave keeps >= 2 blocks
-    if (n_tiles < 512 && blocks % 8 == 0 && blocks >= 16)
-        return 8;
-    if (blocks % 4 == 0 && blocks >= 8)
-        return 4;
-    if (blocks % 2 == 0)
-        return 2;
-    return 1;
+    const int grid = grid_for(n_tiles, 65535);
+    if constexpr (KSPLIT == 16)
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
+                           n_tiles, x, W, K, y32, y16, N, round_f32);
+    else if (W <= 16)
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
+                           n_tiles, x, W, K, y32, y16, N, round_f32);
+    else
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 2, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
+                           n_tiles, x, W, K, y32, y16, N, round_f32);
+}
+
+template <int NS>
+static void launch_a_planes(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, uint32_t W, uint32_t K,
+                            float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32, hipStream_t stream)
+{
+    const LinearSplit sp = pick_split(K >> 7, W, n_tiles);
+#define PW_A(KS, BPW) launch_a_split<NS, KS, BPW>(tiles, n_tiles, x, W, K, y32, y16, N, round_f32, stream)
+#define PW_A_BPW(KS)                                                                                       \
+    do {                                                                                                   \
+        if (sp.bpw == 8) PW_A(KS, 8); else if (sp.bpw == 4) PW_A(KS, 4); else if (sp.bpw == 2) PW_A(KS, 2); \
+        else PW_A(KS, 1);                                                                                  \
+    } while (0)
+    if (sp.ks == 16) PW_A_BPW(16); else if (sp.ks == 8) PW_A_BPW(8); else if (sp.ks == 4) PW_A_BPW(4);
+    else if (sp.ks == 2) PW_A_BPW(2); else PW_A_BPW(1);
+#undef PW_A_BPW
+#undef PW_A
 }
 
 void launch_linear_a(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, int planes,
                      uint32_t W, uint32_t K, float *y32, uint16_t *y16, uint32_t N,
                      uint32_t round_f32, hipStream_t stream)
 {
-    const int ks = pick_ksplit(n_tiles, K >> 7);
     const int t = timer_begin(K_LINEAR_A, stream);
-#define PW_A(NS, KS) launch_a_ks<NS, KS>(tiles, n_tiles, x, W, K, y32, y16, N, round_f32, stream)
-    if (planes == 3) {
-        if (ks == 8) PW_A(3, 8); else if (ks == 4) PW_A(3, 4); else if (ks == 2) PW_A(3, 2); else PW_A(3, 1);
-    } else {
-        if (ks == 8) PW_A(1, 8); else if (ks == 4) PW_A(1, 4); else if (ks == 2) PW_A(1, 2); else PW_A(1, 1);
-    }
-#undef PW_A
+    if (planes == 3)
+        launch_a_planes<3>(tiles, n_tiles, x, W, K, y32, y16, N, round_f32, stream);
+    else
+        launch_a_planes<1>(tiles, n_tiles, x, W, K, y32, y16, N, round_f32, stream);
     timer_end(t, stream);
 }
 
-template <int KSPLIT>
-static void launch_b_ks(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *codes,
-                        const float *scales, uint32_t W, uint32_t K, float *y32, uint16_t *y16,
-                        uint32_t N, uint32_t round_f32, hipStream_t stream)
+template <int KSPLIT, int BPW>
+static void launch_b_split(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *codes, const float *scales,
+                           uint32_t W, uint32_t K, float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32,
+                           hipStream_t stream)
 {
     const int grid = grid_for(n_tiles, 65535);
-    if (W <= 16)
-        hipLaunchKernelGGL((linear_b_kernel<KSPLIT, 1>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
-                           tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32);
+    if constexpr (KSPLIT == 16)
+        hipLaunchKernelGGL((linear_b_kernel<KSPLIT, 1, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
+                           n_tiles, codes, scales, W, K, y32, y16, N, round_f32);
+    else if (W <= 16)
+        hipLaunchKernelGGL((linear_b_kernel<KSPLIT, 1, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
+                           n_tiles, codes, scales, W, K, y32, y16, N, round_f32);
     else
-        hipLaunchKernelGGL((linear_b_kernel<KSPLIT, 2>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
-                           tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32);
+        hipLaunchKernelGGL((linear_b_kernel<KSPLIT, 2, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
+                           n_tiles, codes, scales, W, K, y32, y16, N, round_f32);
 }
 
 void launch_linear_b(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *codes,
                      const float *scales, uint32_t W, uint32_t K, float *y32, uint16_t *y16,
                      uint32_t N, uint32_t round_f32, hipStream_t stream)
 {
-    const int ks = pick_ksplit(n_tiles, K >> 7);
+    const LinearSplit sp = pick_split(K >> 7, W, n_tiles);
     const int t = timer_begin(K_LINEAR_B, stream);
-    if (ks == 8) launch_b_ks<8>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
-    else if (ks == 4) launch_b_ks<4>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
-    else if (ks == 2) launch_b_ks<2>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
-    else launch_b_ks<1>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream);
+#define PW_B(KS, BPW) launch_b_split<KS, BPW>(tiles, n_tiles, codes, scales, W, K, y32, y16, N, round_f32, stream)
+#define PW_B_BPW(KS)                                                                                       \
+    do {                                                                                                   \
+        if (sp.bpw == 8) PW_B(KS, 8); else if (sp.bpw == 4) PW_B(KS, 4); else if (sp.bpw == 2) PW_B(KS, 2); \
+        else PW_B(KS, 1);                                                                                  \
+    } while (0)
+    if (sp.ks == 16) PW_B_BPW(16); else if (sp.ks == 8) PW_B_BPW(8); else if (sp.ks == 4) PW_B_BPW(4);
+    else if (sp.ks == 2) PW_B_BPW(2); else PW_B_BPW(1);
+#undef PW_B_BPW
+#undef PW_B
     timer_end(t, stream);
 }
 
