@@ -95,6 +95,7 @@ struct ExpertPtrs {
     const uint8_t *down_w;
     const float *down_s;
 };
+static_assert(sizeof(ExpertPtrs) == 48, "ExpertPtrs is copied as three 16-byte units");
 
 // One routed expert's entry of the device schedule: its weights, its placement slots
 // [off, off + cnt) and the token rows of its first 16 slots (read with the entry's scalar load,

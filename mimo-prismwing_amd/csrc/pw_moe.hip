@@ -216,6 +216,162 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     }
 }
 
+// ------------------------------------------------------------------ decode-batch schedule
+// The same schedule for a decode batch (rows <= 8, so at most 64 placements: one per lane) in one
+// wave, with no workgroup barriers: a bitmap of the routed expert ids in LDS ranks each placement's
+// expert among the routed ones (ascending id, the BTreeMap order), and every per-expert table is
+// then filled lane-parallel (lane a: the a-th routed expert). Route rejection follows
+// moe_schedule_kernel: an id >= E, a non-finite weight or a token naming one expert twice raises
+// FLAG_SCHEDULE and leaves the placement tables zeroed.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, int lane)
+{
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t o = __shfl_up(v, d, 64);
+        if (lane >= d)
+            v += o;
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
+    const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids, const float *__restrict__ weights,
+    uint32_t rows, uint32_t E, uint32_t max_active, MoePlan *plan, uint32_t *__restrict__ active_expert,
+    uint32_t *__restrict__ active_offset, ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos,
+    float *__restrict__ placement_w, uint32_t *__restrict__ row_slots, uint32_t *flags)
+{
+    extern __shared__ u32x4 lds_bank[];  // the bank's ExpertPtrs table, E x 48 bytes
+    __shared__ uint32_t bitmap[32];      // routed expert ids (E <= 1024)
+    __shared__ uint32_t expert_of[64];   // by rank
+    __shared__ uint32_t count_of[64];
+    __shared__ uint16_t tok_of[64 * 16]; // token rows of each expert's first 16 placements
+    const int lane = threadIdx.x;
+    const uint32_t P = rows * 8;
+    // the routes and the whole pointer table go out together (one memory round trip in all)
+    uint32_t id = 0;
+    float w = 0.f;
+    if ((uint32_t)lane < P) {
+        id = ids[lane];
+        w = weights[lane];
+    }
+    const uint32_t units = E * 3;  // 16-byte units of the table
+    for (uint32_t u0 = 0; u0 < units; u0 += 64)
+        if (u0 + (uint32_t)lane < units)
+            lds_load16((const u32x4 *)bank + u0 + lane, lds_bank + u0);
+    const uint32_t nw = (E + 31) >> 5;
+    if ((uint32_t)lane < nw)
+        bitmap[lane] = 0u;
+    count_of[lane] = 0u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        tok_of[i * 64 + lane] = 0;
+    bool ok = (uint32_t)lane < P && id < E && finite_f32(w);
+    // a token naming one expert twice: the later slot is rejected
+    const int base = lane & ~7, sl = lane & 7;
+    bool dup = false;
+#pragma unroll
+    for (int k = 0; k < 7; ++k) {
+        const uint32_t o = __shfl(id, base + k, 64);
+        const int ov = __shfl((int)ok, base + k, 64);
+        dup |= k < sl && ov && o == id;
+    }
+    ok &= !dup;
+    const bool bad = __ballot((uint32_t)lane < P && !ok) != 0;
+    const uint64_t valid = __ballot(ok);
+    __syncthreads();
+    if (ok)
+        atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    __syncthreads();
+    // rank of this lane's expert: routed ids below it
+    const uint32_t word = (uint32_t)lane < nw ? bitmap[lane] : 0u;
+    const uint32_t wc = __popc(word);
+    const uint32_t wincl = wave_inclusive_scan(wc, lane);
+    const uint32_t U = __builtin_amdgcn_readlane(wincl, 63);
+    const int src = ok ? (int)(id >> 5) : 0;
+    const uint32_t wsel = __shfl(word, src, 64), esel = __shfl(wincl - wc, src, 64);
+    const uint32_t rank = ok ? esel + __popc(wsel & ((1u << (id & 31)) - 1u)) : 0u;
+    if (ok) {
+        expert_of[rank] = id;
+        atomicAdd(&count_of[rank], 1u);
+    }
+    // slot of this placement (lower expert ids first, then lower token rows) and its position
+    // among the token's routes ordered by expert id
+    uint32_t slot = 0;
+    for (int j = 0; j < 64; ++j) {
+        const uint32_t idj = (uint32_t)__builtin_amdgcn_readlane((int)id, j);
+        const bool vj = (valid >> j) & 1u;
+        slot += (vj && (idj < id || (idj == id && j < lane))) ? 1u : 0u;
+    }
+    uint32_t before = 0;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const uint32_t o = __shfl(id, base + m, 64);
+        before += (((valid >> (base + m)) & 1u) && o < id) ? 1u : 0u;
+    }
+    __syncthreads();
+    // lane a: the a-th routed expert
+    const uint32_t a = (uint32_t)lane;
+    const uint32_t e_a = a < U ? expert_of[a] : 0u;
+    const uint32_t c_a = a < U ? count_of[a] : 0u;
+    const uint32_t incl = wave_inclusive_scan(c_a, lane);
+    const uint32_t off_a = incl - c_a, total = __builtin_amdgcn_readlane(incl, 63);
+    // this placement's index inside its expert -> token row table
+    if (ok) {
+        const uint32_t t = slot - (uint32_t)__shfl((int)off_a, (int)rank, 64);
+        if (t < 16)
+            tok_of[rank * 16 + t] = (uint16_t)(lane >> 3);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the table copy has landed in LDS
+    __syncthreads();
+    u32x4 ep0 = {0u, 0u, 0u, 0u}, ep1 = ep0, ep2 = ep0;
+    if (a < U && a < max_active) {
+        ep0 = lds_bank[e_a * 3];
+        ep1 = lds_bank[e_a * 3 + 1];
+        ep2 = lds_bank[e_a * 3 + 2];
+    }
+    if (a < max_active) {
+        uint32_t tw[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            tw[k] = a < U ? (uint32_t)tok_of[a * 16 + 2 * k] | ((uint32_t)tok_of[a * 16 + 2 * k + 1] << 16) : 0u;
+        u32x4 *dst = (u32x4 *)(active + a);
+        dst[0] = ep0;
+        dst[1] = ep1;
+        dst[2] = ep2;
+        dst[3] = u32x4{a < U ? off_a : 0u, c_a, tw[0], tw[1]};
+        dst[4] = u32x4{tw[2], tw[3], tw[4], tw[5]};
+        dst[5] = u32x4{tw[6], tw[7], 0u, 0u};
+    }
+    if (a < U) {
+        active_expert[a] = e_a;
+        active_offset[a] = off_a;
+    }
+    if (lane == 0)
+        active_offset[U] = total;
+    if ((uint32_t)lane < P) {
+        if (bad) {
+            placement_pos[lane] = 0;
+            placement_w[lane] = 0.f;
+            row_slots[lane] = 0;
+        } else {
+            placement_pos[slot] = (uint32_t)lane >> 3;
+            placement_w[slot] = w;
+            row_slots[(size_t)(lane >> 3) * 8 + (before & 7)] = slot;
+        }
+    }
+    uint32_t mx = c_a;
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1)
+        mx = max(mx, (uint32_t)__shfl_xor(mx, d, 64));
+    if (lane == 0) {
+        plan->n_active = U;
+        plan->n_placements = total;
+        plan->max_count = mx;
+        if (bad)
+            raise_flag(flags, FLAG_SCHEDULE);
+    }
+}
+
 // --------------------------------------------------------------- shared tile preamble
 struct ExpertTile {
     ExpertPtrs ep;
@@ -588,9 +744,19 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
         (void)hipFuncSetAttribute((const void *)moe_schedule_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds);
     const int t = timer_begin(K_MOE_SCHEDULE, stream);
-    hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
-                       E, max_active, with_prefix, mb.plan, mb.active_expert, mb.active_offset, mb.active,
-                       mb.placement_pos, mb.placement_w, mb.row_slots, flags);
+    if (rows <= 8 && E <= 1024 && max_active <= 64) {
+        const size_t table = (size_t)E * sizeof(ExpertPtrs);
+        if (table > 32768)
+            (void)hipFuncSetAttribute((const void *)moe_schedule_wave_kernel,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)table);
+        hipLaunchKernelGGL(moe_schedule_wave_kernel, dim3(1), dim3(64), table, stream, bank, ids, weights, rows, E,
+                           max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active, mb.placement_pos,
+                           mb.placement_w, mb.row_slots, flags);
+    }
+    else
+        hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
+                           E, max_active, with_prefix, mb.plan, mb.active_expert, mb.active_offset, mb.active,
+                           mb.placement_pos, mb.placement_w, mb.row_slots, flags);
     timer_end(t, stream);
 }
 
