@@ -81,6 +81,8 @@ struct SplitArgs {
     uint32_t cap;                   // routed rows per expert the LDS stage holds
     float *partial;                 // [KS][MATS][P][R]
     uint32_t *flags;
+    uint32_t single;                // 1: one expert on rows 0..rows-1, its entry is `one` (no schedule)
+    ActiveExpert one;
 };
 
 // Where a launch left the per-placement expert outputs: `ks` split-K partial sums of [P][H] f32,
@@ -171,7 +173,8 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,
                         uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream);
 
-void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, uint32_t expert, const MoeBuffers &mb,
+void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, const ExpertPtrs &ep, uint32_t expert,
+                           const MoeBuffers &mb,
                            const void *x, bool x_f32, uint32_t rows, uint32_t H, uint32_t I,
                            float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream);
 

@@ -763,7 +763,7 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
 // Mode A: gate/up (+SwiGLU) then down, both as split-K expert projections (pw_moe_a.hip).
 static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, uint32_t rows,
                               uint32_t placements, uint32_t max_active, uint32_t max_count, uint32_t H,
-                              uint32_t I, uint32_t *flags, hipStream_t stream)
+                              uint32_t I, uint32_t *flags, hipStream_t stream, const ActiveExpert *one = nullptr)
 {
     const int nt = max_count > 16 ? 2 : 1;
     const uint32_t cnt = max_count < 16u * nt ? max_count : 16u * nt;
@@ -784,6 +784,10 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     ga.partial = mb.partial;
     ga.flags = flags;
     ga.cap = cnt;
+    if (one) {
+        ga.single = 1;
+        ga.one = *one;
+    }
     const SplitPlan gp = plan_split(H, 2, x_f32 ? 3 : 1, cnt);
     ga.KS = gp.ks;
     int t = timer_begin(K_MOE_GATEUP, stream);
@@ -865,13 +869,25 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
     timer_end(t, stream);
 }
 
-void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, uint32_t expert, const MoeBuffers &mb,
-                           const void *x, bool x_f32, uint32_t rows, uint32_t H, uint32_t I,
+void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, const ExpertPtrs &ep, uint32_t expert,
+                           const MoeBuffers &mb, const void *x, bool x_f32, uint32_t rows, uint32_t H, uint32_t I,
                            float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream)
 {
-    hipLaunchKernelGGL(moe_single_plan_kernel, dim3(1), dim3(256), 0, stream, bank, expert, rows, mb.plan,
-                       mb.active_expert, mb.active_offset, mb.active, mb.placement_pos, mb.placement_w);
-    const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream);
+    ExpertOut eo{};
+    if (mode == 0) {
+        // mode A takes the expert's schedule entry by value: no plan kernel
+        ActiveExpert one{};
+        one.ep = ep;
+        one.off = 0;
+        one.cnt = rows;
+        for (uint32_t k = 0; k < 16; ++k)
+            one.tok[k] = (uint16_t)k;
+        eo = launch_a_moe(mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream, &one);
+    } else {
+        hipLaunchKernelGGL(moe_single_plan_kernel, dim3(1), dim3(256), 0, stream, bank, expert, rows, mb.plan,
+                           mb.active_expert, mb.active_offset, mb.active, mb.placement_pos, mb.placement_w);
+        eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream);
+    }
     const uint32_t n = rows * H;
     hipLaunchKernelGGL(round_output_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, eo.y, eo.ks, eo.stride,
                        n, out_f32, out_bf16, raw ? 1u : 0u, flags);

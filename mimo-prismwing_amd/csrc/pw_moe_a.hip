@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
     const uint32_t s = blockIdx.x % args.KS;
     const uint32_t g = (blockIdx.x / args.KS) % G;
     const uint32_t a = blockIdx.x / (args.KS * G);
-    const ActiveExpert ae = args.active[a];
+    const ActiveExpert ae = args.single ? args.one : args.active[a];
     if (ae.cnt == 0)
         return;
     if (ae.cnt > 16u * NT || ae.cnt > args.cap) {
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
     uint32_t tok = 0;
     if constexpr (MATS == 2 && NT == 2) {
         if ((uint32_t)lane >= 16 && (uint32_t)lane < ae.cnt)
-            tok = load_g(args.placement_pos + ae.off + lane);
+            tok = args.single ? (uint32_t)lane : load_g(args.placement_pos + ae.off + lane);
     }
 
     // 2. every weight byte of this wave's rows and K split, in flight at once
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     const int q = lane >> 4, r16 = lane & 15;
     const uint32_t G = args.R >> 4;
     const uint32_t g = blockIdx.x % G, a = blockIdx.x / G;
-    const ActiveExpert ae = args.active[a];
+    const ActiveExpert ae = args.single ? args.one : args.active[a];
     if (ae.cnt == 0)
         return;
     if (ae.cnt > 16u || ae.cnt > args.cap) {

@@ -147,6 +147,7 @@ struct pw_projection {
 struct pw_expert_bank {
     pw_runtime *rt = nullptr;
     ExpertPtrs *table = nullptr;  // device [E]
+    std::vector<ExpertPtrs> host_table;  // the same pointers, for launches that take one expert by value
     uint32_t n_experts = 0, hidden = 0, intermediate = 0;
     void *owned = nullptr;        // weights and scales the bank owns (checkpoint banks)
     uint64_t owned_bytes = 0;
@@ -1033,6 +1034,7 @@ int pw_expert_bank_create(pw_runtime *rt, uint32_t n_experts, const pw_projectio
     b->n_experts = n_experts;
     b->hidden = H;
     b->intermediate = I;
+    b->host_table = table;
     hipError_t e = hipMalloc(&b->table, table.size() * sizeof(ExpertPtrs));
     if (e == hipSuccess)
         e = hipMemcpy(b->table, table.data(), table.size() * sizeof(ExpertPtrs), hipMemcpyHostToDevice);
@@ -1075,6 +1077,7 @@ int pw::make_owned_bank(pw_runtime *rt, const std::vector<ExpertPtrs> &table, ui
     b->intermediate = intermediate;
     b->owned = owned;
     b->owned_bytes = owned_bytes;
+    b->host_table = table;
     hipError_t e = hipMalloc(&b->table, table.size() * sizeof(ExpertPtrs));
     if (e == hipSuccess)
         e = hipMemcpy(b->table, table.data(), table.size() * sizeof(ExpertPtrs), hipMemcpyHostToDevice);
@@ -1212,7 +1215,8 @@ int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
     PW_TRY(ensure_moe(rt, rows, bank->n_experts, bank->hidden, bank->intermediate));
-    pw::launch_expert_forward(mode, bank->table, expert, rt->mb, x, x_dtype == PW_DTYPE_F32, rows,
+    pw::launch_expert_forward(mode, bank->table, bank->host_table[expert], expert, rt->mb, x, x_dtype == PW_DTYPE_F32,
+                              rows,
                               bank->hidden, bank->intermediate,
                               out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
                               out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
