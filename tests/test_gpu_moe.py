@@ -221,3 +221,40 @@ def test_whole_k_gateup_matches_split_k(rt, full_bank):
     experts = {e: full_bank.expert_host(e) for e in used}
     _, ref_raw = O.moe_layer("a", x, experts, 256, sel, w, raw=True)
     assert normwise(outs[1], ref_raw) <= 1e-3
+
+
+@pytest.mark.parametrize("rows", [8, 9])
+def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
+    """Route buffers with an expert id outside the bank, one token naming an expert twice, or a NaN
+    weight raise the schedule error bit (src/wide_metal_moe.rs:858-938 rejects such schedules) from
+    both schedule kernels (8 rows: one wave; 9 rows: one workgroup) without faulting, and the next
+    valid call gives the same bytes as before."""
+    import torch
+    x = WL.activations(rows, WL.SEED_BASE + 90)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    _, _, sel, w, _ = O.route(x, rw, bias)
+    xt = torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(ids, wts):
+        out = torch.empty((rows, 4096), dtype=torch.float32, device="cuda")
+        rt.moe_layer_device(full_bank.bank, xt, rows, torch.from_numpy(ids.astype(np.int32)).cuda(),
+                            torch.from_numpy(wts).cuda(), out, mode=P.MODE_A, out_dtype=P.DTYPE_F32_RAW,
+                            stream=stream)
+        torch.cuda.synchronize()
+        return out.cpu().numpy(), rt.take_flags()
+
+    clean, flags = run(sel, w)
+    assert flags == 0
+    bad_id = sel.copy()
+    bad_id[rows - 1, 3] = 256
+    twice = sel.copy()
+    twice[0, 1] = twice[0, 0]
+    nan_w = w.copy()
+    nan_w[1, 5] = np.nan
+    for ids, wts in ((bad_id, w), (twice, w), (sel, nan_w)):
+        _, flags = run(ids, wts)
+        assert flags & P.FLAG_SCHEDULE
+    again, flags = run(sel, w)
+    assert flags == 0
+    assert np.array_equal(clean.view(np.uint32), again.view(np.uint32))
