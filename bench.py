@@ -142,8 +142,8 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
     rt.enable_timing(steps * 8)
     for _ in range(steps):
         run()
-    kt = {}  # average µs per launch (the quantiser runs twice per layer: x, then the hidden)
-    for k in ("moe_schedule", "quant", "prefill_gateup", "prefill_down", "moe_combine"):
+    kt = {}  # average µs per launch (moe_swiglu: the SwiGLU + re-quantisation of the hidden)
+    for k in ("moe_schedule", "quant", "prefill_gateup", "moe_swiglu", "prefill_down", "moe_combine"):
         n, tot = rt.timing(k)
         if n:
             kt[k] = round(1000.0 * tot / n, 2)

@@ -129,11 +129,14 @@ __device__ __forceinline__ void pf_copy_codes(uint4 *slot, const uint8_t *const 
 }
 
 // One step: its blocks in ascending order, each block's FP8 products from one MFMA per 16-token
-// tile, then tot += (p * S_w) * a in f32.
+// tile, then tot += (p * S_w) * a in f32. Each block's weight registers are refilled from column
+// knext (the step WS ahead) as soon as its MFMAs have read them, half a step earlier than a refill
+// of the whole step. cl0 / cl1: the lane's two code units of token r16 in a block (tile j adds
+// 16 tokens = 128 units).
 template <class C>
-__device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], const PfW<C> &w, const uint4 *slot,
-                                           const float *lds_scale, const float *lds_wscale, uint32_t k, int q,
-                                           int r16)
+__device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], PfW<C> &w, const uint4 *slot,
+                                           const float *lds_scale, const float *lds_wscale, uint32_t k, int r16,
+                                           const uint8_t *wrow, uint32_t knext, uint32_t cl0, uint32_t cl1)
 {
 #pragma unroll
     for (int h = 0; h < C::SB; ++h) {
@@ -146,8 +149,8 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], const PfW<C> &w,
         for (int j = 0; j < PF_TT; ++j) {
             const uint32_t t = 16 * j + r16;
             const float sa = lds_scale[b * PF_MT + t];
-            const uint4 c0 = buf[t * PF_UNITS + ((q) ^ (t & 7))];
-            const uint4 c1 = buf[t * PF_UNITS + ((q + 4) ^ (t & 7))];
+            const uint4 c0 = buf[cl0 + 128 * j];
+            const uint4 c1 = buf[cl1 + 128 * j];
             const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
                               (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
             const f32x4 p = mfma_fp8_16x16x128(A, xb, f32x4{0.f, 0.f, 0.f, 0.f});
@@ -155,6 +158,8 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], const PfW<C> &w,
             for (int i = 0; i < 4; ++i)
                 tot[j][i] = __builtin_fmaf(p[i] * sw, sa, tot[j][i]);
         }
+        w.v[2 * h] = load_global16(wrow + knext + 128 * h);
+        w.v[2 * h + 1] = load_global16(wrow + knext + 128 * h + 64);
     }
 }
 
@@ -162,7 +167,7 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], const PfW<C> &w,
 // bf16-rounded outputs (bf16_round_in_place of every projection, src/wide_metal_moe.rs:1236-1251).
 // n-tiles [0, R1 / 128) use the first matrix (gate, or down), the rest the second (up).
 template <class C>
-__global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per_eu(C::SB == 2 ? 5 : 4))) void prefill_b_kernel(const PrefillArgs args)
+__global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per_eu(5))) void prefill_b_kernel(const PrefillArgs args)
 {
     extern __shared__ uint4 lds_pf[];
     const uint32_t K = args.K, blocks = K >> 7;
@@ -265,6 +270,12 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
 #pragma unroll
     for (int i = 0; i < C::WS; ++i)
         pf_issue_w<C>(w[i], wrow, ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB));
+    // the lane's code units of token r16 in a block: units q and q + 4, swizzled by token % 8 (the
+    // same for token r16 + 16 j); opaque to the compiler, which would otherwise fold the tile
+    // offsets into one address register per tile and half instead of immediate offsets
+    uint32_t cl0 = (uint32_t)r16 * PF_UNITS + ((uint32_t)q ^ ((uint32_t)r16 & 7u));
+    uint32_t cl1 = (uint32_t)r16 * PF_UNITS + (((uint32_t)q + 4u) ^ ((uint32_t)r16 & 7u));
+    asm volatile("" : "+v"(cl0), "+v"(cl1));
     f32x4 tot[PF_TT];
 #pragma unroll
     for (int j = 0; j < PF_TT; ++j)
@@ -272,8 +283,8 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
     // this wave's scale copies (issued before the weights) are complete before the first barrier
     wait_vmcnt<2 * C::SB * C::WS>();
 
-    // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, then load
-    // step k + C::WS's weights into that slot. Whole groups of C::G steps run without early exits
+    // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each block's
+    // registers reloaded with step k + C::WS's block right after use. Whole groups of C::G steps run without early exits
     // (static ring indices, one loop state at the loop head); the last steps are peeled. Load
     // indices are clamped to the last step (the tail reloads it: cache hits), keeping every load
     // unconditional.
@@ -283,8 +294,8 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
         for (int i = 0; i < C::G; ++i) {
             const uint32_t k = b + i;
             lds_barrier();
-            pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, q, r16);
-            pf_issue_w<C>(w[i % C::WS], wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB));
+            pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, r16, wrow,
+                          (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
         }
     }
 #pragma unroll
@@ -293,8 +304,8 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
         if (k >= nsteps)
             break;
         lds_barrier();
-        pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, q, r16);
-        pf_issue_w<C>(w[i % C::WS], wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB));
+        pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, r16, wrow,
+                      (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
     }
 
     // epilogue: lane holds rows 4q + i of the wave's 16 for tokens 16j + r16 -> bf16
