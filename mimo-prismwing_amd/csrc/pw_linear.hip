@@ -303,9 +303,7 @@ __global__ __launch_bounds__(256) void quant_group128_kernel(const T *__restrict
     float n0 = v0 / scale, n1 = v1 / scale;
     n0 = n0 < -448.f ? -448.f : (n0 > 448.f ? 448.f : n0);
     n1 = n1 < -448.f ? -448.f : (n1 > 448.f ? 448.f : n1);
-    const uint16_t packed = (uint16_t)encode_e4m3fn_rne(f0 ? n0 : 0.f) |
-                            ((uint16_t)encode_e4m3fn_rne(f1 ? n1 : 0.f) << 8);
-    *(uint16_t *)(codes + base) = packed;
+    *(uint16_t *)(codes + base) = (uint16_t)encode2_e4m3fn(f0 ? n0 : 0.f, f1 ? n1 : 0.f);
 }
 
 // f32 [n] -> bf16 planes hi [n], mid [n], lo [n] with x == hi + mid + lo.

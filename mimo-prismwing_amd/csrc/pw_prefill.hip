@@ -367,13 +367,16 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
     const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
     if (lane16 == 0)
         scales[group] = scale;
-    uint32_t packed[2] = {0u, 0u};
+    float n[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        float n = finite_f32(h[i]) ? h[i] / scale : 0.f;
-        n = n < -448.f ? -448.f : (n > 448.f ? 448.f : n);
-        packed[i >> 2] |= (uint32_t)encode_e4m3fn_rne(n) << (8 * (i & 3));
+        n[i] = finite_f32(h[i]) ? h[i] / scale : 0.f;
+        n[i] = n[i] < -448.f ? -448.f : (n[i] > 448.f ? 448.f : n[i]);
     }
+    uint32_t packed[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+        packed[i] = encode2_e4m3fn(n[4 * i], n[4 * i + 1]) | (encode2_e4m3fn(n[4 * i + 2], n[4 * i + 3]) << 16);
     *(uint2 *)(codes + (size_t)slot * I + c) = make_uint2(packed[0], packed[1]);
 }
 

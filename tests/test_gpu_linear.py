@@ -144,6 +144,36 @@ def test_quantiser_bit_exact(rt, golden_dir):
         assert np.array_equal(scales.view(np.uint32), scales_ref.view(np.uint32))
 
 
+def _encoder_sweep_values():
+    """f32 values with |x| <= 448 that decide e4m3fn round-to-nearest-even: every bit pattern with
+    its low 11 bits clear (all codes and all exact ties between codes are among them), each tie
+    and its neighbours 1 and 2 ulp away, and 2^20 random patterns; both signs, zeros included."""
+    lim = 0x43E00000  # 448.0f
+    coarse = np.arange(0, lim + 1, 2048, dtype=np.int64)
+    mags = np.array([O.decode_e4m3fn(c) for c in range(0x7F)], np.float64)
+    mids = ((mags[:-1] + mags[1:]) / 2).astype(np.float32).view(np.uint32).astype(np.int64)
+    ties = (mids[:, None] + np.arange(-2, 3)).reshape(-1)
+    rand = np.random.default_rng(21).integers(0, lim + 1, 1 << 20, dtype=np.int64)
+    bits = np.unique(np.concatenate([coarse, ties, rand]))
+    vals = bits[(bits >= 0) & (bits <= lim)].astype(np.uint32).view(np.float32)
+    return np.concatenate([vals, -vals])
+
+
+def test_quantiser_encoder_sweep(rt):
+    """Groups whose first value is 448 have scale exactly 1, so their codes are the e4m3fn
+    encodings of the values themselves: the device encoder against the oracle's on ~3.2M values."""
+    vals = _encoder_sweep_values()
+    per = 127
+    n = -(-vals.size // per)
+    body = np.zeros(n * per, np.float32)
+    body[:vals.size] = vals
+    x = np.concatenate([np.full((n, 1), 448.0, np.float32), body.reshape(n, per)], axis=1)
+    codes_ref, scales_ref, _ = O.dynamic_fp8(x)
+    codes, scales = quantize_device(rt, x)
+    assert np.all(scales_ref == 1.0) and np.array_equal(scales.view(np.uint32), scales_ref.view(np.uint32))
+    assert np.array_equal(codes, codes_ref)
+
+
 def quantize_device(rt, data):
     torch = _torch()
     rows, k = data.shape
