@@ -283,6 +283,20 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
                           uint32_t rows, const uint32_t *route_ids, const float *route_weights, void *output,
                           uint32_t out_dtype, void *stream);
 
+/* The device routed schedule on its own, for callers that keep the reference's expert placement
+ * counts: route_ids / route_weights [rows x 8] (device, 16-byte aligned, rows 1..4096) over the
+ * bank's experts -> the reference's BTreeMap<expert, [(position, weight)]>
+ * (src/text_endpoint.rs:4767-4775) as device tables: expert_offsets [n_experts + 1] (expert e's
+ * placement slots are [offsets[e], offsets[e + 1]), so its placement count is the difference),
+ * positions / weights [rows x 8] (token row and router weight of each slot: experts ascending,
+ * token rows ascending within an expert) and row_slots [rows x 8] (each token's eight slots in
+ * ascending expert id, the combine order of src/text_endpoint.rs:5365-5373). Rejected routes
+ * (the checks of WideMetalMoeRuntime::execute, src/wide_metal_moe.rs:858-938) raise
+ * PW_FLAG_SCHEDULE. The same schedule the layer entry points build. Asynchronous on stream. */
+int pw_moe_schedule_device(pw_runtime *rt, const pw_expert_bank *bank, const uint32_t *route_ids,
+                           const float *route_weights, uint32_t rows, uint32_t *expert_offsets,
+                           uint32_t *positions, float *weights, uint32_t *row_slots, void *stream);
+
 /* One complete expert (gate/up -> SwiGLU -> down, no routing, no combine) on device rows
  * x [rows x hidden] -> output [rows x hidden] bf16-rounded: the reference's complete-expert
  * measurement (direct-checkpoint L3 expert, src/lib.rs:4008-6590; mode A widths 1..8 via

@@ -67,6 +67,7 @@ struct MoeBuffers {
     float *xs;                 // [rows * H/128]  mode B activation scales
     uint8_t *hq;               // [rows * 8 * I]
     float *hs;                 // [rows * 8 * I/128]
+    void *sched;               // [moe_sched_scratch_bytes] long-batch schedule tables
     uint32_t max_rows;
     uint32_t experts;
 };
@@ -147,9 +148,14 @@ void launch_linear_b(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *cod
 void launch_quant_group128(const void *x, bool x_f32, uint32_t rows, uint32_t K, uint8_t *codes,
                            float *scales, uint32_t *flags, hipStream_t stream);
 
+// Bytes of MoeBuffers::sched the schedule of `rows` token rows over E experts needs (0 for the
+// batches scheduled in one workgroup).
+size_t moe_sched_scratch_bytes(uint32_t rows, uint32_t E);
 void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
                          uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
                          uint32_t *flags, hipStream_t stream);
+// expert_offsets [E + 1]: expert e's placement slots are [off[e], off[e + 1]) (after a schedule).
+void launch_expert_offsets(const MoeBuffers &mb, uint32_t E, uint32_t *expert_offsets, hipStream_t stream);
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                       bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,

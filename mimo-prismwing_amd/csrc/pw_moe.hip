@@ -216,6 +216,269 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
     }
 }
 
+// ------------------------------------------------------------------ long-batch schedule
+// The same schedule for prefill-sized batches in three short launches over many workgroups (one
+// workgroup would hold E x rows bits in LDS and do every step on one CU):
+//   moe_sched_mark_kernel: one wave per 64 token rows checks its routes (as mark_route_row) and
+//     writes the (expert, 32-row word) bitmap words and their popcounts;
+//   moe_sched_plan_kernel: one workgroup forms each expert's count and per-word prefix counts,
+//     the slot offsets and routed-expert tables (block scans in ascending expert id), the largest
+//     count and the plan;
+//   moe_sched_place_kernel: one thread per token row writes its eight placements at
+//     offset[e] + prefix[e][word] + (bits below the row in its word) -- ascending rows per
+//     expert, as in moe_schedule_kernel -- and the token row of each of an expert's first 16
+//     slots into its ActiveExpert entry.
+// Rejected routes (an id >= E, a non-finite weight, an expert named twice by one token, or any
+// count mismatch) raise FLAG_SCHEDULE and leave every placement table zero.
+constexpr uint32_t SCHED_WG_MAX_ROWS = 128;  // longer batches take the three-launch schedule
+constexpr uint32_t SCHED_MAX_WORDS = 128;     // 4096 rows
+
+struct SchedScratch {
+    uint32_t *mask;  // [E][W] row bits per (expert, 32-row word)
+    uint8_t *cnt;    // [E][Wp] popcounts (Wp = W rounded up to 16)
+    uint16_t *pref;  // [E][Wp] exclusive per-word prefix of the counts
+    uint32_t *offs;  // [E] first slot of each expert
+    uint32_t *acts;  // [E] index among the routed experts (~0 when not routed)
+    uint32_t *badw;  // [ceil(rows / 64)] rejected routes per wave of rows
+};
+
+static inline size_t align16(size_t n) { return (n + 15) & ~(size_t)15; }
+
+static SchedScratch sched_carve(void *base, uint32_t rows, uint32_t E, size_t *bytes)
+{
+    const size_t W = (rows + 31) / 32, Wp = (W + 15) & ~(size_t)15, nwg = (rows + 63) / 64;
+    SchedScratch ss{};
+    size_t at = 0;
+    char *b = (char *)base;
+    ss.mask = (uint32_t *)(b + at);
+    at += align16(E * W * 4);
+    ss.cnt = (uint8_t *)(b + at);
+    at += align16(E * Wp);
+    ss.pref = (uint16_t *)(b + at);
+    at += align16(E * Wp * 2);
+    ss.offs = (uint32_t *)(b + at);
+    at += align16((size_t)E * 4);
+    ss.acts = (uint32_t *)(b + at);
+    at += align16((size_t)E * 4);
+    ss.badw = (uint32_t *)(b + at);
+    at += align16(nwg * 4);
+    if (bytes)
+        *bytes = at;
+    return ss;
+}
+
+size_t moe_sched_scratch_bytes(uint32_t rows, uint32_t E)
+{
+    if (rows <= SCHED_WG_MAX_ROWS)
+        return 0;
+    size_t bytes = 0;
+    (void)sched_carve(nullptr, rows, E, &bytes);
+    return bytes;
+}
+
+__global__ __launch_bounds__(64) void moe_sched_mark_kernel(const uint32_t *__restrict__ ids,
+                                                            const float *__restrict__ weights, uint32_t rows,
+                                                            uint32_t E, SchedScratch ss)
+{
+    extern __shared__ uint32_t lmask[];  // [E][2]: the bitmap words of this wave's 64 rows
+    const uint32_t lane = threadIdx.x, p = blockIdx.x * 64 + lane;
+    const uint32_t W = (rows + 31) >> 5, Wp = (W + 15) & ~15u;
+    const bool has = p < rows;
+    RouteRow rr{};
+    if (has)
+        rr = load_route_row(ids, weights, p);
+    for (uint32_t i = lane; i < 2 * E; i += 64)
+        lmask[i] = 0u;
+    __syncthreads();
+    const bool bad = has && mark_route_row(rr, lane, E, 2, lmask);
+    __syncthreads();
+    const uint32_t w0 = blockIdx.x * 2;
+    for (uint32_t i = lane; i < 2 * E; i += 64) {
+        const uint32_t e = i >> 1, w = w0 + (i & 1);
+        if (w < W) {
+            const uint32_t m = lmask[i];
+            ss.mask[(size_t)e * W + w] = m;
+            ss.cnt[(size_t)e * Wp + w] = (uint8_t)__popc(m);
+        }
+    }
+    const bool any = __ballot(bad) != 0;
+    if (lane == 0)
+        ss.badw[blockIdx.x] = any ? 1u : 0u;
+}
+
+__global__ __launch_bounds__(1024) void moe_sched_plan_kernel(
+    const ExpertPtrs *__restrict__ bank, uint32_t rows, uint32_t E, uint32_t max_active, SchedScratch ss,
+    MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
+    ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
+    uint32_t *__restrict__ row_slots, uint32_t *flags)
+{
+    __shared__ uint32_t s_scan[48], s_bad, s_max;
+    const uint32_t tid = threadIdx.x, e = tid;
+    const uint32_t W = (rows + 31) >> 5, Wp = (W + 15) & ~15u, nwg = (rows + 63) >> 6;
+    const uint32_t P = rows * 8;
+    // the loads every later step waits on go out first: this expert's weight pointers and all of
+    // its per-word counts (W <= 128: at most eight 16-byte loads)
+    u32x4 ep0 = {0u, 0u, 0u, 0u}, ep1 = ep0, ep2 = ep0;
+    uint4 cv[SCHED_MAX_WORDS / 16];
+    if (e < E) {
+        const u32x4 *src = (const u32x4 *)(bank + e);
+        ep0 = src[0];
+        ep1 = src[1];
+        ep2 = src[2];
+        const uint4 *crow = (const uint4 *)(ss.cnt + (size_t)e * Wp);
+#pragma unroll
+        for (uint32_t g = 0; g < SCHED_MAX_WORDS / 16; ++g)
+            cv[g] = g * 16 < W ? crow[g] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (tid == 0) {
+        s_bad = 0;
+        s_max = 0;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < nwg; i += blockDim.x)
+        if (ss.badw[i])
+            atomicOr(&s_bad, 1u);
+    // expert e's count and the exclusive prefix of its per-word counts (words past W count 0)
+    uint32_t c = 0;
+    if (e < E) {
+        uint4 *prow = (uint4 *)(ss.pref + (size_t)e * Wp);
+#pragma unroll
+        for (uint32_t g = 0; g < SCHED_MAX_WORDS / 16; ++g) {
+            const uint32_t b[4] = {cv[g].x, cv[g].y, cv[g].z, cv[g].w};
+            uint32_t pr[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 16; ++k) {
+                const uint32_t n = g * 16 + k < W ? (b[k >> 2] >> (8 * (k & 3))) & 0xffu : 0u;
+                if (k & 1)
+                    pr[k >> 1] |= c << 16;
+                else
+                    pr[k >> 1] = c;
+                c += n;
+            }
+            if (g * 16 < W) {
+                prow[2 * g] = make_uint4(pr[0], pr[1], pr[2], pr[3]);
+                prow[2 * g + 1] = make_uint4(pr[4], pr[5], pr[6], pr[7]);
+            }
+        }
+    }
+    uint32_t total, n_active;
+    const uint32_t off = block_exclusive_scan(c, s_scan, &total);
+    const uint32_t act = block_exclusive_scan(c ? 1u : 0u, s_scan, &n_active);
+    if (e < E) {
+        ss.offs[e] = off;
+        ss.acts[e] = c ? act : 0xffffffffu;
+        if (c) {
+            active_expert[act] = e;
+            active_offset[act] = off;
+            if (act < max_active) {
+                // ExpertPtrs, off, cnt, then tok[16] (the place kernel fills it) and the pad
+                u32x4 *dst = (u32x4 *)(active + act);
+                dst[0] = ep0;
+                dst[1] = ep1;
+                dst[2] = ep2;
+                dst[3] = u32x4{off, c, 0u, 0u};
+                dst[4] = u32x4{0u, 0u, 0u, 0u};
+                dst[5] = u32x4{0u, 0u, 0u, 0u};
+            }
+            atomicMax(&s_max, c);
+        }
+    }
+    if (tid == 0)
+        active_offset[n_active] = total;
+    for (uint32_t a = n_active + tid; a < max_active; a += blockDim.x) {
+        uint4 *dst = (uint4 *)(active + a);
+#pragma unroll
+        for (int i = 0; i < 6; ++i)
+            dst[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+    const bool rejected = s_bad != 0 || total != P;
+    if (rejected)
+        for (uint32_t i = tid; i < P; i += blockDim.x) {
+            placement_pos[i] = 0;
+            placement_w[i] = 0.f;
+            row_slots[i] = 0;
+        }
+    if (tid == 0) {
+        plan->n_active = n_active;
+        plan->n_placements = total;
+        plan->max_count = s_max;
+        plan->rejected = rejected ? 1u : 0u;
+        if (rejected)
+            raise_flag(flags, FLAG_SCHEDULE);
+    }
+}
+
+__global__ __launch_bounds__(64) void moe_sched_place_kernel(
+    const uint32_t *__restrict__ ids, const float *__restrict__ weights, uint32_t rows, uint32_t E,
+    uint32_t max_active, SchedScratch ss, const MoePlan *__restrict__ plan, ActiveExpert *__restrict__ active,
+    uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w, uint32_t *__restrict__ row_slots)
+{
+    const uint32_t p = blockIdx.x * 64 + threadIdx.x;
+    if (p >= rows || plan->rejected)
+        return;  // rejected: the plan kernel left the tables zero
+    const uint32_t W = (rows + 31) >> 5, Wp = (W + 15) & ~15u, P = rows * 8;
+    const RouteRow rr = load_route_row(ids, weights, p);
+    const uint32_t wd = p >> 5, below = (1u << (p & 31)) - 1u;
+    // every table load of the eight placements first (accepted routes: every id < E)
+    uint32_t m[8], pr[8], off[8], ac[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t e = rr.e[j] < E ? rr.e[j] : 0u;
+        m[j] = ss.mask[(size_t)e * W + wd];
+        pr[j] = ss.pref[(size_t)e * Wp + wd];
+        off[j] = ss.offs[e];
+        ac[j] = ss.acts[e];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t ei = rr.e[j];
+        const uint32_t rank = pr[j] + __popc(m[j] & below);
+        const uint32_t slot = off[j] + rank;
+        if (ei >= E || slot >= P)
+            continue;
+        placement_pos[slot] = p;
+        placement_w[slot] = rr.w[j];
+        // position of this placement among its token's eight, ordered by expert id
+        uint32_t before = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            before += rr.e[k] < ei ? 1u : 0u;
+        row_slots[(size_t)p * 8 + (before & 7)] = slot;
+        if (rank < 16 && ac[j] < max_active)
+            active[ac[j]].tok[rank] = (uint16_t)p;
+    }
+}
+
+// Per-expert slot ranges from the routed-expert tables: expert e's placements are
+// [off[e], off[e + 1]) and off[E] is the placement count. One thread per entry: the first routed
+// expert with id >= e, by binary search over active_expert[0, U) (ascending ids).
+__global__ __launch_bounds__(256) void expert_offsets_kernel(const MoePlan *__restrict__ plan,
+                                                             const uint32_t *__restrict__ active_expert,
+                                                             const uint32_t *__restrict__ active_offset, uint32_t E,
+                                                             uint32_t *__restrict__ off)
+{
+    const uint32_t e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e > E)
+        return;
+    const uint32_t U = plan->n_active < E ? plan->n_active : E;
+    uint32_t lo = 0, hi = U;
+    while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (active_expert[mid] < e)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    off[e] = active_offset[lo];
+}
+
+void launch_expert_offsets(const MoeBuffers &mb, uint32_t E, uint32_t *expert_offsets, hipStream_t stream)
+{
+    hipLaunchKernelGGL(expert_offsets_kernel, dim3((E + 1 + 255) / 256), dim3(256), 0, stream, mb.plan,
+                       mb.active_expert, mb.active_offset, E, expert_offsets);
+}
+
 // ------------------------------------------------------------------ decode-batch schedule
 // The same schedule for a decode batch (rows <= 8, so at most 64 placements: one per lane) in one
 // wave, with no workgroup barriers: a bitmap of the routed expert ids in LDS ranks each placement's
@@ -753,10 +1016,22 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
                            max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active, mb.placement_pos,
                            mb.placement_w, mb.row_slots, flags);
     }
-    else
+    else if (rows <= SCHED_WG_MAX_ROWS)
         hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
                            E, max_active, with_prefix, mb.plan, mb.active_expert, mb.active_offset, mb.active,
                            mb.placement_pos, mb.placement_w, mb.row_slots, flags);
+    else {
+        // rows <= 4096 (SCHED_MAX_WORDS words) and E <= 1024 (one plan thread per expert)
+        const SchedScratch ss = sched_carve(mb.sched, rows, E, nullptr);
+        const uint32_t nwg = (rows + 63) / 64;
+        hipLaunchKernelGGL(moe_sched_mark_kernel, dim3(nwg), dim3(64), (size_t)E * 8, stream, ids, weights, rows, E,
+                           ss);
+        hipLaunchKernelGGL(moe_sched_plan_kernel, dim3(1), dim3(1024), 0, stream, bank, rows, E, max_active, ss,
+                           mb.plan, mb.active_expert, mb.active_offset, mb.active, mb.placement_pos,
+                           mb.placement_w, mb.row_slots, flags);
+        hipLaunchKernelGGL(moe_sched_place_kernel, dim3(nwg), dim3(64), 0, stream, ids, weights, rows, E, max_active,
+                           ss, mb.plan, mb.active, mb.placement_pos, mb.placement_w, mb.row_slots);
+    }
     timer_end(t, stream);
 }
 

@@ -106,7 +106,7 @@ struct pw_runtime {
     // routed-MoE per-layer scratch
     DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
         moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
-        moe_active, moe_partial, pf_tiles, router_scores, bf16_partial;
+        moe_active, moe_partial, moe_sched, pf_tiles, router_scores, bf16_partial;
     MoeBuffers mb{};
     pw::KernelTimer timer;
 };
@@ -262,9 +262,8 @@ int read_flags(pw_runtime *rt, uint32_t &flags)
             return s_;               \
     } while (0)
 
-// Routed-MoE scratch for `rows` token rows. mode_a_split: also the mode A buffers (activation
-// and hidden bf16 planes, split-K partial sums), which the decode paths (rows <= 128) use.
-int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, bool mode_a_split = true)
+// The device schedule's tables for `rows` token rows over E experts.
+int ensure_sched(pw_runtime *rt, uint32_t rows, uint32_t E)
 {
     const size_t P = (size_t)rows * 8;
     PW_HIP(rt->moe_plan.ensure(sizeof(pw::MoePlan)));
@@ -273,6 +272,29 @@ int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I
     PW_HIP(rt->moe_pos.ensure(P * 4));
     PW_HIP(rt->moe_w.ensure(P * 4));
     PW_HIP(rt->moe_slots.ensure(P * 4));
+    PW_HIP(rt->moe_active.ensure((size_t)(E + 1) * sizeof(pw::ActiveExpert)));
+    if (const size_t sched = pw::moe_sched_scratch_bytes(rows, E))
+        PW_HIP(rt->moe_sched.ensure(sched));
+    MoeBuffers &mb = rt->mb;
+    mb.plan = (pw::MoePlan *)rt->moe_plan.p;
+    mb.active_expert = (uint32_t *)rt->moe_active_expert.p;
+    mb.active_offset = (uint32_t *)rt->moe_active_offset.p;
+    mb.placement_pos = (uint32_t *)rt->moe_pos.p;
+    mb.placement_w = (float *)rt->moe_w.p;
+    mb.row_slots = (uint32_t *)rt->moe_slots.p;
+    mb.active = (pw::ActiveExpert *)rt->moe_active.p;
+    mb.sched = rt->moe_sched.p;
+    return PW_OK;
+}
+
+// Routed-MoE scratch for `rows` token rows. mode_a_split: also the mode A buffers (activation
+// and hidden bf16 planes, split-K partial sums), which the decode paths (rows <= 128) use.
+int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, bool mode_a_split = true)
+{
+    const size_t P = (size_t)rows * 8;
+    const int st = ensure_sched(rt, rows, E);
+    if (st != PW_OK)
+        return st;
     PW_HIP(rt->moe_hidden.ensure(P * I * 4));
     if (mode_a_split) {
         PW_HIP(rt->moe_hidden_planes.ensure(3 * P * I * 2));
@@ -287,18 +309,10 @@ int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I
     const uint32_t cnt = std::min<uint32_t>(rows, 32);
     const size_t ks_gu = std::max(pw::plan_split(H, 2, 1, cnt).ks, pw::plan_split(H, 2, 3, cnt).ks);
     const size_t ks_d = pw::plan_split(I, 1, 3, cnt).ks;
-    PW_HIP(rt->moe_active.ensure((size_t)(E + 1) * sizeof(pw::ActiveExpert)));
     if (mode_a_split)
         PW_HIP(rt->moe_partial.ensure(std::max(ks_gu * 2 * P * I, ks_d * P * H) * 4));
     MoeBuffers &mb = rt->mb;
-    mb.active = (pw::ActiveExpert *)rt->moe_active.p;
     mb.partial = (float *)rt->moe_partial.p;
-    mb.plan = (pw::MoePlan *)rt->moe_plan.p;
-    mb.active_expert = (uint32_t *)rt->moe_active_expert.p;
-    mb.active_offset = (uint32_t *)rt->moe_active_offset.p;
-    mb.placement_pos = (uint32_t *)rt->moe_pos.p;
-    mb.placement_w = (float *)rt->moe_w.p;
-    mb.row_slots = (uint32_t *)rt->moe_slots.p;
     mb.hidden = (float *)rt->moe_hidden.p;
     mb.hidden_planes = (uint16_t *)rt->moe_hidden_planes.p;
     mb.x_planes = (uint16_t *)rt->moe_x_planes.p;
@@ -1141,10 +1155,6 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
     if (((uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
         return fail(PW_ERR_ARGUMENT, "route buffers must be 16-byte aligned");
     const uint32_t E = bank->n_experts, H = bank->hidden, I = bank->intermediate;
-    // the device schedule keeps one bit per (expert, row) in LDS (160 KB per workgroup)
-    const size_t sched_lds = ((size_t)E * ((rows + 31) / 32) + E) * 4;
-    if (sched_lds > 160 * 1024)
-        return fail(PW_ERR_ARGUMENT, "%u experts x %u rows exceed the schedule's LDS bitmap", E, rows);
     if (H % 128 || I % 128)
         return fail(PW_ERR_LAYOUT, "prefill needs hidden and intermediate sizes in multiples of 128");
     PW_HIP(set_device(rt));
@@ -1165,6 +1175,32 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
                            out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
                            out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
                            out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_moe_schedule_device(pw_runtime *rt, const pw_expert_bank *bank, const uint32_t *route_ids,
+                           const float *route_weights, uint32_t rows, uint32_t *expert_offsets,
+                           uint32_t *positions, float *weights, uint32_t *row_slots, void *stream)
+{
+    if (!rt || !bank || !route_ids || !route_weights || !expert_offsets || !positions || !weights || !row_slots)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (rows < 1 || rows > 4096)
+        return fail(PW_ERR_ARGUMENT, "schedule row count must be between one and 4096");
+    if (((uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
+        return fail(PW_ERR_ARGUMENT, "route buffers must be 16-byte aligned");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    const uint32_t E = bank->n_experts;
+    PW_TRY(ensure_sched(rt, rows, E));
+    const size_t P = (size_t)rows * 8;
+    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, std::min<uint32_t>(E, (uint32_t)P),
+                            rt->mb, rt->d_flags, s);
+    pw::launch_expert_offsets(rt->mb, E, expert_offsets, s);
+    PW_HIP(hipMemcpyAsync(positions, rt->mb.placement_pos, P * 4, hipMemcpyDeviceToDevice, s));
+    PW_HIP(hipMemcpyAsync(weights, rt->mb.placement_w, P * 4, hipMemcpyDeviceToDevice, s));
+    PW_HIP(hipMemcpyAsync(row_slots, rt->mb.row_slots, P * 4, hipMemcpyDeviceToDevice, s));
     PW_HIP(hipGetLastError());
     return PW_OK;
 }

@@ -348,6 +348,13 @@ class WideMoeRuntime:
         check(lib().pw_moe_prefill_device(self.handle, bank.handle, _ptr(x), x_dtype, rows, _ptr(route_ids),
                                           _ptr(route_weights), _ptr(out), out_dtype, stream or 0))
 
+    def moe_schedule_device(self, bank: ExpertBank, rows: int, route_ids, route_weights, expert_offsets,
+                            positions, weights, row_slots, stream: Optional[int] = None):
+        """The device routed schedule: expert_offsets [E + 1], positions / weights / row_slots [rows x 8]."""
+        check(lib().pw_moe_schedule_device(self.handle, bank.handle, _ptr(route_ids), _ptr(route_weights), rows,
+                                           _ptr(expert_offsets), _ptr(positions), _ptr(weights), _ptr(row_slots),
+                                           stream or 0))
+
     def route_device(self, x, rows: int, hidden: int, router_weight, experts: int, bias, route_ids, route_weights,
                      x_dtype: int = DTYPE_BF16, w_dtype: int = DTYPE_BF16, scores=None, tie_rows=None,
                      stream: Optional[int] = None):
