@@ -425,8 +425,10 @@ def main():
         d1 = upload(torch, WL, b1)
         s1 = [step_bytes(sel, 1) for _, sel, _ in b1]
         ms1 = time_layer(torch, rt, bank, P, d1, 1, args.steps, args.warmup, P.MODE_A)
+        kt1 = kernel_times(torch, rt, bank, P, d1, 1, max(20, args.steps // 4), P.MODE_A)
         extras["w1"] = {"layer_us": round(ms1 * 1000, 2),
-                        "GB/s": round(float(np.mean([b for _, b in s1])) / (ms1 * 1e-3) / 1e9, 1)}
+                        "GB/s": round(float(np.mean([b for _, b in s1])) / (ms1 * 1e-3) / 1e9, 1),
+                        "kernels_us": {k: round(v["avg_us"], 2) for k, v in kt1.items()}}
         for zipf in (False, True):
             extras["prefill_t2048" + ("_zipf" if zipf else "")] = prefill_leg(torch, rt, bank, P, WL, zipf)
         extras["router_w8"] = router_leg(torch, rt, P, WL)

@@ -223,12 +223,49 @@ def test_whole_k_gateup_matches_split_k(rt, full_bank):
     assert normwise(outs[1], ref_raw) <= 1e-3
 
 
-@pytest.mark.parametrize("rows", [8, 9])
+def test_one_token_equals_two_copies(rt, full_bank):
+    """Each token's result depends only on its own row and routes: a two-row batch holding the
+    same token twice (every routed expert then has two placements) gives the one-row result in both
+    rows, bit for bit, and that result matches the oracle."""
+    import torch
+    stream = torch.cuda.current_stream().cuda_stream
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    for seed in (0, 1, 2):
+        x = WL.activations(1, WL.SEED_BASE + 120 + seed)
+        _, _, sel, w, _ = O.route(x, rw, bias)
+        for out_dtype in (P.DTYPE_F32_RAW, P.DTYPE_BF16):
+            outs = []
+            for rows in (1, 2):
+                xr = np.repeat(x, rows, axis=0)
+                xt = torch.from_numpy(WL.bf16_bits_np(xr).view(np.int16)).cuda()
+                ids = torch.from_numpy(np.repeat(sel, rows, axis=0).astype(np.int32)).cuda()
+                wts = torch.from_numpy(np.repeat(w, rows, axis=0)).cuda()
+                out = torch.empty((rows, 4096), dtype=torch.float32 if out_dtype == P.DTYPE_F32_RAW else torch.int16,
+                                  device="cuda")
+                rt.moe_layer_device(full_bank.bank, xt, rows, ids, wts, out, mode=P.MODE_A, out_dtype=out_dtype,
+                                    stream=stream)
+                torch.cuda.synchronize()
+                assert rt.take_flags() == 0
+                outs.append(out.cpu().numpy())
+            bits = [o.view(np.uint32) if out_dtype == P.DTYPE_F32_RAW else o.view(np.uint16) for o in outs]
+            assert np.array_equal(bits[0][0], bits[1][0]) and np.array_equal(bits[0][0], bits[1][1])
+        experts = {e: full_bank.expert_host(e) for e in sorted(set(sel.reshape(-1).tolist()))}
+        _, ref_raw = O.moe_layer("a", x, experts, 256, sel, w, raw=True)
+        xt = torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda()
+        raw = torch.empty((1, 4096), dtype=torch.float32, device="cuda")
+        rt.moe_layer_device(full_bank.bank, xt, 1, torch.from_numpy(sel.astype(np.int32)).cuda(),
+                            torch.from_numpy(w).cuda(), raw, mode=P.MODE_A, out_dtype=P.DTYPE_F32_RAW, stream=stream)
+        torch.cuda.synchronize()
+        assert rt.take_flags() == 0
+        assert normwise(raw.cpu().numpy(), ref_raw) <= 1e-3
+
+
+@pytest.mark.parametrize("rows", [1, 8, 9])
 def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
     """Route buffers with an expert id outside the bank, one token naming an expert twice, or a NaN
     weight raise the schedule error bit (src/wide_metal_moe.rs:858-938 rejects such schedules) from
-    both schedule kernels (8 rows: one wave; 9 rows: one workgroup) without faulting, and the next
-    valid call gives the same bytes as before."""
+    both schedule kernels (1 and 8 rows: one wave; 9 rows: one workgroup) without faulting, and the
+    next valid call gives the same bytes as before."""
     import torch
     x = WL.activations(rows, WL.SEED_BASE + 90)
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
@@ -251,7 +288,7 @@ def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
     twice = sel.copy()
     twice[0, 1] = twice[0, 0]
     nan_w = w.copy()
-    nan_w[1, 5] = np.nan
+    nan_w[min(1, rows - 1), 5] = np.nan
     for ids, wts in ((bad_id, w), (twice, w), (sel, nan_w)):
         _, flags = run(ids, wts)
         assert flags & P.FLAG_SCHEDULE
