@@ -284,10 +284,10 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
     wait_vmcnt<2 * C::SB * C::WS>();
 
     // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each block's
-    // registers reloaded with step k + C::WS's block right after use. Whole groups of C::G steps run without early exits
-    // (static ring indices, one loop state at the loop head); the last steps are peeled. Load
-    // indices are clamped to the last step (the tail reloads it: cache hits), keeping every load
-    // unconditional.
+    // registers reloaded with step k + C::WS's block right after use. Whole groups of C::G steps
+    // run without early exits (static ring indices, one loop state at the loop head); the last
+    // steps are peeled. Load indices are clamped to the last step (the tail reloads it: cache
+    // hits), keeping every load unconditional.
     const uint32_t nfull = nsteps - nsteps % C::G;
     for (uint32_t b = 0; b < nfull; b += C::G) {
 #pragma unroll
