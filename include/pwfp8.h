@@ -211,7 +211,8 @@ int pw_bf16_linear_device(pw_runtime *rt, const void *input, uint32_t input_dtyp
  * (dynamic_fp8_quantized_group128, kernels/block_fp8_gemv.metal:84-137; CPU authority
  * dynamic_fp8_activations, src/text_endpoint.rs:3008-3051): scale = max(absmax, 1e-10)/448,
  * code = nearest e4m3fn of clamp(x/scale, +-448), ties to the even code. codes [rows x cols],
- * scales [rows x cols/128]. Non-finite inputs raise PW_FLAG_QUANT_NONFINITE. */
+ * scales [rows x cols/128]; x and codes 16-byte aligned. Non-finite inputs raise
+ * PW_FLAG_QUANT_NONFINITE. */
 int pw_quantize_fp8_group128_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows,
                                     uint32_t cols, uint8_t *codes, float *scales, void *stream);
 
@@ -263,10 +264,10 @@ void pw_expert_bank_release(pw_expert_bank *bank);
 int pw_expert_bank_shape(const pw_expert_bank *bank, uint32_t *n_experts, uint32_t *hidden,
                          uint32_t *intermediate);
 
-/* One routed-MoE layer with inputs already in device memory: x [rows x hidden] (x_dtype),
- * route_ids / route_weights [rows x 8] (the reference's RoutingTrace selected/weights,
- * src/text_endpoint.rs:4342-4380; 16-byte aligned), output [rows x hidden] (out_dtype, bf16-rounded). The
- * schedule is built on the device in the reference's BTreeMap order. rows <= 32.
+/* One routed-MoE layer with inputs already in device memory: x [rows x hidden] (x_dtype, 16-byte
+ * aligned), route_ids / route_weights [rows x 8] (the reference's RoutingTrace selected/weights,
+ * src/text_endpoint.rs:4342-4380; 16-byte aligned), output [rows x hidden] (out_dtype,
+ * bf16-rounded). The schedule is built on the device in the reference's BTreeMap order. rows <= 32.
  * Asynchronous on stream; kernel error bits accumulate in the runtime's error word. */
 int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
                         uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
@@ -277,8 +278,9 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
  * slices through WideMetalMoeRuntime::execute (run_layer_major_moe_slice_mode,
  * src/text_endpoint.rs:4951-5287; src/wide_metal_moe.rs:852-1314), here one grouped block-FP8
  * GEMM per projection on the FP8 MFMA (any number of placements per expert). x [rows x hidden]
- * (x_dtype), route_ids / route_weights [rows x 8] (16-byte aligned), output [rows x hidden] (out_dtype,
- * bf16-rounded). Asynchronous on stream; kernel error bits accumulate in the runtime's word. */
+ * (x_dtype), route_ids / route_weights [rows x 8] (x and the routes 16-byte aligned), output
+ * [rows x hidden] (out_dtype, bf16-rounded). Asynchronous on stream; kernel error bits accumulate
+ * in the runtime's word. */
 int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void *x, uint32_t x_dtype,
                           uint32_t rows, const uint32_t *route_ids, const float *route_weights, void *output,
                           uint32_t out_dtype, void *stream);
@@ -298,7 +300,7 @@ int pw_moe_schedule_device(pw_runtime *rt, const pw_expert_bank *bank, const uin
                            uint32_t *positions, float *weights, uint32_t *row_slots, void *stream);
 
 /* One complete expert (gate/up -> SwiGLU -> down, no routing, no combine) on device rows
- * x [rows x hidden] -> output [rows x hidden] bf16-rounded: the reference's complete-expert
+ * x [rows x hidden] (16-byte aligned) -> output [rows x hidden] bf16-rounded: the reference's complete-expert
  * measurement (direct-checkpoint L3 expert, src/lib.rs:4008-6590; mode A widths 1..8 via
  * block_fp8_gemm{w}_shared_weight_lut_blocked). rows <= 32. Asynchronous on stream. */
 int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t expert,

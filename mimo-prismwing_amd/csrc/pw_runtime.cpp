@@ -907,6 +907,8 @@ int pw_quantize_fp8_group128_device(pw_runtime *rt, const void *x, uint32_t x_dt
         return fail(PW_ERR_LAYOUT, "dynamic FP8 activation shape mismatch");
     if (x_dtype > PW_DTYPE_BF16)
         return fail(PW_ERR_ARGUMENT, "unknown dtype");
+    if (((uintptr_t)x | (uintptr_t)codes) & 15)
+        return fail(PW_ERR_ARGUMENT, "activations and codes must be 16-byte aligned");
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
@@ -1121,6 +1123,8 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
 {
     if (!rt || !bank || !x || !route_ids || !route_weights || !output)
         return fail(PW_ERR_ARGUMENT, "null argument");
+    if ((uintptr_t)x & 15)
+        return fail(PW_ERR_ARGUMENT, "activations must be 16-byte aligned");
     if (mode > PW_MODE_B || x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
         return fail(PW_ERR_ARGUMENT, "unknown mode or dtype");
     if (rows < 1 || rows > 32)
@@ -1148,6 +1152,8 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
 {
     if (!rt || !bank || !x || !route_ids || !route_weights || !output)
         return fail(PW_ERR_ARGUMENT, "null argument");
+    if ((uintptr_t)x & 15)
+        return fail(PW_ERR_ARGUMENT, "activations must be 16-byte aligned");
     if (x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
         return fail(PW_ERR_ARGUMENT, "unknown dtype");
     if (rows < 1 || rows > 4096)
@@ -1241,6 +1247,8 @@ int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_
 {
     if (!rt || !bank || !x || !output)
         return fail(PW_ERR_ARGUMENT, "null argument");
+    if ((uintptr_t)x & 15)
+        return fail(PW_ERR_ARGUMENT, "activations must be 16-byte aligned");
     if (mode > PW_MODE_B || x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
         return fail(PW_ERR_ARGUMENT, "unknown mode or dtype");
     if (expert >= bank->n_experts)

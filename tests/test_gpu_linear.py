@@ -186,6 +186,18 @@ def quantize_device(rt, data):
     return codes.cpu().numpy(), scales.cpu().numpy()
 
 
+def test_quantiser_rejects_misaligned_buffers(rt):
+    torch = _torch()
+    base = torch.zeros(2 * 128 + 8, dtype=torch.float32, device="cuda")
+    codes = torch.empty((2, 128), dtype=torch.uint8, device="cuda")
+    scales = torch.empty((2, 1), dtype=torch.float32, device="cuda")
+    with pytest.raises(P.PwError, match="ARGUMENT"):
+        rt.quantize_fp8_group128_device(base[1:257], 2, 128, codes, scales)
+    raw = torch.empty(2 * 128 + 16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(P.PwError, match="ARGUMENT"):
+        rt.quantize_fp8_group128_device(base[:256], 2, 128, raw[4:260], scales)
+
+
 def test_quantiser_flags_nonfinite(rt):
     torch = _torch()
     data = np.ones((1, 128), np.float32)

@@ -260,6 +260,17 @@ def test_one_token_equals_two_copies(rt, full_bank):
         assert normwise(raw.cpu().numpy(), ref_raw) <= 1e-3
 
 
+def test_device_layer_rejects_misaligned_activations(rt, full_bank):
+    import torch
+    x = torch.zeros(4096 + 8, dtype=torch.int16, device="cuda")[1:4097].view(1, 4096)
+    ids = torch.zeros((1, 8), dtype=torch.int32, device="cuda")
+    ids[0] = torch.arange(8, dtype=torch.int32)
+    w = torch.full((1, 8), 0.125, dtype=torch.float32, device="cuda")
+    out = torch.empty((1, 4096), dtype=torch.int16, device="cuda")
+    with pytest.raises(P.PwError, match="ARGUMENT"):
+        rt.moe_layer_device(full_bank.bank, x, 1, ids, w, out)
+
+
 @pytest.mark.parametrize("rows", [1, 8, 9])
 def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
     """Route buffers with an expert id outside the bank, one token naming an expert twice, or a NaN
