@@ -278,8 +278,8 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
  * slices through WideMetalMoeRuntime::execute (run_layer_major_moe_slice_mode,
  * src/text_endpoint.rs:4951-5287; src/wide_metal_moe.rs:852-1314), here one grouped block-FP8
  * GEMM per projection on the FP8 MFMA (any number of placements per expert). x [rows x hidden]
- * (x_dtype), route_ids / route_weights [rows x 8] (x and the routes 16-byte aligned), output
- * [rows x hidden] (out_dtype, bf16-rounded). Asynchronous on stream; kernel error bits accumulate
+ * (x_dtype), route_ids / route_weights [rows x 8], output [rows x hidden] (out_dtype,
+ * bf16-rounded); x, the routes and the output 16-byte aligned. Asynchronous on stream; kernel error bits accumulate
  * in the runtime's word. */
 int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void *x, uint32_t x_dtype,
                           uint32_t rows, const uint32_t *route_ids, const float *route_weights, void *output,

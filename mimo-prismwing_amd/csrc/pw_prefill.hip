@@ -16,12 +16,13 @@
 // Tiles: (96 placement slots of one routed expert = an m-tile) x (128 weight rows = an n-tile);
 // 96 slots hold a whole expert's placements at the uniform-routing count (64 on average), so its
 // weights stream once. Gate and up run as one stacked projection (2I output columns per slot),
-// then a SwiGLU + re-quantisation kernel, then down. A workgroup walks K in 128-column steps with
+// then a SwiGLU + re-quantisation kernel, then down. A workgroup walks K in 256-column steps with
 // two kinds of waves, so the two streams never wait on each other in the in-order memory counter:
 // eight consumer waves (16 weight rows each) load their weight bytes (one row per lane) into a
-// four-step register ring and run the MFMAs; one producer wave copies the m-tile's activation
-// codes (cache hits, shared by the expert's n-tiles) with direct-to-LDS loads into a four-step LDS
-// ring (16-byte units XOR-swizzled by token so the B-operand reads spread over the LDS banks).
+// register ring (two steps of two 128-column blocks) and run the MFMAs; one producer wave copies
+// the m-tile's activation codes (cache hits, shared by the expert's n-tiles) with direct-to-LDS
+// loads into a two-step LDS ring (16-byte units XOR-swizzled by token so the B-operand reads
+// spread over the LDS banks).
 // One LDS-only barrier per step publishes a ring slot and frees the previous one; the weight
 // stream stays in flight across it. The m-tile's activation scales (transposed, [block][token])
 // and the tile's weight block scales are staged in LDS once.
@@ -381,41 +382,61 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
 }
 
 // route_weighted_scatter_add_f32 + final bf16 round over bf16 expert outputs: each token sums
-// its eight placements in ascending expert id, out += y * w in f32 (no fused multiply-add).
+// its eight placements in ascending expert id, out += y * w in f32 (no fused multiply-add). One
+// thread per eight consecutive columns of a token row (16-byte loads of each placement's outputs).
 __global__ __launch_bounds__(256) void prefill_combine_kernel(
     const uint16_t *__restrict__ y, const float *__restrict__ placement_w, const uint32_t *__restrict__ row_slots,
     uint32_t rows, uint32_t H, float *__restrict__ out_f32, uint16_t *__restrict__ out_bf16, uint32_t raw,
     uint32_t *flags)
 {
-    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;  // four values of one token row
-    const uint32_t per_row = H >> 2;
+    const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;  // eight values of one token row
+    const uint32_t per_row = H >> 3;
     if (idx >= rows * per_row)
         return;
-    const uint32_t row = idx / per_row, c4 = idx - row * per_row;
+    const uint32_t row = idx / per_row, c8 = idx - row * per_row;
     const uint32_t P = rows * 8;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const uint4 s0 = *(const uint4 *)(row_slots + (size_t)row * 8), s1 = *(const uint4 *)(row_slots + (size_t)row * 8 + 4);
+    uint32_t slot[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    float w[8];
+    uint4 v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        uint32_t slot = row_slots[row * 8 + j];
-        slot = slot < P ? slot : 0;
-        const float w = placement_w[slot];
-        const uint2 v = *(const uint2 *)(y + (size_t)slot * H + c4 * 4);
-        const float f[4] = {f32_from(v.x << 16), f32_from(v.x & 0xffff0000u), f32_from(v.y << 16),
-                            f32_from(v.y & 0xffff0000u)};
+        slot[j] = slot[j] < P ? slot[j] : 0;
+        w[j] = placement_w[slot[j]];
+        v[j] = *(const uint4 *)(y + (size_t)slot[j] * H + c8 * 8);
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            acc[i] = __fadd_rn(acc[i], __fmul_rn(f[i], w));
+    for (int j = 0; j < 8; ++j) {
+        const uint32_t u[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[2 * i] = __fadd_rn(acc[2 * i], __fmul_rn(f32_from(u[i] << 16), w[j]));
+            acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __fmul_rn(f32_from(u[i] & 0xffff0000u), w[j]));
+        }
     }
     bool bad = false;
-    const size_t at = (size_t)row * H + c4 * 4;
+    const size_t at = (size_t)row * H + c8 * 8;
+    float r[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float r = round_bf16(acc[i]);
-        bad |= !finite_f32(r);
-        if (out_f32)
-            out_f32[at + i] = raw ? acc[i] : r;
-        if (out_bf16)
-            out_bf16[at + i] = (uint16_t)(f32_bits(r) >> 16);
+    for (int i = 0; i < 8; ++i) {
+        r[i] = round_bf16(acc[i]);
+        bad |= !finite_f32(r[i]);
+    }
+    if (out_f32) {
+        float o[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            o[i] = raw ? acc[i] : r[i];
+        *(float4 *)(out_f32 + at) = make_float4(o[0], o[1], o[2], o[3]);
+        *(float4 *)(out_f32 + at + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    if (out_bf16) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            pk[i] = (f32_bits(r[2 * i]) >> 16) | (f32_bits(r[2 * i + 1]) & 0xffff0000u);
+        *(uint4 *)(out_bf16 + at) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
     if (bad)
         raise_flag(flags, FLAG_ROUND_NONFINITE);
@@ -497,9 +518,9 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     launch_prefill_projection(da, stream);
     timer_end(t, stream);
 
-    const uint32_t n4 = rows * (H >> 2);
+    const uint32_t n8 = rows * (H >> 3);
     t = timer_begin(K_MOE_COMBINE, stream);
-    hipLaunchKernelGGL(prefill_combine_kernel, dim3((n4 + 255) / 256), dim3(256), 0, stream, pb.y, mb.placement_w,
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3((n8 + 255) / 256), dim3(256), 0, stream, pb.y, mb.placement_w,
                        mb.row_slots, rows, H, out_f32, out_bf16, raw ? 1u : 0u, flags);
     timer_end(t, stream);
 }

@@ -1152,8 +1152,8 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
 {
     if (!rt || !bank || !x || !route_ids || !route_weights || !output)
         return fail(PW_ERR_ARGUMENT, "null argument");
-    if ((uintptr_t)x & 15)
-        return fail(PW_ERR_ARGUMENT, "activations must be 16-byte aligned");
+    if (((uintptr_t)x | (uintptr_t)output) & 15)
+        return fail(PW_ERR_ARGUMENT, "activations and output must be 16-byte aligned");
     if (x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
         return fail(PW_ERR_ARGUMENT, "unknown dtype");
     if (rows < 1 || rows > 4096)
