@@ -116,12 +116,12 @@ def _decode_chunks(rt, torch, bank, x, sel, w, chunk=32):
     return _from_bf16(out)
 
 
-@pytest.mark.parametrize("zipf", [False, True])
-def test_prefill_2048_tokens_matches_decode_chunks(rt, full_bank, zipf):
-    """2048 tokens, top-8 of 256 experts (16 384 placements): the prefill equals the decode layer
-    run on 32-row chunks (the same mode B numerics per placement) and, on sampled rows, the oracle."""
+@pytest.mark.parametrize("rows,zipf", [(2048, False), (2048, True), (4096, False)])
+def test_prefill_matches_decode_chunks(rt, full_bank, rows, zipf):
+    """2048 tokens (and the 4096-row maximum), top-8 of 256 experts (16 384 / 32 768 placements):
+    the prefill equals the decode layer run on 32-row chunks (the same mode B numerics per
+    placement) and, on sampled rows, the oracle."""
     import torch
-    rows = 2048
     x = WL.activations(rows, WL.SEED_BASE + 4)
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
     sel, w, _ = WL.route_host(x, rw, bias)
@@ -132,7 +132,7 @@ def test_prefill_2048_tokens_matches_decode_chunks(rt, full_bank, zipf):
     assert normwise(got, dec) <= MODE_B_TOL
     assert rel_l2(got, dec) <= 2e-3
     # oracle on three sampled rows (only their experts are fetched)
-    pick = np.array([0, 1111, 2047])
+    pick = np.array([0, 1111, rows - 1])
     used = sorted(set(sel[pick].reshape(-1).tolist()))
     experts = {e: full_bank.expert_host(e) for e in used}
     ref = O.moe_layer("b", x[pick], experts, 256, sel[pick], w[pick])
