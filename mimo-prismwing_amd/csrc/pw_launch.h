@@ -62,8 +62,8 @@ struct MoeBuffers {
     uint16_t *x_planes;        // [3][rows][H]        mode A f32 activations as bf16 planes
     float *y;                  // [rows * 8 * H]
     ActiveExpert *active;      // [E]   per routed expert: weights, placement slots
-    ActiveExpert *down_active; // [rows * 8] decode batches (<= 8 rows): the routed experts' slots
-                               // in pieces of at most four rows, for the down projection
+    ActiveExpert *pieces;      // [rows * 8] decode batches (<= 8 rows): the routed experts' slots
+                               // in pieces of at most four rows, for the projections
     float *partial;            // split-K partial sums of the mode A projections
     uint8_t *xq;               // [rows * H]      mode B activation codes
     float *xs;                 // [rows * H/128]  mode B activation scales

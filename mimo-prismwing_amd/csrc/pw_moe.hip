@@ -479,8 +479,8 @@ void launch_expert_offsets(const MoeBuffers &mb, uint32_t E, uint32_t *expert_of
                        mb.active_expert, mb.active_offset, E, expert_offsets);
 }
 
-// Rows per down-projection entry when the one-wave schedule cuts experts into pieces.
-constexpr uint32_t DOWN_PIECE_ROWS = 4;
+// Rows per projection entry when the one-wave schedule cuts experts into pieces.
+constexpr uint32_t PIECE_ROWS = 4;
 
 // The schedule of a decode batch runs in one wave (moe_schedule_wave_kernel) under these bounds.
 static bool wave_schedule(uint32_t rows, uint32_t E, uint32_t max_active)
@@ -510,8 +510,8 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
     const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids, const float *__restrict__ weights,
     uint32_t rows, uint32_t E, uint32_t max_active, MoePlan *plan, uint32_t *__restrict__ active_expert,
     uint32_t *__restrict__ active_offset, ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos,
-    float *__restrict__ placement_w, uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ down_active,
-    uint32_t max_down, uint32_t *flags)
+    float *__restrict__ placement_w, uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces,
+    uint32_t max_pieces, uint32_t *flags)
 {
     extern __shared__ u32x4 lds_bank[];  // the bank's ExpertPtrs table, E x 48 bytes
     __shared__ uint32_t bitmap[32];      // routed expert ids (E <= 1024)
@@ -621,26 +621,29 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
     }
     if (lane == 0)
         active_offset[U] = total;
-    // the down projection's entries: each routed expert's slots in pieces of at most
-    // DOWN_PIECE_ROWS, so its LDS stage is sized for that many rows (see launch_a_moe)
-    const uint32_t np = (c_a + DOWN_PIECE_ROWS - 1) / DOWN_PIECE_ROWS;  // 0 past the routed experts
+    // the projections' entries: each routed expert's slots in pieces of at most PIECE_ROWS, so
+    // their LDS stages are sized for that many rows (see launch_a_moe); a piece carries its slots'
+    // token rows (slots 0..15 of an expert: PIECE_ROWS * pieces <= 16 here)
+    const uint32_t np = (c_a + PIECE_ROWS - 1) / PIECE_ROWS;  // 0 past the routed experts
     const uint32_t pincl = wave_inclusive_scan(np, lane);
     const uint32_t pbase = pincl - np, npieces = __builtin_amdgcn_readlane(pincl, 63);
     for (uint32_t i = 0; i < np; ++i) {
-        if (pbase + i < max_down) {
-            const uint32_t left = c_a - i * DOWN_PIECE_ROWS;
-            const uint32_t pc = left < DOWN_PIECE_ROWS ? left : DOWN_PIECE_ROWS;
-            u32x4 *dst = (u32x4 *)(down_active + pbase + i);
+        if (pbase + i < max_pieces) {
+            const uint32_t left = c_a - i * PIECE_ROWS;
+            const uint32_t pc = left < PIECE_ROWS ? left : PIECE_ROWS;
+            const uint16_t *tk = tok_of + a * 16 + i * PIECE_ROWS;
+            u32x4 *dst = (u32x4 *)(pieces + pbase + i);
             dst[0] = ep0;
             dst[1] = ep1;
             dst[2] = ep2;
-            dst[3] = u32x4{off_a + i * DOWN_PIECE_ROWS, pc, 0u, 0u};
+            dst[3] = u32x4{off_a + i * PIECE_ROWS, pc, (uint32_t)tk[0] | ((uint32_t)tk[1] << 16),
+                           (uint32_t)tk[2] | ((uint32_t)tk[3] << 16)};
             dst[4] = u32x4{0u, 0u, 0u, 0u};
             dst[5] = u32x4{0u, 0u, 0u, 0u};
         }
     }
-    for (uint32_t d = npieces + (uint32_t)lane; d < max_down; d += 64) {
-        u32x4 *dst = (u32x4 *)(down_active + d);
+    for (uint32_t d = npieces + (uint32_t)lane; d < max_pieces; d += 64) {
+        u32x4 *dst = (u32x4 *)(pieces + d);
 #pragma unroll
         for (int i = 0; i < 6; ++i)
             dst[i] = u32x4{0u, 0u, 0u, 0u};
@@ -1048,7 +1051,7 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)table);
         hipLaunchKernelGGL(moe_schedule_wave_kernel, dim3(1), dim3(64), table, stream, bank, ids, weights, rows, E,
                            max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active, mb.placement_pos,
-                           mb.placement_w, mb.row_slots, mb.down_active, rows * 8, flags);
+                           mb.placement_w, mb.row_slots, mb.pieces, rows * 8, flags);
     }
     else if (rows <= SCHED_WG_MAX_ROWS)
         hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
@@ -1100,7 +1103,18 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     const SplitPlan gp = plan_split(H, 2, x_f32 ? 3 : 1, cnt);
     ga.KS = gp.ks;
     int t = timer_begin(K_MOE_GATEUP, stream);
-    const bool fused = nt == 1 && launch_moe_a_gateup_fused(x_f32 ? 3 : 1, ga, max_active, mb.hidden_planes, stream);
+    // the one-wave schedule also cut every routed expert's slots into entries of at most
+    // PIECE_ROWS rows (with their token rows): a decode batch gives most experts one to three
+    // rows, and LDS stages sized for four rows let more workgroups share a CU (an expert with more
+    // rows reads its weights once per piece; every slot's arithmetic is unchanged)
+    const bool pieces = !one && cnt > PIECE_ROWS && wave_schedule(rows, mb.experts, max_active);
+    SplitArgs gp_args = ga;
+    if (pieces && !x_f32) {
+        gp_args.active = mb.pieces;
+        gp_args.cap = PIECE_ROWS;
+    }
+    const bool fused = nt == 1 && launch_moe_a_gateup_fused(x_f32 ? 3 : 1, gp_args, pieces && !x_f32 ? placements
+                                                            : max_active, mb.hidden_planes, stream);
     if (!fused)
         launch_moe_a_split(2, x_f32 ? 3 : 1, nt, ga, gp, max_active, stream);
     timer_end(t, stream);
@@ -1117,16 +1131,13 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     da.K = I;
     da.R = H;
     da.rows = placements;
-    // the one-wave schedule also cut every routed expert's slots into down-projection entries of
-    // at most DOWN_PIECE_ROWS rows: a decode batch gives most experts one to three rows, and an
-    // LDS stage of four rows (25 KB at hidden 4096) fits five workgroups per CU instead of three
-    // at eight rows (an expert with more rows reads its down weights once per piece)
-    const bool pieces = !one && cnt > DOWN_PIECE_ROWS && wave_schedule(rows, mb.experts, max_active);
+    // down in pieces: a four-row LDS stage (25 KB at hidden 4096) fits five workgroups per CU
+    // instead of three at eight rows
     if (pieces) {
-        da.active = mb.down_active;
-        da.cap = DOWN_PIECE_ROWS;
+        da.active = mb.pieces;
+        da.cap = PIECE_ROWS;
     }
-    const SplitPlan dp = plan_split(I, 1, 3, pieces ? DOWN_PIECE_ROWS : cnt);
+    const SplitPlan dp = plan_split(I, 1, 3, pieces ? PIECE_ROWS : cnt);
     da.KS = dp.ks;
     t = timer_begin(K_MOE_DOWN, stream);
     launch_moe_a_split(1, 3, pieces ? 1 : nt, da, dp, pieces ? placements : max_active, stream);

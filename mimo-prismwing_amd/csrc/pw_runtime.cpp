@@ -106,7 +106,7 @@ struct pw_runtime {
     // routed-MoE per-layer scratch
     DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
         moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
-        moe_active, moe_down_active, moe_partial, moe_sched, pf_tiles, router_scores, bf16_partial;
+        moe_active, moe_pieces, moe_partial, moe_sched, pf_tiles, router_scores, bf16_partial;
     MoeBuffers mb{};
     pw::KernelTimer timer;
 };
@@ -273,7 +273,7 @@ int ensure_sched(pw_runtime *rt, uint32_t rows, uint32_t E)
     PW_HIP(rt->moe_w.ensure(P * 4));
     PW_HIP(rt->moe_slots.ensure(P * 4));
     PW_HIP(rt->moe_active.ensure((size_t)(E + 1) * sizeof(pw::ActiveExpert)));
-    PW_HIP(rt->moe_down_active.ensure((P + 1) * sizeof(pw::ActiveExpert)));
+    PW_HIP(rt->moe_pieces.ensure((P + 1) * sizeof(pw::ActiveExpert)));
     if (const size_t sched = pw::moe_sched_scratch_bytes(rows, E))
         PW_HIP(rt->moe_sched.ensure(sched));
     MoeBuffers &mb = rt->mb;
@@ -284,7 +284,7 @@ int ensure_sched(pw_runtime *rt, uint32_t rows, uint32_t E)
     mb.placement_w = (float *)rt->moe_w.p;
     mb.row_slots = (uint32_t *)rt->moe_slots.p;
     mb.active = (pw::ActiveExpert *)rt->moe_active.p;
-    mb.down_active = (pw::ActiveExpert *)rt->moe_down_active.p;
+    mb.pieces = (pw::ActiveExpert *)rt->moe_pieces.p;
     mb.sched = rt->moe_sched.p;
     return PW_OK;
 }
