@@ -223,18 +223,19 @@ def test_whole_k_gateup_matches_split_k(rt, full_bank):
     assert normwise(outs[1], ref_raw) <= 1e-3
 
 
-def test_down_pieces_match_one_workgroup_schedule(rt, full_bank):
-    """A decode batch of up to 8 rows stages the down projection four rows at a time: its one-wave
-    schedule cuts each expert's slots into pieces of at most four. With every token on the same
-    eight experts (eight slots each: two pieces), the first 8 rows of a 9-row batch (one-workgroup
-    schedule, one piece per expert) equal the 8-row batch bit for bit."""
+@pytest.mark.parametrize("width", [5, 6, 8])
+def test_pieces_match_one_workgroup_schedule(rt, full_bank, width):
+    """A decode batch of 5 to 8 rows runs both projections on pieces of at most four slots of an
+    expert (its one-wave schedule cuts them). With every token on the same eight experts (width
+    slots each: pieces of 4 + 1, 4 + 2, 4 + 4), the first rows of a 9-row batch (one-workgroup
+    schedule, no pieces) equal the smaller batch bit for bit."""
     import torch
     x = WL.activations(9, WL.SEED_BASE + 130)
     sel = np.tile(np.array([17, 3, 250, 99, 128, 64, 5, 200], np.uint32), (9, 1))
     w = np.random.default_rng(5).uniform(0.01, 0.3, (9, 8)).astype(np.float32)
     stream = torch.cuda.current_stream().cuda_stream
     outs = []
-    for rows in (8, 9):
+    for rows in (width, 9):
         xt = torch.from_numpy(WL.bf16_bits_np(x[:rows]).view(np.int16)).cuda()
         ids = torch.from_numpy(sel[:rows].astype(np.int32)).cuda()
         wts = torch.from_numpy(w[:rows]).cuda()
@@ -244,9 +245,9 @@ def test_down_pieces_match_one_workgroup_schedule(rt, full_bank):
         torch.cuda.synchronize()
         assert rt.take_flags() == 0
         outs.append(raw.cpu().numpy())
-    assert np.array_equal(outs[0].view(np.uint32), outs[1][:8].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1][:width].view(np.uint32))
     experts = {e: full_bank.expert_host(e) for e in sorted(set(sel.reshape(-1).tolist()))}
-    _, ref_raw = O.moe_layer("a", x[:8], experts, 256, sel[:8], w[:8], raw=True)
+    _, ref_raw = O.moe_layer("a", x[:width], experts, 256, sel[:width], w[:width], raw=True)
     assert normwise(outs[0], ref_raw) <= 1e-3
 
 
