@@ -1,7 +1,7 @@
 """GPU parity of the block-scaled FP8 projections (modes A and B, plain / segmented / TP4 layouts)
 against the C oracle, through the C ABI.
 
-Tolerances (BASELINE north star): mode A f32 accumulation <= 1e-3 max|d|/max|ref| on the f32
+Tolerances: mode A f32 accumulation <= 1e-3 max|d|/max|ref| on the f32
 result before the final bf16 round (in practice ~1e-7: products are exact, only the summation
 order differs), and bf16 outputs within one bf16 rounding step plus 1e-5 * sum|terms| of the
 oracle's; mode B <= 2e-2 max|d|/max|ref|. Integer work (codes, scales) is bit-exact.
