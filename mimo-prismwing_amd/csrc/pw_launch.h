@@ -175,7 +175,9 @@ struct PrefillBuffers {
     uint32_t *n_tiles;  // [1]
     uint16_t *hidden;   // [rows * 8][2I] bf16 gate and up outputs
     uint16_t *y;        // [rows * 8][H] bf16 expert outputs
+    const uint16_t *silu;  // [65536] bf16-staged silu of every bf16 gate, from launch_silu_table
 };
+void launch_silu_table(uint16_t *table, hipStream_t stream);
 uint32_t prefill_max_tiles(uint32_t rows, uint32_t E);
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,

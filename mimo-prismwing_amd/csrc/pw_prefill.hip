@@ -326,14 +326,34 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
     }
 }
 
+// silu of a bf16 gate as the bf16-staged SwiGLU rounds it, round(g / (1 + e^-g))
+// (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343), for all 65,536 bf16
+// bit patterns: the table entry of bits b is the function's value at the bf16 number b, computed
+// by this expression once, so a lookup gives the same bits as evaluating it in place.
+__device__ __forceinline__ float silu_bf16_staged(float g) { return round_bf16(g / (1.0f + expf(-g))); }
+
+__global__ __launch_bounds__(256) void silu_table_kernel(uint16_t *__restrict__ table)
+{
+    const uint32_t b = blockIdx.x * 256 + threadIdx.x;  // grid covers exactly 65,536 entries
+    table[b] = (uint16_t)(f32_bits(silu_bf16_staged(f32_from(b << 16))) >> 16);
+}
+
+void launch_silu_table(uint16_t *table, hipStream_t stream)
+{
+    hipLaunchKernelGGL(silu_table_kernel, dim3(256), dim3(256), 0, stream, table);
+}
+
 // bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343)
 // on the bf16 gate/up outputs, h = round(round(g / (1 + e^-g)) * u), fused with the dynamic
 // per-(slot, 128-column group) re-quantisation of h for the down projection
 // (dynamic_fp8_quantized_group128, kernels/block_fp8_gemv.metal:84-137). 16 lanes per group,
 // eight consecutive values per lane (16-byte loads of gate and up), four groups per wave;
-// gu [P][2I] bf16 (gate columns, then up).
+// gu [P][2I] bf16 (gate columns, then up). The silu factor comes from silu_table (65,536 bf16
+// entries indexed by the gate's bits, built by silu_table_kernel), which keeps the exponential
+// and the division out of this VALU-bound kernel.
 __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_t *__restrict__ gu, uint32_t P,
-                                                                   uint32_t I, uint8_t *__restrict__ codes,
+                                                                   uint32_t I, const uint16_t *__restrict__ silu_table,
+                                                                   uint8_t *__restrict__ codes,
                                                                    float *__restrict__ scales, uint32_t *flags)
 {
     const uint32_t lane16 = threadIdx.x & 15;
@@ -345,6 +365,10 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
     const uint16_t *row = gu + (size_t)slot * 2 * I;
     const uint4 g4 = *(const uint4 *)(row + c), u4 = *(const uint4 *)(row + I + c);
     const uint32_t gw[4] = {g4.x, g4.y, g4.z, g4.w}, uw[4] = {u4.x, u4.y, u4.z, u4.w};
+    uint32_t sb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        sb[i] = load_g(silu_table + ((i & 1) ? (gw[i >> 1] >> 16) : (gw[i >> 1] & 0xffffu)));
     float h[8];
     bool bad = false;
 #pragma unroll
@@ -352,8 +376,7 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
         const uint32_t gb = gw[i >> 1], ub = uw[i >> 1];
         const float gv = f32_from((i & 1) ? (gb & 0xffff0000u) : (gb << 16));
         const float uv = f32_from((i & 1) ? (ub & 0xffff0000u) : (ub << 16));
-        const float silu = round_bf16(gv / (1.0f + expf(-gv)));
-        h[i] = round_bf16(silu * uv);
+        h[i] = round_bf16(f32_from(sb[i] << 16) * uv);
         bad |= !finite_f32(gv) || !finite_f32(uv) || !finite_f32(h[i]);
     }
     if (bad)
@@ -502,7 +525,7 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     const uint32_t groups = P * (I >> 7);
     t = timer_begin(K_MOE_SWIGLU, stream);
     hipLaunchKernelGGL(prefill_swiglu_quant_kernel, dim3((groups + 15) / 16), dim3(256), 0, stream, pb.hidden, P,
-                       I, mb.hq, mb.hs, flags);
+                       I, pb.silu, mb.hq, mb.hs, flags);
     timer_end(t, stream);
 
     PrefillArgs da = ga;

@@ -106,7 +106,7 @@ struct pw_runtime {
     // routed-MoE per-layer scratch
     DevBuf moe_plan, moe_active_expert, moe_active_offset, moe_pos, moe_w, moe_slots, moe_hidden,
         moe_hidden_planes, moe_x_planes, moe_y, moe_xq, moe_xs, moe_hq, moe_hs, lin_planes,
-        moe_active, moe_pieces, moe_partial, moe_sched, pf_tiles, router_scores, bf16_partial;
+        moe_active, moe_pieces, moe_partial, moe_sched, pf_tiles, pf_silu, router_scores, bf16_partial;
     MoeBuffers mb{};
     pw::KernelTimer timer;
 };
@@ -1176,6 +1176,13 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
     pb.n_tiles = (uint32_t *)((char *)rt->pf_tiles.p + (size_t)max_tiles * 8);
     pb.hidden = (uint16_t *)rt->moe_hidden.p;  // [P][I] f32 scratch holds the bf16 hidden
     pb.y = (uint16_t *)rt->moe_y.p;            // [P][H] f32 scratch holds the bf16 outputs
+    if (!rt->pf_silu.p) {  // built once per runtime, and complete before any stream reads it
+        PW_HIP(rt->pf_silu.ensure(65536 * sizeof(uint16_t)));
+        pw::launch_silu_table((uint16_t *)rt->pf_silu.p, rt->stream);
+        PW_HIP(hipGetLastError());
+        PW_HIP(hipStreamSynchronize(rt->stream));
+    }
+    pb.silu = (const uint16_t *)rt->pf_silu.p;
     const uint32_t P = rows * 8;
     pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, std::min<uint32_t>(E, P), rt->mb,
                             rt->d_flags, s);
