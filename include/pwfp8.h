@@ -280,7 +280,8 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
  * GEMM per projection on the FP8 MFMA (any number of placements per expert). x [rows x hidden]
  * (x_dtype), route_ids / route_weights [rows x 8], output [rows x hidden] (out_dtype,
  * bf16-rounded); x, the routes and the output 16-byte aligned. Asynchronous on stream; kernel error bits accumulate
- * in the runtime's word. */
+ * in the runtime's word. The first call on a runtime also builds a 128 KB silu table on the
+ * runtime's stream and waits for that stream once. */
 int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void *x, uint32_t x_dtype,
                           uint32_t rows, const uint32_t *route_ids, const float *route_weights, void *output,
                           uint32_t out_dtype, void *stream);
