@@ -661,6 +661,15 @@ static int build_schedule(size_t rows, size_t n_experts, const uint32_t *selecte
             return -1;
         slots[selected[i]].count++;
     }
+    /* A token naming one expert twice is not a placement bijection: the reference's routes never
+     * hold one (pytorch_noaux_routes checks the selected set, src/text_endpoint.rs:4426-4432) and
+     * reconstruct_routed_from_schedule rejects a repeated (position, expert) pair
+     * (src/text_endpoint.rs:10681-10710). */
+    for (size_t p = 0; p < rows; ++p)
+        for (size_t s = 0; s < top_k; ++s)
+            for (size_t t = s + 1; t < top_k; ++t)
+                if (selected[p * top_k + s] == selected[p * top_k + t])
+                    return -1;
     for (size_t e = 0; e < n_experts; ++e) {
         slots[e].positions = slots[e].count ? (size_t *)malloc(slots[e].count * sizeof(size_t)) : NULL;
         slots[e].weights = slots[e].count ? (float *)malloc(slots[e].count * sizeof(float)) : NULL;

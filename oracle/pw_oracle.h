@@ -21,16 +21,24 @@
  *                            activation codes are exact and scales are 1
  *   pwo_fp8_linear_mode_b    f64 brute force on tiny shapes; bf16-rounding idempotence
  *   pwo_swiglu_f32           golden swiglu-f32.json (f64 oracle)
+ *   pwo_swiglu_bf16_staged   known answers where dropping any one of the four bf16 roundings changes
+ *                            the bits (incl. the reference's gate 1.03125 / up 0.71484375 case and a
+ *                            tie of the product)
  *   pwo_sleef_expf_u10       golden pw0068-sleef-boundaries.json; pw0062 via the sigmoid
  *   pwo_sigmoid_f32          golden pw0062-router-sigmoid.json, pw0068
  *   pwo_topk_unsorted        golden pw0063-topk-order.json + 5 tie cases of pw0157 (order and set)
- *   pwo_noaux_routes         pw0157 tie counting; weights sum to 1 within 1e-6; tiny-MoE fixture set
+ *   pwo_noaux_routes         pw0157 tie counting; selected set = top 8 of the corrected scores and
+ *                            weights = uncorrected scores over their sum (f64), summing to 1 within 1e-6
  *   pwo_router_logits_t256   known-answer sums whose f32 value fixes the fma, the column order, the
  *                            lane tree and the wave order; f64 brute force (tolerance). The order is
  *                            this build's declared one; the reference's (Apple Accelerate SGEMM) is
  *                            closed
- *   pwo_moe_layer_mode_a/_b  schedule bijection + exact reconstruction with one-hot weights; f64
- *                            brute force on tiny shapes; moe-noaux-tc-swiglu.json structure
+ *   pwo_moe_layer_mode_a/_b  the reference's tiny noaux-tc MoE fixture (moe-noaux-tc-swiglu.json,
+ *                            each weight carried by its own 128x128 block); f64 brute force on tiny
+ *                            FP8 shapes; bit equality with the routed composition of the pinned
+ *                            projections and SwiGLU; one-hot route weights reproduce the expert bit
+ *                            for bit; repeated (token, expert) pairs rejected
+ *   pwo_expert_mode_a        f64 brute force; its bf16 output is the round of its f32 output
  *   pwo_full/swa_qkv_*       known-answer row/scale maps of src/text_endpoint.rs:13686-13732
  */
 #ifndef PW_ORACLE_H
