@@ -18,7 +18,11 @@
  * Threading: one runtime per device, calls on one runtime are serialised by the caller (the
  * reference's &self + one command queue). Host-memory calls are synchronous like the reference;
  * the *_device calls are asynchronous on the HIP stream given (NULL = the runtime's stream, a
- * blocking stream, so it is ordered with work on the HIP null stream).
+ * blocking stream, so it is ordered with work on the HIP null stream). Calls share the runtime's
+ * scratch buffers, so the runtime orders each call's GPU work after the previous call's: a call
+ * on another stream than the previous call makes its stream wait for the previous call's work
+ * first (nothing is waited for while calls keep to one stream). A caller's stream is not used
+ * after the call returns. To overlap work, use one runtime per stream.
  */
 #ifndef PWFP8_H
 #define PWFP8_H
@@ -215,6 +219,16 @@ int pw_bf16_linear_device(pw_runtime *rt, const void *input, uint32_t input_dtyp
  * PW_FLAG_QUANT_NONFINITE. */
 int pw_quantize_fp8_group128_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t rows,
                                     uint32_t cols, uint8_t *codes, float *scales, void *stream);
+
+/* bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160, the reference's own elementwise pass
+ * between the gate/up and down projections; CPU src/text_endpoint.rs:5336-5343) on device f32
+ * arrays: out[i] = round(round(silu(round(gate[i]))) * round(up[i])) with silu(g) = g / (1 + e^-g)
+ * and round = bf16 round-to-nearest-even. form 0 evaluates the silu in place, as the decode
+ * kernels do; form 1 looks it up in the runtime's 65,536-entry table, as the prefill kernels do
+ * (the first such call on a runtime builds the table on the runtime's stream and waits for it).
+ * Non-finite gate, up or output values raise PW_FLAG_SWIGLU_NONFINITE. Asynchronous on stream. */
+int pw_swiglu_staged_device(pw_runtime *rt, const float *gate, const float *up, uint32_t count, float *out,
+                            uint32_t form, void *stream);
 
 /* ---- checkpoint files ------------------------------------------------------------------------ */
 /* One tensor of a safetensors file: dtype string ("F8_E4M3", "F32", "BF16", ...), shape, and a

@@ -179,6 +179,12 @@ __device__ __forceinline__ bf16x8 bf16x8_from_u4(uint4 v) { return __builtin_bit
 
 __device__ __forceinline__ bool finite_f32(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
 
+// silu of a bf16 gate as the bf16-staged SwiGLU rounds it, round(g / (1 + e^-g))
+// (bf16_staged_swiglu, kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343).
+// One definition for every kernel that evaluates it (mode B decode gate/up, the prefill silu
+// table, the elementwise staged SwiGLU), so the in-place and table forms give the same bits.
+__device__ __forceinline__ float silu_bf16_staged(float g) { return round_bf16(g / (1.0f + expf(-g))); }
+
 // Butterfly max over the 64 lanes of a wave.
 __device__ __forceinline__ float wave_max(float v)
 {

@@ -178,6 +178,9 @@ struct PrefillBuffers {
     const uint16_t *silu;  // [65536] bf16-staged silu of every bf16 gate, from launch_silu_table
 };
 void launch_silu_table(uint16_t *table, hipStream_t stream);
+// Elementwise bf16-staged SwiGLU of f32 gate/up [n]; silu_table null: silu evaluated in place.
+void launch_swiglu_staged(const float *gate, const float *up, uint32_t n, const uint16_t *silu_table, float *out,
+                          uint32_t *flags, hipStream_t stream);
 uint32_t prefill_max_tiles(uint32_t rows, uint32_t E);
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,

@@ -810,8 +810,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void moe_b_gateup_kernel(
         for (int i = 0; i < 4; ++i) {
             const float g = round_bf16(tg[nt][i]);
             const float u = round_bf16(tu[nt][i]);
-            const float silu = round_bf16(g / (1.0f + expf(-g)));
-            o[i] = round_bf16(silu * u);
+            o[i] = round_bf16(silu_bf16_staged(g) * u);
             bad |= !finite_f32(g) || !finite_f32(u) || !finite_f32(o[i]);
         }
         *(float4 *)(hidden + (size_t)(et.off + t) * I + row0 + q * 4) = out;

@@ -326,12 +326,9 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
     }
 }
 
-// silu of a bf16 gate as the bf16-staged SwiGLU rounds it, round(g / (1 + e^-g))
-// (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343), for all 65,536 bf16
-// bit patterns: the table entry of bits b is the function's value at the bf16 number b, computed
-// by this expression once, so a lookup gives the same bits as evaluating it in place.
-__device__ __forceinline__ float silu_bf16_staged(float g) { return round_bf16(g / (1.0f + expf(-g))); }
-
+// silu_bf16_staged for all 65,536 bf16 bit patterns: the table entry of bits b is the function's
+// value at the bf16 number b, computed by the shared device function once, so a lookup gives the
+// same bits as evaluating it in place.
 __global__ __launch_bounds__(256) void silu_table_kernel(uint16_t *__restrict__ table)
 {
     const uint32_t b = blockIdx.x * 256 + threadIdx.x;  // grid covers exactly 65,536 entries
@@ -341,6 +338,32 @@ __global__ __launch_bounds__(256) void silu_table_kernel(uint16_t *__restrict__ 
 void launch_silu_table(uint16_t *table, hipStream_t stream)
 {
     hipLaunchKernelGGL(silu_table_kernel, dim3(256), dim3(256), 0, stream, table);
+}
+
+// Elementwise bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU
+// src/text_endpoint.rs:5336-5343) on f32 arrays: out = round(round(silu(round(g))) * round(u)).
+// With a table the silu comes from it (the prefill form), else it is evaluated in place (the
+// decode form). One thread per value.
+__global__ __launch_bounds__(256) void swiglu_staged_kernel(const float *__restrict__ gate, const float *__restrict__ up,
+                                                            uint32_t n, const uint16_t *__restrict__ silu_table,
+                                                            float *__restrict__ out, uint32_t *flags)
+{
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n)
+        return;
+    const float g = round_bf16(gate[i]), u = round_bf16(up[i]);
+    const float silu = silu_table ? f32_from((uint32_t)silu_table[f32_bits(g) >> 16] << 16) : silu_bf16_staged(g);
+    const float h = round_bf16(silu * u);
+    out[i] = h;
+    if (!finite_f32(g) || !finite_f32(u) || !finite_f32(h))
+        raise_flag(flags, FLAG_SWIGLU_NONFINITE);
+}
+
+void launch_swiglu_staged(const float *gate, const float *up, uint32_t n, const uint16_t *silu_table, float *out,
+                          uint32_t *flags, hipStream_t stream)
+{
+    hipLaunchKernelGGL(swiglu_staged_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, gate, up, n, silu_table,
+                       out, flags);
 }
 
 // bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343)

@@ -109,9 +109,40 @@ struct pw_runtime {
         moe_active, moe_pieces, moe_partial, moe_sched, pf_tiles, pf_silu, router_scores, bf16_partial;
     MoeBuffers mb{};
     pw::KernelTimer timer;
+    bool silu_ready = false;  // pf_silu holds the complete silu table
+    // Calls share the scratch above, so each call is ordered after the previous one: the stream
+    // the last call enqueued on, and an event recorded at the end of that call when it was not the
+    // runtime's own stream (the runtime never touches a caller's stream after the call returns).
+    hipStream_t last_stream = nullptr;
+    hipEvent_t order_event = nullptr;
 };
 
 namespace {
+
+// Orders one call's work after the previous call's (they share the runtime's scratch): on entry,
+// a stream other than the previous call's waits for the previous call's work; on exit, work
+// enqueued on a caller's stream is marked with the runtime's event. No cost while every call uses
+// the same stream.
+struct StreamOrder {
+    pw_runtime *rt;
+    hipStream_t s;
+    hipError_t err = hipSuccess;
+    StreamOrder(pw_runtime *r, hipStream_t stream) : rt(r), s(stream)
+    {
+        if (rt->last_stream && rt->last_stream != s) {
+            if (rt->last_stream == rt->stream)
+                err = hipEventRecord(rt->order_event, rt->stream);
+            if (err == hipSuccess)
+                err = hipStreamWaitEvent(s, rt->order_event, 0);
+        }
+    }
+    ~StreamOrder()
+    {
+        if (s != rt->stream)
+            (void)hipEventRecord(rt->order_event, s);
+        rt->last_stream = s;
+    }
+};
 
 // Points the launchers at the runtime's event timer for the duration of one ABI call.
 struct TimerScope {
@@ -328,6 +359,21 @@ int ensure_moe(pw_runtime *rt, uint32_t rows, uint32_t E, uint32_t H, uint32_t I
     return PW_OK;
 }
 
+// The 65,536-entry silu table of the bf16-staged SwiGLU, built once per runtime on the runtime's
+// stream and complete (the host waits for it) before any call reads it; a failed build leaves it
+// marked unbuilt, so the next call builds it again.
+int ensure_silu_table(pw_runtime *rt)
+{
+    if (rt->silu_ready)
+        return PW_OK;
+    PW_HIP(rt->pf_silu.ensure(65536 * sizeof(uint16_t)));
+    pw::launch_silu_table((uint16_t *)rt->pf_silu.p, rt->stream);
+    PW_HIP(hipGetLastError());
+    PW_HIP(hipStreamSynchronize(rt->stream));
+    rt->silu_ready = true;
+    return PW_OK;
+}
+
 // The libc++ nth_element top-k and the noaux route row are shared with the device router
 // (pw_topk.h).
 
@@ -363,6 +409,8 @@ int pw_runtime_create(int device, uint32_t flags, pw_runtime **out)
         // stream) is ordered before the runtime's launches, and vice versa
         e = hipStreamCreateWithFlags(&rt->stream, hipStreamDefault);
     if (e == hipSuccess)
+        e = hipEventCreateWithFlags(&rt->order_event, hipEventDisableTiming);
+    if (e == hipSuccess)
         e = hipMalloc((void **)&rt->d_flags, sizeof(uint32_t));
     if (e == hipSuccess)
         e = hipMemset(rt->d_flags, 0, sizeof(uint32_t));
@@ -384,6 +432,8 @@ void pw_runtime_destroy(pw_runtime *rt)
     if (rt->d_flags)
         (void)hipFree(rt->d_flags);
     free_timer(rt->timer);
+    if (rt->order_event)
+        (void)hipEventDestroy(rt->order_event);
     if (rt->stream)
         (void)hipStreamDestroy(rt->stream);
     delete rt;
@@ -461,6 +511,7 @@ int pw_runtime_take_flags(pw_runtime *rt, uint32_t *flags)
     TimerScope timer_scope(rt);
     // device-resident calls may have run on a caller's stream: wait for all of them
     PW_HIP(hipDeviceSynchronize());
+    rt->last_stream = nullptr;  // nothing of an earlier call is pending
     PW_TRY(read_flags(rt, *flags));
     PW_TRY(reset_flags(rt));
     PW_HIP(hipStreamSynchronize(rt->stream));
@@ -716,6 +767,8 @@ int pw_fp8_linear(pw_runtime *rt, uint32_t mode, const float *input, uint32_t ro
             return fail(PW_ERR_NONFINITE, "wide FP8 linear input is non-finite");
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
+    StreamOrder order(rt, rt->stream);
+    PW_HIP(order.err);
     PW_TRY(reset_flags(rt));
     bool x_f32;
     PW_TRY(stage_input(rt, input, n_in, x_f32));
@@ -753,6 +806,8 @@ int pw_fp8_linear_device(pw_runtime *rt, uint32_t mode, const void *input, uint3
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     float *y32 = output_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr;
     uint16_t *y16 = output_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr;
     const uint32_t round_f32 = output_dtype == PW_DTYPE_F32 && round_output ? 1u : 0u;
@@ -858,6 +913,8 @@ int pw_bf16_linear(pw_runtime *rt, const float *input, uint32_t rows, const pw_p
             return fail(PW_ERR_NONFINITE, "wide BF16 linear layout mismatch (non-finite input)");
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
+    StreamOrder order(rt, rt->stream);
+    PW_HIP(order.err);
     PW_TRY(reset_flags(rt));
     bool x_f32;
     PW_TRY(stage_input(rt, input, n_in, x_f32));
@@ -894,6 +951,8 @@ int pw_bf16_linear_device(pw_runtime *rt, const void *input, uint32_t input_dtyp
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     float *y32 = output_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr;
     uint16_t *y16 = output_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr;
     const uint32_t round_f32 = output_dtype == PW_DTYPE_F32 && round_output ? 1u : 0u;
@@ -914,7 +973,29 @@ int pw_quantize_fp8_group128_device(pw_runtime *rt, const void *x, uint32_t x_dt
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     pw::launch_quant_group128(x, x_dtype == PW_DTYPE_F32, rows, cols, codes, scales, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_swiglu_staged_device(pw_runtime *rt, const float *gate, const float *up, uint32_t count, float *out,
+                            uint32_t form, void *stream)
+{
+    if (!rt || !gate || !up || !out || count == 0)
+        return fail(PW_ERR_ARGUMENT, "null argument or zero count");
+    if (form > 1)
+        return fail(PW_ERR_ARGUMENT, "unknown staged SwiGLU form %u", form);
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    if (form == 1)
+        PW_TRY(ensure_silu_table(rt));
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
+    pw::launch_swiglu_staged(gate, up, count, form == 1 ? (const uint16_t *)rt->pf_silu.p : nullptr, out,
+                             rt->d_flags, s);
     PW_HIP(hipGetLastError());
     return PW_OK;
 }
@@ -988,6 +1069,8 @@ int pw_moe_execute(pw_runtime *rt, uint32_t mode, uint32_t fused_gate_up, const 
                     return fail(PW_ERR_SCHEDULE, "position %u routed twice to one expert binding", p);
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
+    StreamOrder order(rt, rt->stream);
+    PW_HIP(order.err);
     PW_TRY(reset_flags(rt));
     bool x_f32;
     PW_TRY(stage_input(rt, input, n_in, x_f32));
@@ -1136,6 +1219,8 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     PW_TRY(ensure_moe(rt, rows, bank->n_experts, bank->hidden, bank->intermediate));
     pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, bank->n_experts,
                             std::min<uint32_t>(bank->n_experts, rows * 8), rt->mb, rt->d_flags, s);
@@ -1168,6 +1253,8 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     PW_TRY(ensure_moe(rt, rows, E, H, I, false));
     const uint32_t max_tiles = pw::prefill_max_tiles(rows, E);
     PW_HIP(rt->pf_tiles.ensure((size_t)max_tiles * 8 + 16));
@@ -1176,12 +1263,7 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
     pb.n_tiles = (uint32_t *)((char *)rt->pf_tiles.p + (size_t)max_tiles * 8);
     pb.hidden = (uint16_t *)rt->moe_hidden.p;  // [P][I] f32 scratch holds the bf16 hidden
     pb.y = (uint16_t *)rt->moe_y.p;            // [P][H] f32 scratch holds the bf16 outputs
-    if (!rt->pf_silu.p) {  // built once per runtime, and complete before any stream reads it
-        PW_HIP(rt->pf_silu.ensure(65536 * sizeof(uint16_t)));
-        pw::launch_silu_table((uint16_t *)rt->pf_silu.p, rt->stream);
-        PW_HIP(hipGetLastError());
-        PW_HIP(hipStreamSynchronize(rt->stream));
-    }
+    PW_TRY(ensure_silu_table(rt));
     pb.silu = (const uint16_t *)rt->pf_silu.p;
     const uint32_t P = rows * 8;
     pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, std::min<uint32_t>(E, P), rt->mb,
@@ -1207,6 +1289,8 @@ int pw_moe_schedule_device(pw_runtime *rt, const pw_expert_bank *bank, const uin
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     const uint32_t E = bank->n_experts;
     PW_TRY(ensure_sched(rt, rows, E));
     const size_t P = (size_t)rows * 8;
@@ -1239,6 +1323,8 @@ int pw_route_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t ro
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     float *sc = scores;
     if (!sc) {
         PW_HIP(rt->router_scores.ensure((size_t)rows * experts * 4));
@@ -1267,6 +1353,8 @@ int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_
     PW_HIP(set_device(rt));
     TimerScope timer_scope(rt);
     hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
     PW_TRY(ensure_moe(rt, rows, bank->n_experts, bank->hidden, bank->intermediate));
     pw::launch_expert_forward(mode, bank->table, bank->host_table[expert], expert, rt->mb, x, x_dtype == PW_DTYPE_F32,
                               rows,

@@ -6,14 +6,16 @@ C ABI of include/pwfp8.h. Names and argument meanings follow the reference: ``co
 ``WideExpertBinding`` (expert, positions, route_weights, gate, up, down) and the routing helpers
 of src/text_endpoint.rs:4342-4473. Errors raise ``PwError`` (the reference returns Err(String)).
 """
-from ._abi import (DTYPE_BF16, DTYPE_F32, DTYPE_F32_RAW, FLAG_ROUTE, FLAG_SCHEDULE, LAYOUT_FULL_QKV_TP4,
+from ._abi import (DTYPE_BF16, DTYPE_F32, DTYPE_F32_RAW, FLAG_QUANT_NONFINITE, FLAG_ROUND_NONFINITE, FLAG_ROUTE,
+                   FLAG_SCHEDULE, FLAG_SWIGLU_NONFINITE, LAYOUT_FULL_QKV_TP4,
                    LAYOUT_PLAIN, LAYOUT_SWA_QKV_TP4, MODE_A, MODE_B, PwError, lib)
 from .runtime import (ExpertBank, Projection, Safetensors, WideExpertBinding, WideLinearExecution,
                       WideMoeExecution, WideMoeRuntime, full_qkv_scale_row, full_qkv_source_row,
                       noaux_routes, route_from_logits, swa_qkv_source_row, topk_unsorted)
 
 __all__ = [
-    "DTYPE_BF16", "DTYPE_F32", "DTYPE_F32_RAW", "FLAG_ROUTE", "FLAG_SCHEDULE", "LAYOUT_FULL_QKV_TP4",
+    "DTYPE_BF16", "DTYPE_F32", "DTYPE_F32_RAW", "FLAG_QUANT_NONFINITE", "FLAG_ROUND_NONFINITE", "FLAG_ROUTE",
+    "FLAG_SCHEDULE", "FLAG_SWIGLU_NONFINITE", "LAYOUT_FULL_QKV_TP4",
     "LAYOUT_PLAIN", "LAYOUT_SWA_QKV_TP4",
     "MODE_A", "MODE_B", "PwError", "lib", "ExpertBank", "Projection", "Safetensors", "WideExpertBinding",
     "WideLinearExecution", "WideMoeExecution", "WideMoeRuntime", "full_qkv_scale_row",

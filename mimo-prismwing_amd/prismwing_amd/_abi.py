@@ -20,6 +20,9 @@ DTYPE_F32, DTYPE_BF16, DTYPE_F32_RAW = 0, 1, 2
 LAYOUT_PLAIN, LAYOUT_FULL_QKV_TP4, LAYOUT_SWA_QKV_TP4 = 0, 1, 2
 RUNTIME_FUSED_GATE_UP = 1
 # GPU error bits (include/pwfp8.h PW_FLAG_*)
+FLAG_QUANT_NONFINITE = 2
+FLAG_SWIGLU_NONFINITE = 4
+FLAG_ROUND_NONFINITE = 32
 FLAG_SCHEDULE = 256
 FLAG_ROUTE = 1024
 
@@ -86,6 +89,7 @@ SIGNATURES = {
     "pw_fp8_linear": (_i, [_vp, _u32, _f32p, _u32, _vp, _f32p, ctypes.POINTER(LinearStats)]),
     "pw_fp8_linear_device": (_i, [_vp, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _u32, _vp]),
     "pw_quantize_fp8_group128_device": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "pw_swiglu_staged_device": (_i, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
     "pw_safetensors_open": (_i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "pw_safetensors_close": (None, [_vp]),
     "pw_safetensors_count": (_u32, [_vp]),

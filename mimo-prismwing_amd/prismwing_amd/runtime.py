@@ -335,6 +335,12 @@ class WideMoeRuntime:
         check(lib().pw_quantize_fp8_group128_device(self.handle, _ptr(x), x_dtype, rows, cols, _ptr(codes),
                                                     _ptr(scales), stream or 0))
 
+    def swiglu_staged_device(self, gate, up, count: int, out, form: int = 0, stream: Optional[int] = None):
+        """bf16_staged_swiglu on device f32 arrays; form 0 evaluates the silu in place (the decode
+        kernels' form), form 1 looks it up in the runtime's table (the prefill kernels' form)."""
+        check(lib().pw_swiglu_staged_device(self.handle, _ptr(gate), _ptr(up), count, _ptr(out), form,
+                                            stream or 0))
+
     def moe_layer_device(self, bank: ExpertBank, x, rows: int, route_ids, route_weights, out,
                          mode: int = MODE_A, x_dtype: int = DTYPE_BF16, out_dtype: int = DTYPE_BF16,
                          stream: Optional[int] = None):

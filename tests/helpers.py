@@ -114,3 +114,139 @@ def write_safetensors(path, tensors, metadata=None, header_pad=True, raw_header=
     with open(path, "wb") as f:
         f.write(struct.pack("<Q", len(hb)) + hb + payload)
     return path
+
+
+# ------------------------------------------------------------------ closed-form mode-B layers
+def _unit_codes(rng, shape, p_zero):
+    """e4m3 codes of magnitude in [1, 2) (0x38..0x3f) with random signs; zero with probability p_zero."""
+    c = (0x38 + rng.integers(0, 8, shape)).astype(np.uint8)
+    c |= np.where(rng.random(shape) < 0.5, 0x80, 0).astype(np.uint8)
+    c[rng.random(shape) < p_zero] = 0
+    return c
+
+
+def _lowbits(t: np.ndarray) -> np.ndarray:
+    """The lowest set bit (a power of two) of each dyadic value of t, exact in f64; 0 where t == 0."""
+    t = np.abs(np.asarray(t, np.float64))
+    m, e = np.frexp(t)
+    mant = (m * 2.0 ** 53).astype(np.int64)
+    return np.where(t == 0, 0.0, np.ldexp((mant & -mant).astype(np.float64), e - 53))
+
+
+def exact_in_f32(x: np.ndarray, w: np.ndarray) -> bool:
+    """Every partial sum of every x[p] . w[o] (f64 dyadic values), in any order, is exact in f32:
+    all products are multiples of q = (lowest bit of x) (lowest bit of w) and sum |x w| < 2^24 q."""
+    lx, lw = _lowbits(x[x != 0]), _lowbits(w[w != 0])
+    if lx.size == 0 or lw.size == 0:
+        return True
+    return bool((np.abs(x) @ np.abs(w).T).max() < 2.0 ** 24 * lx.min() * lw.min())
+
+
+def fp8_blocks_exact(q: np.ndarray, w: np.ndarray) -> bool:
+    """The FP8 MFMA adds the 128 products of a block exactly only when every product keeps its bits
+    within 14 bits of the block's largest product (it truncates bits below 2^(e - 13), e the
+    exponent of the largest product: measured 448 + 2^-9 -> 448, 64 + 7 * 2^-9 -> 64 + 2^-7).
+    q [rows, K] and w [n, K] hold e4m3 values (without block scales): True when every block of every
+    (row, output) sum is inside that window (a product's lowest bit is the product of its operands')."""
+    lq, lw = _lowbits(q), _lowbits(w)
+    for b in range(q.shape[1] // 128):
+        blk = slice(128 * b, 128 * b + 128)
+        mx = (np.abs(q[:, None, blk]) * np.abs(w[None, :, blk])).max(axis=-1)
+        lp = lq[:, None, blk] * lw[None, :, blk]
+        low = np.where(lp > 0, lp, np.inf).min(axis=-1)
+        live = mx > 0
+        window = np.ldexp(1.0, np.floor(np.log2(np.where(live, mx, 1.0))).astype(np.int64) - 13)
+        if np.any(live & (low < window)):
+            return False
+    return True
+
+
+def closed_form_mode_b(seed, rows, n_experts, hidden=256, inter=256, top_k=8, check=False):
+    """A routed layer whose mode-B result is fixed bit for bit, whatever the summation order.
+
+    Every activation group holds +-448 (so its dynamic scale is exactly 1 and the codes are the
+    values), weights are e4m3 codes in [1, 2) times power-of-two block scales, and the columns that
+    hold the +-448 entries carry no weight, so every gate/up sum is exact in f32. Hidden row 128 j of
+    every expert has gate 32 and up 14 (silu(32) rounds to 32 in f32), so h = 448 there and every
+    hidden group's scale is exactly 1 too; the down weights skip those rows and hold one code per
+    128-column block (hidden codes span e4m3's range, and one product per block keeps the FP8
+    MFMA's block sums exact, see fp8_blocks_exact). Gate rows whose silu
+    lies within 16 f32 steps of a bf16 rounding boundary are zeroed (an exp evaluated one step
+    differently could round them the other way). Returns experts {id: (gw, gs, uw, us, dw, ds)},
+    x [rows, hidden] f32, selected [rows, top_k], weights [rows, top_k]. With check, asserts that
+    every projection sum of the routed placements is exact in f32 and inside the FP8 MFMA's window
+    (a CPU test runs the checks for the seeds and sizes the GPU tests use)."""
+    rng = np.random.default_rng(seed)
+    experts = {}
+    for e in range(n_experts):
+        gw, uw = _unit_codes(rng, (inter, hidden), 0.3), _unit_codes(rng, (inter, hidden), 0.3)
+        dw = np.zeros((hidden, inter), np.uint8)
+        for b in range(inter // 128):
+            c = 128 * b + rng.integers(1, 128, hidden)
+            dw[np.arange(hidden), c] = _unit_codes(rng, hidden, 0.0)
+        for w in (gw, uw):
+            w[:, 0] = 0
+            w[:, 1::128] = 0
+        gs = (2.0 ** rng.integers(-5, -3, (inter // 128, hidden // 128))).astype(np.float32)
+        us = (2.0 ** rng.integers(-5, -3, (inter // 128, hidden // 128))).astype(np.float32)
+        ds = (2.0 ** rng.integers(-5, -3, (hidden // 128, inter // 128))).astype(np.float32)
+        for j in range(inter // 128):
+            r = 128 * j
+            gw[r, :] = 0
+            uw[r, :] = 0
+            # x[:, 0] = 32: code * scale * 32 = 32 (gate) and 14 (up)
+            gw[r, 0] = 0x58 if gs[j, 0] == 2.0 ** -4 else 0x60   # 16 or 32
+            uw[r, 0] = 0x4E if us[j, 0] == 2.0 ** -4 else 0x56   # 7 or 14
+            dw[:, r] = 0
+        experts[e] = (gw, gs, uw, us, dw, ds)
+    x = decode_table()[_unit_codes(rng, (rows, hidden), 0.2)].astype(np.float32)
+    x[:, 0] = 32.0
+    x[:, 1::128] = 448.0 * np.where(rng.random((rows, hidden // 128)) < 0.5, -1.0, 1.0)
+    sel = np.stack([rng.permutation(n_experts)[:top_k] for _ in range(rows)]).astype(np.uint32)
+    w = rng.uniform(0.05, 1.0, (rows, top_k)).astype(np.float32)
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    for e in sorted(set(sel.reshape(-1).tolist())):
+        gw, gs, uw, us, dw, ds = experts[e]
+        xs = x[[p for p in range(rows) if e in sel[p].tolist()]].astype(np.float64)
+        if check:
+            for wm, sm in ((gw, gs), (uw, us)):
+                assert exact_in_f32(xs, dequant(wm, sm))
+                assert fp8_blocks_exact(xs, decode_table()[wm])
+        g = bf16_round((xs @ dequant(gw, gs).T).astype(np.float32)).astype(np.float64)
+        silu = (g / (1.0 + np.exp(-g))).astype(np.float32)
+        low = (silu.view(np.uint32) & 0xFFFF).astype(np.int64)
+        near = np.any(np.abs(low - 0x8000) <= 16, axis=0)
+        near[::128] = False
+        gw[near, :] = 0
+        g = bf16_round((xs @ dequant(gw, gs).T).astype(np.float32)).astype(np.float64)
+        u = bf16_round((xs @ dequant(uw, us).T).astype(np.float32)).astype(np.float32)
+        h = bf16_round(bf16_round((g / (1.0 + np.exp(-g))).astype(np.float32)) * u).astype(np.float64)
+        if check:
+            assert np.all(np.abs(h[:, ::128]) == 448.0) and np.all(np.abs(h) <= 448.0)
+            hd = decode_table()[encode_e4m3(h)]
+            assert exact_in_f32(hd, dequant(dw, ds))
+            assert fp8_blocks_exact(hd, decode_table()[dw])
+    return experts, x, sel, w
+
+
+def moe_condition(x, experts, sel, w):
+    """Scale of the f32 summation-order error of a mode-A routed layer, per output [rows, hidden]:
+    sum over the token's slots of |w| (|Wd| @ (|h| + |silu'(g) u| |Wg| |x| + |silu(g)| |Wu| |x|)),
+    the sum of the magnitudes of every term whose rounding reaches the output (f64)."""
+    x = np.asarray(x, np.float64)
+    out = np.zeros(x.shape)
+    for e in sorted(set(np.asarray(sel).reshape(-1).tolist())):
+        gw, gs, uw, us, dw, ds = experts[e]
+        rows_e = [p for p in range(x.shape[0]) if e in np.asarray(sel)[p].tolist()]
+        xs = x[rows_e]
+        wg, wu, wd = dequant(gw, gs), dequant(uw, us), dequant(dw, ds)
+        g, u = xs @ wg.T, xs @ wu.T
+        sig = 1.0 / (1.0 + np.exp(-g))
+        silu = g * sig
+        dsilu = sig * (1.0 + g * (1.0 - sig))
+        ag, au = np.abs(xs) @ np.abs(wg).T, np.abs(xs) @ np.abs(wu).T
+        inner = np.abs(silu * u) + np.abs(dsilu * u) * ag + np.abs(silu) * au
+        cond = inner @ np.abs(wd).T
+        for l, p in enumerate(rows_e):
+            out[p] += abs(float(np.asarray(w)[p, np.asarray(sel)[p].tolist().index(e)])) * cond[l]
+    return out

@@ -14,7 +14,7 @@ import pytest
 
 import oracle as O
 import prismwing_amd as P
-from helpers import (bf16_normal, bf16_round, condition, decode_table, dequant, fp8_weight,
+from helpers import (bf16_normal, bf16_round, condition, decode_table, dequant, encode_e4m3, fp8_weight,
                      from_bf16_bits, log_uniform_scales, normwise, rel_l2, to_bf16_bits,
                      within_bf16_cond)
 
@@ -288,6 +288,35 @@ def test_tp4_qkv_layouts(rt, layout):
     wd = dec * np.repeat(s[srow], 128, axis=1)
     ref = x.astype(np.float64) @ wd.T.astype(np.float64)
     assert normwise(got, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("layout", [P.LAYOUT_FULL_QKV_TP4, P.LAYOUT_SWA_QKV_TP4])
+@pytest.mark.parametrize("rows", [1, 8])
+def test_tp4_qkv_mode_b_as_the_reference_calls_it(rt, layout, rows):
+    """The reference's attention projection: execute_fp8_linear(.., full_qkv_layout = true) in
+    mode B on the TP4 layout (full_qkv_fp8_gemm8_sglang_blockscaled; the SWA form is picked by its
+    14848 x 4096 shape, src/wide_metal_moe.rs:241-350). CPU authority: decode_full_qkv_weight
+    (src/text_endpoint.rs:3260-3314) and fp8_linear (:3053-3108), i.e. the dynamically quantised
+    input times the deinterleaved dequantised weight, rounded to bf16. Outputs within one bf16
+    rounding step plus 1e-5 of the sum of |terms| (f32 order and the FP8 MFMA's block sums)."""
+    rng = np.random.default_rng(70 + layout + rows)
+    n, srows = (13568, 108) if layout == P.LAYOUT_FULL_QKV_TP4 else (14848, 116)
+    s = (2.0 ** rng.uniform(-10, -6, size=(srows, 32))).astype(np.float32)
+    w = encode_e4m3(rng.standard_normal((n, 4096)) / np.repeat(np.repeat(s.astype(np.float64), 128, 0), 128, 1)[:n])
+    x = bf16_normal(rng, (rows, 4096))
+    proj = rt.bind_projection(w, s, layout=layout)
+    got = rt.execute_fp8_linear(x, proj, full_qkv_layout=layout == P.LAYOUT_FULL_QKV_TP4, mode=P.MODE_B).output
+    src = np.array([(O.full_qkv_source_row if layout == P.LAYOUT_FULL_QKV_TP4 else O.swa_qkv_source_row)(r)
+                    for r in range(n)])
+    srow = (np.array([O.full_qkv_scale_row(r) for r in range(n)]) if layout == P.LAYOUT_FULL_QKV_TP4
+            else src // 128)
+    wd = decode_table()[w[src]] * np.repeat(s[srow].astype(np.float64), 128, axis=1)
+    _, _, xd = O.dynamic_fp8(x)
+    exact = xd.astype(np.float64) @ wd.T
+    ref = bf16_round(exact.astype(np.float32))
+    assert got.shape == (rows, n)
+    assert normwise(got, exact) <= 2e-2
+    assert within_bf16_cond(got, ref, np.abs(xd.astype(np.float64)) @ np.abs(wd).T)
 
 
 def test_fail_closed_validation(rt):

@@ -2,9 +2,13 @@
 C oracle, through the C ABI: the reference's execute/execute_fused_gate_up host surface and the
 device-resident layer on a full 256-expert bank.
 
-Tolerances: mode A <= 1e-3 max|d|/max|ref| on the f32 combine before the final bf16 round and
-<= 8e-3 on bf16 outputs (one rounding step of the largest element); mode B <= 2e-2. Routes, placement
-counts and the schedule are integer work and bit-exact.
+Tolerances: mode A products are exact (e4m3 weights times bf16 activation planes), so the f32
+combine before the final bf16 round may differ from the oracle only by summation order: each
+element within 1e-8 of its condition scale C (the sum of the magnitudes of every term whose
+rounding reaches it, `helpers.moe_condition`; observed at most 1.6e-9 C on MI355X), and bf16
+outputs within one rounding step of that. Mode B <= 2e-2 max|d|/max|ref| (block sums come from the
+FP8 MFMA, which truncates products 14 bits below a block's largest). Routes, placement counts and
+the schedule are integer work and bit-exact.
 """
 import numpy as np
 import pytest
@@ -12,14 +16,23 @@ import pytest
 import oracle as O
 import prismwing_amd as P
 from prismwing_amd import workloads as WL
-from helpers import bf16_normal, fp8_weight, log_uniform_scales, normwise, rel_l2
-
-# bf16 outputs: the f32 result may sit on the other side of a bf16 rounding boundary, so the
-# largest element may move by one step (<= 2^-7 of its magnitude); the f32 result itself is
-# held to the 1e-3 bound through the F32_RAW outputs.
-BF16_OUT = 8e-3
+from helpers import (bf16_normal, fp8_weight, log_uniform_scales, moe_condition, normwise, rel_l2,
+                     within_bf16_cond)
 
 pytestmark = pytest.mark.gpu
+
+# mode A: |got - oracle| <= COND_REL * C per element on the f32 combine; bf16 outputs may also sit
+# on the other side of one bf16 rounding boundary
+COND_REL = 1e-8
+
+
+def check_mode_a(got, ref, cond, raw):
+    """got/ref f32 combines (raw) or bf16-valued outputs against the oracle's, element-wise."""
+    if raw:
+        d = np.abs(got.astype(np.float64) - ref)
+        assert np.all(d <= COND_REL * cond), float((d / np.maximum(cond, 1e-30)).max())
+    else:
+        assert within_bf16_cond(got, ref, cond, rel=COND_REL)
 
 
 def make_experts(rng, n, hidden, inter):
@@ -74,19 +87,40 @@ def test_execute_matches_oracle(rt, small_layer, rows, mode):
     ref = O.moe_layer("a" if mode == P.MODE_A else "b", x, experts, n, sel, w)
     assert res.unique_experts == len(set(sel.reshape(-1).tolist()))
     assert res.expert_rows == rows * 8
-    assert normwise(res.output, ref) <= (BF16_OUT if mode == P.MODE_A else 2e-2)
+    if mode == P.MODE_A:
+        check_mode_a(res.output, ref, moe_condition(x, experts, sel, w), raw=False)
+    else:
+        assert normwise(res.output, ref) <= 2e-2
 
 
-def test_fused_and_unfused_are_byte_identical(rt, small_layer):
-    experts, projs, hidden, inter, n = small_layer
-    rng = np.random.default_rng(3)
-    x = bf16_normal(rng, (6, hidden))
-    sel, w = random_routes(rng, 6, n)
-    b = bindings_from_routes(projs, sel, w)
-    for mode in (P.MODE_A, P.MODE_B):
-        a = rt.execute(x, b, mode=mode).output
-        f = rt.execute_fused_gate_up(x, b, mode=mode).output
-        assert np.array_equal(a.view(np.uint32), f.view(np.uint32))
+@pytest.fixture(scope="module")
+def wide_layer(rt):
+    rng = np.random.default_rng(64)
+    hidden, inter, n = 256, 128, 64
+    experts = make_experts(rng, n, hidden, inter)
+    projs = {e: (rt.bind_projection(v[0], v[1]), rt.bind_projection(v[2], v[3]), rt.bind_projection(v[4], v[5]))
+             for e, v in experts.items()}
+    return experts, projs, hidden, inter, n
+
+
+@pytest.mark.parametrize("rows", [64, 128])
+@pytest.mark.parametrize("mode", [P.MODE_A, P.MODE_B])
+def test_execute_layer_major_slices(rt, wide_layer, rows, mode):
+    """The reference's layer-major prefill drives execute with 128-row slices (LAYER_MAJOR_ROWS,
+    src/wide_metal_moe.rs:11, checked at :858): 64 and 128 rows over 64 experts, each expert at
+    most 32 placements."""
+    experts, projs, hidden, inter, n = wide_layer
+    rng = np.random.default_rng(rows + mode)
+    x = bf16_normal(rng, (rows, hidden))
+    sel, w = random_routes(rng, rows, n)
+    assert np.bincount(sel.reshape(-1), minlength=n).max() <= 32
+    res = rt.execute(x, bindings_from_routes(projs, sel, w), mode=mode)
+    ref = O.moe_layer("a" if mode == P.MODE_A else "b", x, experts, n, sel, w)
+    assert res.expert_rows == rows * 8
+    if mode == P.MODE_A:
+        check_mode_a(res.output, ref, moe_condition(x, experts, sel, w), raw=False)
+    else:
+        assert normwise(res.output, ref) <= 2e-2 and rel_l2(res.output, ref) <= 5e-3
 
 
 def test_thirty_two_rows_per_expert(rt, small_layer):
@@ -100,7 +134,10 @@ def test_thirty_two_rows_per_expert(rt, small_layer):
     for mode in (P.MODE_A, P.MODE_B):
         res = rt.execute(x, bindings_from_routes(projs, sel, w), mode=mode)
         ref = O.moe_layer("a" if mode == P.MODE_A else "b", x, experts, n, sel, w)
-        assert normwise(res.output, ref) <= (BF16_OUT if mode == P.MODE_A else 2e-2)
+        if mode == P.MODE_A:
+            check_mode_a(res.output, ref, moe_condition(x, experts, sel, w), raw=False)
+        else:
+            assert normwise(res.output, ref) <= 2e-2
 
 
 def test_slot_order_does_not_change_output(rt, small_layer):
@@ -153,12 +190,14 @@ def test_complete_expert_widths(rt):
         assert rt.take_flags() == 0
         raw = out.cpu().numpy()
         ref32, ref16 = O.expert_mode_a(x, host)
-        assert normwise(raw, ref32) <= 1e-3 and rel_l2(raw, ref32) <= 1e-5
+        one = np.zeros((width, 1), np.uint32)
+        cond = moe_condition(x, {0: host}, one, np.ones((width, 1), np.float32))
+        check_mode_a(raw, ref32, cond, raw=True)
         out16 = torch.empty((width, 4096), dtype=torch.float32, device="cuda")
         rt.expert_forward_device(bank.bank, 0, xt, width, out16, mode=P.MODE_A, out_dtype=P.DTYPE_F32,
                                  stream=torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
-        assert normwise(out16.cpu().numpy(), ref16) <= BF16_OUT
+        check_mode_a(out16.cpu().numpy(), ref16, cond, raw=False)
 
 
 @pytest.fixture(scope="module")
@@ -189,10 +228,11 @@ def test_decode_layer_256_experts_width8(rt, full_bank, zipf):
         ref, ref_raw = O.moe_layer("a" if mode == P.MODE_A else "b", x, experts, 256, sel, w, raw=True)
         got16 = (out.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
         if mode == P.MODE_A:
-            assert normwise(raw.cpu().numpy(), ref_raw) <= 1e-3
-            assert normwise(got16, ref) <= BF16_OUT
+            cond = moe_condition(x, experts, sel, w)
+            check_mode_a(raw.cpu().numpy(), ref_raw, cond, raw=True)
+            check_mode_a(got16, ref, cond, raw=False)
         else:
-            assert normwise(got16, ref) <= 2e-2
+            assert normwise(got16, ref) <= 2e-2 and rel_l2(got16, ref) <= 5e-3
 
 
 def test_whole_k_gateup_matches_split_k(rt, full_bank):
@@ -220,7 +260,7 @@ def test_whole_k_gateup_matches_split_k(rt, full_bank):
     used = sorted(set(sel.reshape(-1).tolist()))
     experts = {e: full_bank.expert_host(e) for e in used}
     _, ref_raw = O.moe_layer("a", x, experts, 256, sel, w, raw=True)
-    assert normwise(outs[1], ref_raw) <= 1e-3
+    check_mode_a(outs[1], ref_raw, moe_condition(x, experts, sel, w), raw=True)
 
 
 @pytest.mark.parametrize("width", [5, 6, 8])
@@ -248,7 +288,7 @@ def test_pieces_match_one_workgroup_schedule(rt, full_bank, width):
     assert np.array_equal(outs[0].view(np.uint32), outs[1][:width].view(np.uint32))
     experts = {e: full_bank.expert_host(e) for e in sorted(set(sel.reshape(-1).tolist()))}
     _, ref_raw = O.moe_layer("a", x[:width], experts, 256, sel[:width], w[:width], raw=True)
-    assert normwise(outs[0], ref_raw) <= 1e-3
+    check_mode_a(outs[0], ref_raw, moe_condition(x[:width], experts, sel[:width], w[:width]), raw=True)
 
 
 def test_one_token_equals_two_copies(rt, full_bank):
@@ -285,7 +325,7 @@ def test_one_token_equals_two_copies(rt, full_bank):
                             torch.from_numpy(w).cuda(), raw, mode=P.MODE_A, out_dtype=P.DTYPE_F32_RAW, stream=stream)
         torch.cuda.synchronize()
         assert rt.take_flags() == 0
-        assert normwise(raw.cpu().numpy(), ref_raw) <= 1e-3
+        check_mode_a(raw.cpu().numpy(), ref_raw, moe_condition(x, experts, sel, w), raw=True)
 
 
 def test_device_layer_rejects_misaligned_activations(rt, full_bank):
@@ -334,3 +374,38 @@ def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
     again, flags = run(sel, w)
     assert flags == 0
     assert np.array_equal(clean.view(np.uint32), again.view(np.uint32))
+
+
+def test_calls_on_two_streams_are_ordered(rt, full_bank):
+    """Calls share the runtime's scratch: layers enqueued alternately on two streams with no host
+    wait between them still give their one-stream results, bit for bit (each call's stream waits
+    for the previous call's work)."""
+    import torch
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    batches = []
+    for seed in (140, 141):
+        x = WL.activations(8, WL.SEED_BASE + seed)
+        _, _, sel, w, _ = O.route(x, rw, bias)
+        batches.append((torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda(),
+                        torch.from_numpy(sel.astype(np.int32)).cuda(), torch.from_numpy(w).cuda()))
+
+    def run(b, out, stream):
+        rt.moe_layer_device(full_bank.bank, b[0], 8, b[1], b[2], out, mode=P.MODE_A, out_dtype=P.DTYPE_F32_RAW,
+                            stream=stream)
+
+    ref = []
+    for b in batches:
+        out = torch.empty((8, 4096), dtype=torch.float32, device="cuda")
+        run(b, out, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        ref.append(out.cpu().numpy())
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.empty((8, 4096), dtype=torch.float32, device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
+    for _ in range(3):
+        run(batches[0], outs[0], s1.cuda_stream)
+        run(batches[1], outs[1], s2.cuda_stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    for o, r in zip(outs, ref):
+        assert np.array_equal(o.cpu().numpy().view(np.uint32), r.view(np.uint32))

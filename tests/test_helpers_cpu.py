@@ -2,7 +2,7 @@
 import numpy as np
 
 import oracle as O
-from helpers import decode_table, encode_e4m3
+from helpers import closed_form_mode_b, decode_table, encode_e4m3, exact_in_f32, fp8_blocks_exact
 
 
 def test_helper_encoder_matches_oracle():
@@ -15,3 +15,37 @@ def test_helper_encoder_matches_oracle():
     assert np.array_equal(encode_e4m3(np.array([1000.0, -1e9])), np.array([0x7E, 0xFE], np.uint8))
     t = decode_table()
     assert t[0x38] == 1.0 and t[0xB8] == -1.0 and np.isnan(t[0x7F])
+
+
+def test_fp8_window_rule_matches_the_measured_mfma_sums():
+    """The window rule reproduces what the FP8 MFMA gave on MI355X for one 128-product block:
+    448 + 2^-3 exact, 448 + 2^-6 and 448 + 2^-9 truncated to 448, 64 + 7 * 2^-9 to 64 + 2^-7,
+    1 + 2^-9 exact, 1 + 2^-18 truncated to 1; zero products do not widen the window."""
+    q = np.zeros((1, 128))
+    q[0, :6] = [448.0, 1.0, 2.0 ** -9, 2.0 ** -6, 2.0 ** -3, 64.0]
+    q[0, 6] = 7 * 2.0 ** -9
+
+    def exact(cols):
+        w = np.zeros((1, 128))
+        for c, v in cols.items():
+            w[0, c] = v
+        return fp8_blocks_exact(q, w)
+
+    assert exact({0: 1.0, 4: 1.0}) and exact({1: 1.0, 2: 1.0}) and exact({1: 1.0, 3: 1.0})
+    assert not exact({0: 1.0, 3: 1.0}) and not exact({0: 1.0, 2: 1.0}) and not exact({5: 1.0, 6: 1.0})
+    assert not exact({1: 1.0, 2: 2.0 ** -9})
+    assert exact({0: 0.0, 1: 1.0, 2: 1.0})
+
+
+def test_exact_in_f32_bound():
+    assert exact_in_f32(np.array([[2.0 ** 23, 1.0]]), np.array([[1.0, 1.0]]))
+    assert not exact_in_f32(np.array([[2.0 ** 24, 1.0]]), np.array([[1.0, 1.0]]))
+
+
+def test_closed_form_layer_data_meets_its_preconditions():
+    """The closed-form mode-B data the GPU tests use (seed and size as there): every gate, up and
+    down sum is exact in f32 in any order and inside the FP8 MFMA window, hidden groups have
+    absmax 448, and the oracle's layer runs on it."""
+    experts, x, sel, w = closed_form_mode_b(0x50570100, 192, 12, check=True)
+    out = O.moe_layer("b", x[:8], experts, 12, sel[:8], w[:8])
+    assert np.all(np.isfinite(out)) and np.any(out)
