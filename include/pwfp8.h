@@ -287,6 +287,20 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
                         uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
                         const float *route_weights, void *output, uint32_t out_dtype, void *stream);
 
+/* No counterpart in the reference: pw_moe_layer_device for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as pw_moe_layer_device, for decode batches of 1..8 rows over
+ * banks of at most 256 experts, hidden <= 4096 and intermediate <= 2048 (larger requests fail with
+ * PW_ERR_ARGUMENT). Its scratch (schedule tables, activation planes, split-K partials, expert
+ * outputs; 12 MiB) is a static device array that each GPU holds until the process ends, looked up
+ * once per device by pw_runtime_create; the call allocates nothing. Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU race: calls through one runtime are ordered
+ * like its other calls, but two runtimes (or threads) on one device must not run it concurrently.
+ * Asynchronous on stream. */
+int pw_moe_layer_device_noalloc(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
+                                uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
+                                const float *route_weights, void *output, uint32_t out_dtype, void *stream);
+
 /* Routed-MoE prefill over many token rows (rows 1..4096, e.g. 2048 tokens -> 16 384 placements)
  * with inputs in device memory, in mode B: the reference's layer-major prefill runs 128-row
  * slices through WideMetalMoeRuntime::execute (run_layer_major_moe_slice_mode,

@@ -13,6 +13,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -379,6 +380,84 @@ int ensure_silu_table(pw_runtime *rt)
 
 }  // namespace
 
+// ---- scratch of the entry point that allocates nothing (pw_moe_layer_device_noalloc) ---------
+// A decode batch (rows <= 8) over a bank of at most 256 experts, hidden <= 4096 and intermediate
+// <= 2048 needs about 10.8 MB of schedule tables, activation planes, split-K partials and expert
+// outputs; the array holds 12 MiB. Each GPU the library runs on holds its own copy until the process
+// ends. Every call on a GPU shares that GPU's copy (its contents stay from the last call; every
+// table the kernels read is written by the same call's schedule first, so nothing needs clearing),
+// and calls that overlap on one GPU race.
+namespace {
+constexpr uint32_t NOALLOC_MAX_ROWS = 8, NOALLOC_MAX_EXPERTS = 256, NOALLOC_MAX_HIDDEN = 4096,
+                   NOALLOC_MAX_INTER = 2048;
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)12 << 20;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+void *g_scratch_ptr[NOALLOC_MAX_DEVICES];  // device address of `scratch` on each device
+std::mutex g_scratch_mutex;
+
+// With `device` current: look up this device's address of the scratch array once.
+int noalloc_scratch_init(int device)
+{
+    if (device < 0 || device >= NOALLOC_MAX_DEVICES)
+        return PW_OK;  // the no-alloc entry point refuses such a device
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[device])
+        return PW_OK;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+        return fail(PW_ERR_DEVICE, "scratch array address on device %d: %s", device, hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+    return PW_OK;
+}
+
+// The routed-MoE buffers of `rows` token rows over E experts carved out of one block at `base`, with
+// the sizes ensure_moe allocates (mode A split buffers included); returns the bytes used. base may
+// be null to size the block.
+size_t carve_moe(char *base, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, MoeBuffers &mb)
+{
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> char * {
+        char *p = base ? base + off : nullptr;
+        off += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    const size_t P = (size_t)rows * 8;
+    const uint32_t cnt = std::min<uint32_t>(rows, 32);
+    const size_t ks_gu = std::max(pw::plan_split(H, 2, 1, cnt).ks, pw::plan_split(H, 2, 3, cnt).ks);
+    const size_t ks_d = pw::plan_split(I, 1, 3, cnt).ks;
+    mb = MoeBuffers{};
+    mb.plan = (pw::MoePlan *)take(sizeof(pw::MoePlan));
+    mb.active_expert = (uint32_t *)take((E + 1) * 4);
+    mb.active_offset = (uint32_t *)take((E + 1) * 4);
+    mb.placement_pos = (uint32_t *)take(P * 4);
+    mb.placement_w = (float *)take(P * 4);
+    mb.row_slots = (uint32_t *)take(P * 4);
+    mb.active = (pw::ActiveExpert *)take((size_t)(E + 1) * sizeof(pw::ActiveExpert));
+    mb.pieces = (pw::ActiveExpert *)take((P + 1) * sizeof(pw::ActiveExpert));
+    mb.hidden = (float *)take(P * I * 4);
+    mb.hidden_planes = (uint16_t *)take(3 * P * I * 2);
+    mb.x_planes = (uint16_t *)take(3 * (size_t)rows * H * 2);
+    mb.y = (float *)take(P * H * 4);
+    mb.xq = (uint8_t *)take((size_t)rows * H);
+    mb.xs = (float *)take((size_t)rows * (H / 128) * 4);
+    mb.hq = (uint8_t *)take(P * I);
+    mb.hs = (float *)take(P * (I / 128) * 4);
+    mb.partial = (float *)take(std::max(ks_gu * 2 * P * I, ks_d * P * H) * 4);
+    mb.sched = nullptr;  // decode batches are scheduled by one wave, without these tables
+    mb.max_rows = rows;
+    mb.experts = E;
+    return off;
+}
+
+}  // namespace
+
 // ===================================================================================== C ABI
 extern "C" {
 
@@ -417,6 +496,11 @@ int pw_runtime_create(int device, uint32_t flags, pw_runtime **out)
     if (e != hipSuccess) {
         pw_runtime_destroy(rt);
         return fail(PW_ERR_DEVICE, "runtime setup failed: %s", hipGetErrorString(e));
+    }
+    const int st = noalloc_scratch_init(device);
+    if (st != PW_OK) {
+        pw_runtime_destroy(rt);
+        return st;
     }
     *out = rt;
     return PW_OK;
@@ -1229,6 +1313,49 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
                          bank->intermediate, out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
                          out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
                          out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_moe_layer_device_noalloc(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
+                                uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
+                                const float *route_weights, void *output, uint32_t out_dtype, void *stream)
+{
+    if (!rt || !bank || !x || !route_ids || !route_weights || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if ((uintptr_t)x & 15)
+        return fail(PW_ERR_ARGUMENT, "activations must be 16-byte aligned");
+    if (mode > PW_MODE_B || x_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
+        return fail(PW_ERR_ARGUMENT, "unknown mode or dtype");
+    if (((uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
+        return fail(PW_ERR_ARGUMENT, "route buffers must be 16-byte aligned");
+    const uint32_t E = bank->n_experts, H = bank->hidden, I = bank->intermediate;
+    if (rows < 1 || rows > NOALLOC_MAX_ROWS)
+        return fail(PW_ERR_ARGUMENT, "the no-alloc MoE layer takes 1 to %u token rows (got %u)", NOALLOC_MAX_ROWS,
+                    rows);
+    if (E > NOALLOC_MAX_EXPERTS || H > NOALLOC_MAX_HIDDEN || I > NOALLOC_MAX_INTER)
+        return fail(PW_ERR_ARGUMENT,
+                    "the no-alloc MoE layer takes banks of at most %u experts, hidden %u, intermediate %u "
+                    "(got %u, %u, %u)", NOALLOC_MAX_EXPERTS, NOALLOC_MAX_HIDDEN, NOALLOC_MAX_INTER, E, H, I);
+    MoeBuffers mb{};
+    const size_t need = carve_moe(nullptr, rows, E, H, I, mb);
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail(PW_ERR_ARGUMENT, "the no-alloc MoE layer needs %zu bytes of scratch, its array holds %zu", need,
+                    NOALLOC_SCRATCH_BYTES);
+    if (rt->device >= NOALLOC_MAX_DEVICES || !g_scratch_ptr[rt->device])
+        return fail(PW_ERR_DEVICE, "no scratch array address for device %d", rt->device);
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
+    carve_moe((char *)g_scratch_ptr[rt->device], rows, E, H, I, mb);
+    const uint32_t max_active = std::min<uint32_t>(E, rows * 8);
+    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, max_active, mb, rt->d_flags, s);
+    pw::launch_moe_layer(mode, bank->table, mb, x, x_dtype == PW_DTYPE_F32, rows, max_active, rows, H, I,
+                         out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
+                         out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr, out_dtype == PW_DTYPE_F32_RAW,
+                         rt->d_flags, s);
     PW_HIP(hipGetLastError());
     return PW_OK;
 }

@@ -348,6 +348,14 @@ class WideMoeRuntime:
                                         _ptr(route_ids), _ptr(route_weights), _ptr(out), out_dtype,
                                         stream or 0))
 
+    def moe_layer_device_noalloc(self, bank: ExpertBank, x, rows: int, route_ids, route_weights, out,
+                                 mode: int = MODE_A, x_dtype: int = DTYPE_BF16, out_dtype: int = DTYPE_BF16,
+                                 stream: Optional[int] = None):
+        """moe_layer_device on the library's static scratch (no device allocation): rows <= 8."""
+        check(lib().pw_moe_layer_device_noalloc(self.handle, bank.handle, mode, _ptr(x), x_dtype, rows,
+                                                _ptr(route_ids), _ptr(route_weights), _ptr(out), out_dtype,
+                                                stream or 0))
+
     def moe_prefill_device(self, bank: ExpertBank, x, rows: int, route_ids, route_weights, out,
                            x_dtype: int = DTYPE_BF16, out_dtype: int = DTYPE_BF16, stream: Optional[int] = None):
         """Mode B routed-MoE layer over up to 4096 token rows (grouped FP8 GEMM), device buffers."""

@@ -1,0 +1,64 @@
+"""The decode-layer entry point that allocates nothing (pw_moe_layer_device_noalloc) against the
+allocating one (pw_moe_layer_device), through the C ABI: same kernels, so the same bytes, on two
+calls in a row with the second one smaller (its static scratch keeps the first call's contents),
+in both modes; and requests beyond its limits fail with a clear error."""
+import numpy as np
+import pytest
+
+import oracle as O
+import prismwing_amd as P
+from prismwing_amd import workloads as WL
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def bank(rt):
+    return WL.synth_bank(rt, n_experts=256, seed=WL.SEED_BASE + 2)
+
+
+def _inputs(torch, rows, seed, f32=False):
+    x = WL.activations(rows, WL.SEED_BASE + seed)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    _, _, sel, w, _ = O.route(x, rw, bias)
+    xt = torch.from_numpy(x).cuda() if f32 else torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda()
+    return xt, torch.from_numpy(sel.astype(np.int32)).cuda(), torch.from_numpy(w).cuda()
+
+
+@pytest.mark.parametrize("mode", [P.MODE_A, P.MODE_B])
+@pytest.mark.parametrize("out_dtype", [P.DTYPE_F32_RAW, P.DTYPE_BF16])
+def test_noalloc_layer_equals_allocating_layer(rt, bank, mode, out_dtype):
+    import torch
+    stream = torch.cuda.current_stream().cuda_stream
+    for rows, seed, f32 in ((8, 150, False), (3, 151, False), (5, 152, True)):
+        xt, ids, wts = _inputs(torch, rows, seed, f32)
+        x_dtype = P.DTYPE_F32 if f32 else P.DTYPE_BF16
+        dt = torch.float32 if out_dtype == P.DTYPE_F32_RAW else torch.int16
+        want = torch.empty((rows, 4096), dtype=dt, device="cuda")
+        got = torch.full((rows, 4096), 7, dtype=dt, device="cuda")
+        rt.moe_layer_device(bank.bank, xt, rows, ids, wts, want, mode=mode, x_dtype=x_dtype, out_dtype=out_dtype,
+                            stream=stream)
+        rt.moe_layer_device_noalloc(bank.bank, xt, rows, ids, wts, got, mode=mode, x_dtype=x_dtype,
+                                    out_dtype=out_dtype, stream=stream)
+        torch.cuda.synchronize()
+        assert rt.take_flags() == 0
+        a, b = want.cpu().numpy(), got.cpu().numpy()
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (rows, mode, out_dtype)
+
+
+def test_noalloc_layer_rejects_requests_beyond_its_scratch(rt, bank):
+    import torch
+    xt, ids, wts = _inputs(torch, 9, 153)
+    out = torch.empty((9, 4096), dtype=torch.int16, device="cuda")
+    with pytest.raises(P.PwError, match="1 to 8 token rows"):
+        rt.moe_layer_device_noalloc(bank.bank, xt, 9, ids, wts, out)
+    # a bank with an intermediate size above 2048
+    g = rt.bind_projection(np.full((4096, 128), 0x38, np.uint8), np.ones((32, 1), np.float32))
+    d = rt.bind_projection(np.full((128, 4096), 0x38, np.uint8), np.ones((1, 32), np.float32))
+    wide = rt.expert_bank([g], [g], [d])
+    x = torch.zeros((1, 128), dtype=torch.int16, device="cuda")
+    ids1 = torch.zeros((1, 8), dtype=torch.int32, device="cuda")
+    w1 = torch.full((1, 8), 0.125, dtype=torch.float32, device="cuda")
+    out1 = torch.empty((1, 128), dtype=torch.int16, device="cuda")
+    with pytest.raises(P.PwError, match="intermediate 2048"):
+        rt.moe_layer_device_noalloc(wide, x, 1, ids1, w1, out1)
