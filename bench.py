@@ -335,28 +335,77 @@ def measured_traffic():
     return int(m.group(1)) if m else None
 
 
-def cpu_baseline(WL, bank, batch, budget_s=12.0):
-    """The C oracle (mode A, single thread) on a bounded sample of the same layer: the routed
-    experts of one width-8 batch, taken in ascending id until ~budget_s of CPU work."""
+def _cpu_threads():
+    """Worker threads for the all-cores legs: the process's affinity mask, at most 16 (the host
+    share of one GPU)."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    return max(1, min(16, affinity)), affinity
+
+
+def cpu_baseline(WL, bank, batch, scalar_budget_s=12.0, blas_budget_s=3.0):
+    """CPU legs on a bounded sample of the same layer (the routed experts of one width-8 batch):
+
+    - value: the reference's own CPU path restated (src/lib.rs:5807-5862, oracle.moe_layer_blas):
+      f32-dequantised weights (made before timing, as the reference makes them when it loads the
+      layer) and f32 SGEMMs per expert, experts dealt over all worker threads (one BLAS thread
+      each), combined in ascending expert id; whole layers repeated for ~blas_budget_s;
+    - the scalar C oracle (mode A): on one thread over the experts in ascending id until
+      ~scalar_budget_s, and the same per-expert arithmetic over all routed experts on all worker
+      threads.
+    GB/s counts the same algorithmic bytes as the GPU value (e4m3 weights and scales, activations)."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threadpoolctl import threadpool_limits
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     x, sel, w = batch
     used = sorted(set(sel.reshape(-1).tolist()))
-    done_bytes, t_total, n_exp = 0, 0.0, 0
+    threads, affinity = _cpu_threads()
+    hosts = {e: bank.expert_host(e) for e in used}
+    rows_of = {e: np.nonzero(sel == e)[0] for e in used}
+
+    # scalar oracle, one thread, then the same experts over all threads
+    done, t_one = [], 0.0
     for e in used:
-        host = bank.expert_host(e)
-        pos, slot = np.nonzero(sel == e)
-        xs = x[pos]
         t0 = time.perf_counter()
-        O.expert_mode_a(xs, host)
-        t_total += time.perf_counter() - t0
-        done_bytes += EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES + xs.nbytes
-        n_exp += 1
-        if t_total >= budget_s:
+        O.expert_mode_a(x[rows_of[e]], hosts[e])
+        t_one += time.perf_counter() - t0
+        done.append(e)
+        if t_one >= scalar_budget_s:
             break
-    return {"value": done_bytes / t_total / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"mode-A oracle (oracle/pw_oracle.c, single thread) over {n_exp} of the {len(used)} "
-                      f"routed experts of one width-8 batch ({t_total:.1f} s)"}
+    def expert_bytes(experts):
+        return sum(EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES + x[rows_of[e]].nbytes for e in experts)
+    with ThreadPoolExecutor(threads) as pool:
+        t0 = time.perf_counter()
+        list(pool.map(lambda e: O.expert_mode_a(x[rows_of[e]], hosts[e]), used))
+        t_all = time.perf_counter() - t0
+
+        # the reference's CPU BLAS path over the whole layer
+        def deq(e):
+            gw, gs, uw, us, dw, ds = hosts[e]
+            return e, (O.decode_fp8_matrix_f32(gw, gs), O.decode_fp8_matrix_f32(uw, us),
+                       O.decode_fp8_matrix_f32(dw, ds))
+        dequantised = dict(pool.map(deq, used))
+        layer_bytes = step_bytes(sel, x.shape[0])[1]
+        with threadpool_limits(1, "blas"):
+            O.moe_layer_blas(x, dequantised, sel, w, pool=pool)  # untimed first pass
+            reps, t0 = 0, time.perf_counter()
+            while reps < 2 or time.perf_counter() - t0 < blas_budget_s:
+                O.moe_layer_blas(x, dequantised, sel, w, pool=pool)
+                reps += 1
+            t_blas = (time.perf_counter() - t0) / reps
+    return {"value": round(layer_bytes / t_blas / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "layer_ms": round(t_blas * 1e3, 2),
+            "sample": f"the reference's CPU BLAS layer (f32-dequantised weights, f32 SGEMM per expert, "
+                      f"oracle.moe_layer_blas) over all {len(used)} routed experts of one width-8 batch, "
+                      f"{reps} layers timed on {threads} threads (OpenBLAS, one thread per expert)",
+            "hardware_concurrency": os.cpu_count(), "affinity_cpus": affinity,
+            "scalar_oracle": {"one_thread": {"GB/s": round(expert_bytes(done) / t_one / 1e9, 4),
+                                             "experts": len(done), "s": round(t_one, 2)},
+                              "all_threads": {"GB/s": round(expert_bytes(used) / t_all / 1e9, 4),
+                                              "experts": len(used), "s": round(t_all, 2), "threads": threads}}}
 
 
 def main():
@@ -461,7 +510,8 @@ def main():
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on a bounded sample")
         cpu = cpu_baseline(WL, bank, batches[0])
-        log(f"cpu baseline {cpu['value']:.3f} GB/s ({cpu['sample']})")
+        log(f"cpu baseline {cpu['value']:.3f} GB/s, {cpu['layer_ms']} ms per layer ({cpu['sample']}); "
+            f"scalar oracle {cpu['scalar_oracle']}")
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,

@@ -277,3 +277,53 @@ def full_qkv_scale_row(r: int) -> int:
 
 def swa_qkv_source_row(r: int) -> int:
     return lib().pwo_swa_qkv_source_row(r)
+
+
+# ------------------------------------------------------------------ the reference's CPU BLAS path
+def decode_fp8_matrix_f32(w: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """f32 copy of a block-FP8 matrix, dec(w[r, c]) * s[r / 128, c / 128] rounded to f32
+    (src/lib.rs:2003-2015; the reference makes these copies once, when it loads a layer)."""
+    lut = np.array([decode_e4m3fn(b) for b in range(256)], np.float32)
+    rows, cols = w.shape
+    full = np.repeat(np.repeat(np.asarray(s, np.float32), 128, axis=0)[:rows], 128, axis=1)[:, :cols]
+    return lut[w] * full
+
+
+def expert_blas_f32(x: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray) -> np.ndarray:
+    """One expert on the reference's CPU BLAS path (src/lib.rs:5807-5850): f32 SGEMMs against the
+    dequantised weights (x . G^T, x . U^T), silu(g) * u as g / (1 + exp(-g)) * u in f32, then
+    h . D^T. Summation order is the BLAS library's, so this agrees with the mode-A layer to f32
+    rounding, not bit for bit."""
+    x = np.asarray(x, np.float32)
+    g = x @ gate.T
+    u = x @ up.T
+    with np.errstate(over="ignore"):
+        h = (g / (np.float32(1.0) + np.exp(-g))) * u
+    return h @ down.T
+
+
+def moe_layer_blas(x: np.ndarray, dequantised: dict, selected: np.ndarray, weights: np.ndarray,
+                   pool=None) -> np.ndarray:
+    """The reference's CPU BLAS routed layer (src/lib.rs:5807-5862) over f32-dequantised experts
+    {id: (gate, up, down)}: per expert in ascending id, gather its token rows in ascending order,
+    run expert_blas_f32, and add y * route weight into the f32 block. With a thread pool the experts
+    run concurrently and are still combined in ascending id, so the block is the same either way."""
+    x = np.asarray(x, np.float32)
+    selected = np.asarray(selected)
+    rows = x.shape[0]
+    plan = []
+    for e in sorted(set(selected.reshape(-1).tolist())):
+        pos, slot = np.nonzero(selected == e)
+        order = np.argsort(pos, kind="stable")
+        plan.append((e, pos[order], np.asarray(weights, np.float32)[pos[order], slot[order]]))
+
+    def run(item):
+        e, pos, _ = item
+        return expert_blas_f32(x[pos], *dequantised[e])
+
+    outs = list(pool.map(run, plan)) if pool is not None else [run(p) for p in plan]
+    block = np.zeros((rows, x.shape[1]), np.float32)
+    for (e, pos, wts), y in zip(plan, outs):
+        for l, p in enumerate(pos.tolist()):
+            block[p] = block[p] + y[l] * wts[l]
+    return block

@@ -323,3 +323,68 @@ def test_staged_swiglu_rounds_every_stage():
     h = O.swiglu_bf16_staged(rng.standard_normal(4096).astype(np.float32) * 3,
                              rng.standard_normal(4096).astype(np.float32))
     assert not np.any(h.view(np.uint32) & 0xFFFF)
+
+
+# ------------------------------------------------------------------ the CPU BLAS restatement
+# (the CPU-baseline leg times it; src/lib.rs:2003-2015 and 5807-5862)
+def test_decode_fp8_matrix_f32_rounds_each_product_once():
+    """dec(w) * s is one f32 rounding of the exact product (f64 holds it exactly); a partial
+    trailing 128-row block and a partial 128-column block take their block's scale."""
+    rng = np.random.default_rng(700)
+    s = log_uniform_scales(rng, 300, 256)
+    w = fp8_weight(rng, 300, 256, s)
+    got = O.decode_fp8_matrix_f32(w, s)
+    assert got.shape == (300, 256) and got.dtype == np.float32
+    assert np.array_equal(got, dequant(w, s).astype(np.float32))
+    # the element at (299, 200) lives in block (2, 1)
+    assert got[299, 200] == np.float32(O.decode_e4m3fn(int(w[299, 200])) * np.float64(s[2, 1]))
+    # a partial trailing 128-column block
+    got2 = O.decode_fp8_matrix_f32(w[:, :200], s)
+    assert np.array_equal(got2, got[:, :200])
+
+
+@pytest.mark.parametrize("rows", [1, 4])
+def test_blas_layer_f64_brute_force(rows):
+    rng = np.random.default_rng(710 + rows)
+    hidden, inter, n_exp = 256, 256, 10
+    experts = _bank(rng, n_exp, hidden, inter)
+    x = bf16_normal(rng, (rows, hidden))
+    sel, w = _routes(rng, rows, n_exp)
+    deq = {e: (O.decode_fp8_matrix_f32(ex[0], ex[1]), O.decode_fp8_matrix_f32(ex[2], ex[3]),
+               O.decode_fp8_matrix_f32(ex[4], ex[5])) for e, ex in experts.items()}
+    got = O.moe_layer_blas(x, deq, sel, w)
+    want = np.zeros((rows, hidden))
+    for p in range(rows):
+        for e, wt in zip(sel[p].tolist(), w[p].tolist()):
+            want[p] += wt * _expert_f64(experts[e], x[p:p + 1])[0]
+    # f32 weight copies (one rounding per weight) and f32 sums: ~1e-6 relative; a swapped gate/up,
+    # a transposed projection or a weight on the wrong token moves the output by far more
+    assert np.max(np.abs(got - want)) <= 2e-5 * np.max(np.abs(want))
+    _, raw = O.moe_layer("a", x, experts, n_exp, sel, w, raw=True)
+    assert np.max(np.abs(got - raw)) <= 2e-5 * np.max(np.abs(raw))
+
+
+def test_blas_layer_thread_pool_and_one_hot():
+    """Experts run concurrently but combine in ascending id: same bits as the serial loop; one-hot
+    weights give the first routed expert's own output for that token (its rows gathered as the
+    layer gathers them: BLAS may sum a one-row product in another order)."""
+    from concurrent.futures import ThreadPoolExecutor
+    rng = np.random.default_rng(720)
+    hidden, inter, n_exp, rows = 256, 128, 12, 5
+    experts = _bank(rng, n_exp, hidden, inter)
+    deq = {e: (O.decode_fp8_matrix_f32(ex[0], ex[1]), O.decode_fp8_matrix_f32(ex[2], ex[3]),
+               O.decode_fp8_matrix_f32(ex[4], ex[5])) for e, ex in experts.items()}
+    x = bf16_normal(rng, (rows, hidden))
+    sel, w = _routes(rng, rows, n_exp)
+    serial = O.moe_layer_blas(x, deq, sel, w)
+    with ThreadPoolExecutor(4) as pool:
+        pooled = O.moe_layer_blas(x, deq, sel, w, pool=pool)
+    assert np.array_equal(serial.view(np.uint32), pooled.view(np.uint32))
+    one = np.zeros_like(w)
+    one[:, 0] = 1.0
+    got = O.moe_layer_blas(x, deq, sel, one)
+    for p in range(rows):
+        e = int(sel[p, 0])
+        pos = sorted({q for q in range(rows) if e in sel[q].tolist()})
+        want = O.expert_blas_f32(x[pos], *deq[e])[pos.index(p)]
+        assert np.array_equal(got[p], want), p
