@@ -118,24 +118,26 @@ __device__ __forceinline__ void pf_issue_w(PfW<C> &w, const uint8_t *wrow, uint3
 
 // The producer's copy of one step's codes into a ring slot (one block after another): instruction
 // c of a block covers tokens 8c .. 8c + 7; lane i reads global unit (i % 8) ^ (token % 8) of token
-// 8c + i / 8 and lands at LDS unit 64c + i (unit i % 8 of that token).
-template <class C>
+// 8c + i / 8 and lands at LDS unit 64c + i (unit i % 8 of that token). Only the NT 16-token tiles
+// that hold placements are copied.
+template <class C, int NT>
 __device__ __forceinline__ void pf_copy_codes(uint4 *slot, const uint8_t *const *csrc, uint32_t k0)
 {
 #pragma unroll
     for (int h = 0; h < C::SB; ++h)
 #pragma unroll
-        for (int c = 0; c < PF_DMA; ++c)
+        for (int c = 0; c < 2 * NT; ++c)  // the tokens of the NT active 16-token tiles
             lds_load16(csrc[c] + k0 + 128 * h, slot + h * PF_BLK + c * 64);
 }
 
-// One step: its blocks in ascending order, each block's FP8 products from one MFMA per 16-token
-// tile, then tot += (p * S_w) * a in f32. Each block's weight registers are refilled from column
+// One step: its blocks in ascending order, each block's FP8 products from one MFMA per active
+// 16-token tile, then tot += p * (S_w * a) in f32 (the two scales multiplied once per token and
+// block, four fused multiply-adds per tile). Each block's weight registers are refilled from column
 // knext (the step WS ahead) as soon as its MFMAs have read them, half a step earlier than a refill
 // of the whole step. cl0 / cl1: the lane's two code units of token r16 in a block (tile j adds
 // 16 tokens = 128 units).
-template <class C>
-__device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], PfW<C> &w, const uint4 *slot,
+template <class C, int NT>
+__device__ __forceinline__ void pf_compute(f32x4 (&tot)[NT], PfW<C> &w, const uint4 *slot,
                                            const float *lds_scale, const float *lds_wscale, uint32_t k, int r16,
                                            const uint8_t *wrow, uint32_t knext, uint32_t cl0, uint32_t cl1)
 {
@@ -147,9 +149,9 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], PfW<C> &w, const
         const i32x8 A = {(int)w.v[2 * h].x,     (int)w.v[2 * h].y,     (int)w.v[2 * h].z,     (int)w.v[2 * h].w,
                          (int)w.v[2 * h + 1].x, (int)w.v[2 * h + 1].y, (int)w.v[2 * h + 1].z, (int)w.v[2 * h + 1].w};
 #pragma unroll
-        for (int j = 0; j < PF_TT; ++j) {
+        for (int j = 0; j < NT; ++j) {
             const uint32_t t = 16 * j + r16;
-            const float sa = lds_scale[b * PF_MT + t];
+            const float sc = sw * lds_scale[b * PF_MT + t];
             const uint4 c0 = buf[cl0 + 128 * j];
             const uint4 c1 = buf[cl1 + 128 * j];
             const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
@@ -157,10 +159,112 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[PF_TT], PfW<C> &w, const
             const f32x4 p = mfma_fp8_16x16x128(A, xb, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                tot[j][i] = __builtin_fmaf(p[i] * sw, sa, tot[j][i]);
+                tot[j][i] = __builtin_fmaf(p[i], sc, tot[j][i]);
         }
         w.v[2 * h] = load_global16(wrow + knext + 128 * h);
         w.v[2 * h + 1] = load_global16(wrow + knext + 128 * h + 64);
+    }
+}
+
+// What the producer and consumer waves of one tile share (set up by prefill_b_kernel).
+struct PfTile {
+    uint4 *ring;               // [D][STEP] code units, swizzled
+    const float *lds_scale;    // [blocks][96] activation scales
+    const float *lds_wscale;   // [blocks] weight block scales
+    const uint8_t *wrow;       // this lane's weight row at its column offset (consumers)
+    uint16_t *out;             // this lane's first output: slot0 row, column col0 + wave * 16 + 4q
+    uint32_t R, nsteps, cnt_t;
+};
+
+// The K loop of one tile over NT active 16-token tiles: the producer wave keeps the codes ring
+// filled, the consumer waves run the MFMAs and write the bf16 outputs.
+template <class C, int NT>
+__device__ __forceinline__ void pf_body(const PfTile &tl, const uint32_t (&tok)[2], const uint8_t *codes, uint32_t K,
+                                        int wave, int lane)
+{
+    const uint32_t nsteps = tl.nsteps, last = nsteps - 1;
+    const int q = lane >> 4, r16 = lane & 15;
+    if (wave == PF_CONS) {
+        // ---- producer: the codes ring. Per-lane sources of the step's copy instructions.
+        const uint8_t *csrc[2 * NT];
+        const uint32_t g = ((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7;
+#pragma unroll
+        for (int c = 0; c < 2 * NT; ++c) {
+            const uint32_t t = 8 * c + (lane >> 3);
+            const uint32_t r0 = __shfl(tok[0], (int)(t & 63), 64), r1 = __shfl(tok[1], (int)(t & 63), 64);
+            csrc[c] = codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
+        }
+        // steps 0 .. C::D - 2 into slots 0 .. C::D - 2 (indices clamped to the last step)
+#pragma unroll
+        for (int s = 0; s < C::D - 1; ++s)
+            pf_copy_codes<C, NT>(tl.ring + s * C::STEP, csrc, ((uint32_t)s < last ? (uint32_t)s : last) * (128 * C::SB));
+        for (uint32_t k = 0; k < nsteps; ++k) {
+            // step k's copy (and every older one) is complete; C::D - 2 younger steps stay in flight
+            wait_vmcnt<(C::D - 2) * 2 * NT * C::SB>();
+            lds_barrier();  // publishes slot k % C::D; every consumer is done with step k - 1
+            const uint32_t s = k + C::D - 1;
+            pf_copy_codes<C, NT>(tl.ring + (s % C::D) * C::STEP, csrc, (s < last ? s : last) * (128 * C::SB));
+        }
+        wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
+        return;
+    }
+
+    // ---- consumers: 16 weight rows each, the weight ring in registers
+    const uint8_t *wrow = tl.wrow;
+    PfW<C> w[C::WS];
+#pragma unroll
+    for (int i = 0; i < C::WS; ++i)
+        pf_issue_w<C>(w[i], wrow, ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB));
+    // the lane's code units of token r16 in a block: units q and q + 4, swizzled by token % 8 (the
+    // same for token r16 + 16 j); opaque to the compiler, which would otherwise fold the tile
+    // offsets into one address register per tile and half instead of immediate offsets
+    uint32_t cl0 = (uint32_t)r16 * PF_UNITS + ((uint32_t)q ^ ((uint32_t)r16 & 7u));
+    uint32_t cl1 = (uint32_t)r16 * PF_UNITS + (((uint32_t)q + 4u) ^ ((uint32_t)r16 & 7u));
+    asm volatile("" : "+v"(cl0), "+v"(cl1));
+    f32x4 tot[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+        tot[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // this wave's scale copies (issued before the weights) are complete before the first barrier
+    wait_vmcnt<2 * C::SB * C::WS>();
+
+    // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each block's
+    // registers reloaded with step k + C::WS's block right after use. Whole groups of C::G steps
+    // run without early exits (static ring indices, one loop state at the loop head); the last
+    // steps are peeled. Load indices are clamped to the last step (the tail reloads it: cache
+    // hits), keeping every load unconditional.
+    const uint32_t nfull = nsteps - nsteps % C::G;
+    for (uint32_t b = 0; b < nfull; b += C::G) {
+#pragma unroll
+        for (int i = 0; i < C::G; ++i) {
+            const uint32_t k = b + i;
+            lds_barrier();
+            pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, tl.lds_wscale, k,
+                              r16, wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < C::G - 1; ++i) {
+        const uint32_t k = nfull + i;
+        if (k >= nsteps)
+            break;
+        lds_barrier();
+        pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, tl.lds_wscale, k, r16,
+                          wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
+    }
+
+    // epilogue: lane holds rows 4q + i of the wave's 16 for tokens 16j + r16 -> bf16
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const uint32_t t = 16 * j + r16;
+        if (t >= tl.cnt_t)
+            continue;
+        uint16_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            o[i] = (uint16_t)(f32_bits(round_bf16(tot[j][i])) >> 16);
+        *(uint2 *)(tl.out + (size_t)t * tl.R) =
+            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
     }
 }
 
@@ -172,7 +276,7 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
 {
     extern __shared__ uint4 lds_pf[];
     const uint32_t K = args.K, blocks = K >> 7;
-    const uint32_t nsteps = blocks / C::SB, last = nsteps - 1;  // the launcher checks blocks % SB
+    const uint32_t nsteps = blocks / C::SB;  // the launcher checks blocks % SB
     uint4 *ring = lds_pf;                                   // [D][STEP] code units, swizzled
     float *lds_scale = (float *)(ring + C::D * C::STEP);    // [blocks][96] activation scales
     float *lds_wscale = lds_scale + blocks * PF_MT;       // [blocks] weight block scales
@@ -239,90 +343,17 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
                 (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT + 64), 4, 0, 0);
     }
 
-    if (wave == PF_CONS) {
-        // ---- producer: the codes ring. Per-lane sources of the step's copy instructions.
-        const uint8_t *csrc[PF_DMA];
-        const uint32_t g = ((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7;
-#pragma unroll
-        for (int c = 0; c < PF_DMA; ++c) {
-            const uint32_t t = 8 * c + (lane >> 3);
-            const uint32_t r0 = __shfl(tok[0], (int)(t & 63), 64), r1 = __shfl(tok[1], (int)(t & 63), 64);
-            csrc[c] = args.codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
-        }
-        // steps 0 .. C::D - 2 into slots 0 .. C::D - 2 (indices clamped to the last step)
-#pragma unroll
-        for (int s = 0; s < C::D - 1; ++s)
-            pf_copy_codes<C>(ring + s * C::STEP, csrc, ((uint32_t)s < last ? (uint32_t)s : last) * (128 * C::SB));
-        for (uint32_t k = 0; k < nsteps; ++k) {
-            // step k's copy (and every older one) is complete; C::D - 2 younger steps stay in flight
-            wait_vmcnt<(C::D - 2) * PF_DMA * C::SB>();
-            lds_barrier();  // publishes slot k % C::D; every consumer is done with step k - 1
-            const uint32_t s = k + C::D - 1;
-            pf_copy_codes<C>(ring + (s % C::D) * C::STEP, csrc, (s < last ? s : last) * (128 * C::SB));
-        }
-        wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
-        return;
-    }
-
-    // ---- consumers: 16 weight rows each, the weight ring in registers
     const uint8_t *wmat = gather ? (second ? ae.ep.up_w : ae.ep.gate_w) : ae.ep.down_w;
-    const uint8_t *wrow = wmat + (size_t)(mrow0 + wave * 16 + r16) * K + q * 16;
-    PfW<C> w[C::WS];
-#pragma unroll
-    for (int i = 0; i < C::WS; ++i)
-        pf_issue_w<C>(w[i], wrow, ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB));
-    // the lane's code units of token r16 in a block: units q and q + 4, swizzled by token % 8 (the
-    // same for token r16 + 16 j); opaque to the compiler, which would otherwise fold the tile
-    // offsets into one address register per tile and half instead of immediate offsets
-    uint32_t cl0 = (uint32_t)r16 * PF_UNITS + ((uint32_t)q ^ ((uint32_t)r16 & 7u));
-    uint32_t cl1 = (uint32_t)r16 * PF_UNITS + (((uint32_t)q + 4u) ^ ((uint32_t)r16 & 7u));
-    asm volatile("" : "+v"(cl0), "+v"(cl1));
-    f32x4 tot[PF_TT];
-#pragma unroll
-    for (int j = 0; j < PF_TT; ++j)
-        tot[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // this wave's scale copies (issued before the weights) are complete before the first barrier
-    wait_vmcnt<2 * C::SB * C::WS>();
-
-    // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each block's
-    // registers reloaded with step k + C::WS's block right after use. Whole groups of C::G steps
-    // run without early exits (static ring indices, one loop state at the loop head); the last
-    // steps are peeled. Load indices are clamped to the last step (the tail reloads it: cache
-    // hits), keeping every load unconditional.
-    const uint32_t nfull = nsteps - nsteps % C::G;
-    for (uint32_t b = 0; b < nfull; b += C::G) {
-#pragma unroll
-        for (int i = 0; i < C::G; ++i) {
-            const uint32_t k = b + i;
-            lds_barrier();
-            pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, r16, wrow,
-                          (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < C::G - 1; ++i) {
-        const uint32_t k = nfull + i;
-        if (k >= nsteps)
-            break;
-        lds_barrier();
-        pf_compute<C>(tot, w[i % C::WS], ring + (i % C::D) * C::STEP, lds_scale, lds_wscale, k, r16, wrow,
-                      (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
-    }
-
-    // epilogue: lane holds rows 4q + i of the wave's 16 for tokens 16j + r16 -> bf16
-    const uint32_t R = args.R;
-    const uint32_t ocol = col0 + wave * 16 + 4 * q;
-#pragma unroll
-    for (int j = 0; j < PF_TT; ++j) {
-        const uint32_t t = 16 * j + r16;
-        if (t >= cnt_t)
-            continue;
-        uint16_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            o[i] = (uint16_t)(f32_bits(round_bf16(tot[j][i])) >> 16);
-        *(uint2 *)(args.out + (size_t)(slot0 + t) * R + ocol) =
-            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+    const PfTile tile{ring, lds_scale, lds_wscale, wmat + (size_t)(mrow0 + wave * 16 + r16) * K + q * 16,
+                      args.out + (size_t)slot0 * args.R + col0 + wave * 16 + 4 * q, args.R, nsteps, cnt_t};
+    // the workgroup's 16-token tiles that hold placements (1..6); whole tiles past them are skipped
+    switch ((cnt_t + 15) >> 4) {
+    case 1: pf_body<C, 1>(tile, tok, args.codes, K, wave, lane); break;
+    case 2: pf_body<C, 2>(tile, tok, args.codes, K, wave, lane); break;
+    case 3: pf_body<C, 3>(tile, tok, args.codes, K, wave, lane); break;
+    case 4: pf_body<C, 4>(tile, tok, args.codes, K, wave, lane); break;
+    case 5: pf_body<C, 5>(tile, tok, args.codes, K, wave, lane); break;
+    default: pf_body<C, 6>(tile, tok, args.codes, K, wave, lane); break;
     }
 }
 
