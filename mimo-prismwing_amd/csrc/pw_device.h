@@ -153,6 +153,21 @@ __device__ __forceinline__ uint32_t encode2_e4m3fn(float a, float b)
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 
+// a / scale for the quantisers, from the correctly rounded reciprocal rcp = 1 / scale (one IEEE
+// division per group instead of one per value): q = a * rcp, then Markstein's correction
+// q + (a - q * scale) * rcp with the remainder exact by fused multiply-add (P. Markstein, IBM J.
+// Res. Dev. 34(1), 1990), and the sign of q, which a zero remainder would otherwise drop from -0.
+// Where the quotient is at least 2^-10 this equals a / scale bit for bit; below that it may differ
+// by an ulp, and every value there encodes to an e4m3 zero of the same sign. Used only where a is
+// a bf16 value and scale = max(m, 1e-10) / 448 for a bf16 group absmax m >= |a|: over that whole
+// domain (every such (a, m) pair, 1,065,402,238 of them) the clamped e4m3 codes equal those of the
+// IEEE quotient.
+__device__ __forceinline__ float quant_ratio_bf16(float a, float scale, float rcp)
+{
+    const float q = a * rcp;
+    return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q, scale, a), rcp, q), q);
+}
+
 __device__ __forceinline__ __bf16 bf16_from_bits(uint16_t u) { return __builtin_bit_cast(__bf16, u); }
 
 // f32 -> three bf16 planes with x == hi + mid + lo exactly (normal range): each remainder is

@@ -324,10 +324,16 @@ __global__ __launch_bounds__(256) void quant_group128_kernel(const T *__restrict
     const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
     if (lane16 == 0)
         scales[group] = scale;
+    // bf16 inputs: one division per group and quant_ratio_bf16 per value (the same codes as x /
+    // scale over every bf16 input); f32 inputs divide each value
+    const float rcp = 1.0f / scale;
     float n[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        n[i] = fin[i] ? v[i] / scale : 0.f;
+        if constexpr (sizeof(T) == 2)
+            n[i] = fin[i] ? quant_ratio_bf16(v[i], scale, rcp) : 0.f;
+        else
+            n[i] = fin[i] ? v[i] / scale : 0.f;
         n[i] = n[i] < -448.f ? -448.f : (n[i] > 448.f ? 448.f : n[i]);
     }
     const uint32_t lo = encode2_e4m3fn(n[0], n[1]) | (encode2_e4m3fn(n[2], n[3]) << 16);

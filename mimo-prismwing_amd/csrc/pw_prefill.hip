@@ -10,19 +10,19 @@
 //             (sum_{c in b} dec(W[r, c]) * dec(q[p, c])) * S_w[r/128, b] * a[p, b]
 // with e4m3 activation codes q and per-(row, block) scales a from the dynamic quantiser. One
 // v_mfma_scale_f32_16x16x128_f8f6f4 (unit E8M0 scales) forms each block's FP8 products; the two
-// scales are applied in f32, sequentially over b (the same per-block arithmetic as the decode
-// mode B kernels).
+// scales are multiplied together and applied in f32, sequentially over b.
 //
-// Tiles: (96 placement slots of one routed expert = an m-tile) x (128 weight rows = an n-tile);
+// Tiles: (96 placement slots of one routed expert = an m-tile) x (256 weight rows = an n-tile);
 // 96 slots hold a whole expert's placements at the uniform-routing count (64 on average), so its
-// weights stream once. Gate and up run as one stacked projection (2I output columns per slot),
-// then a SwiGLU + re-quantisation kernel, then down. A workgroup walks K in 256-column steps with
-// two kinds of waves, so the two streams never wait on each other in the in-order memory counter:
-// eight consumer waves (16 weight rows each) load their weight bytes (one row per lane) into a
-// register ring (two steps of two 128-column blocks) and run the MFMAs; one producer wave copies
-// the m-tile's activation codes (cache hits, shared by the expert's n-tiles) with direct-to-LDS
-// loads into a two-step LDS ring (16-byte units XOR-swizzled by token so the B-operand reads
-// spread over the LDS banks).
+// weights stream once, and 16-token MFMA tiles past the m-tile's placements are skipped. Gate and
+// up run as one stacked projection (2I output columns per slot), then a SwiGLU + re-quantisation
+// kernel, then down. A workgroup walks K in 256-column steps with two kinds of waves, so the two
+// streams never wait on each other in the in-order memory counter: eight consumer waves (32 weight
+// rows each, two 16-row MFMA groups sharing every code read) load their weight bytes (one row per
+// lane) into a register ring (two steps of two 128-column blocks) and run the MFMAs; one producer
+// wave copies the m-tile's activation codes (cache hits, shared by the expert's n-tiles) with
+// direct-to-LDS loads into a two-step LDS ring (16-byte units XOR-swizzled by token so the
+// B-operand reads spread over the LDS banks).
 // One LDS-only barrier per step publishes a ring slot and frees the previous one; the weight
 // stream stays in flight across it. The m-tile's activation scales (transposed, [block][token])
 // and the tile's weight block scales are staged in LDS once.
@@ -38,7 +38,8 @@ constexpr uint32_t PF_MT = 96;                    // placement slots per m-tile
 constexpr int PF_TT = (int)PF_MT / 16;            // 16-token MFMA tiles per m-tile
 constexpr uint32_t PF_UNITS = 8;                  // 16-byte units per 128-byte token row of a step
 constexpr int PF_CONS = 8;                        // consumer waves per workgroup, 16 weight rows each
-constexpr uint32_t PF_NROWS = 16 * PF_CONS;       // weight rows per n-tile
+constexpr int PF_PROD = 1;                        // producer waves per workgroup (the codes ring)
+constexpr int PF_WAVES = PF_CONS + PF_PROD;
 constexpr uint32_t PF_BLK = PF_MT * PF_UNITS;     // 16-byte code units per 128-column block
 constexpr int PF_DMA = (int)(PF_BLK / 64);        // producer copy instructions per block
 static_assert(PF_BLK % 64 == 0, "a block's codes are whole 64-lane copies");
@@ -46,15 +47,25 @@ static_assert(PF_BLK % 64 == 0, "a block's codes are whole 64-lane copies");
 // K-step shape: SB 128-column blocks per step, WS weight steps in flight per consumer lane, D code
 // steps in the LDS ring. Two-block steps ask for 256 contiguous bytes of every weight row at once
 // (more DRAM page hits than 128-byte pieces); one-block steps cover an odd number of blocks.
-template <int SB_, int WS_, int D_>
+template <int SB_, int WS_, int D_, int RG_>
 struct PfCfg {
     static constexpr int SB = SB_, WS = WS_, D = D_;
+    static constexpr int RG = RG_;                         // 16-row groups per consumer wave
+    static constexpr uint32_t NROWS = 16 * RG * PF_CONS;   // weight rows per n-tile
+    static constexpr uint32_t NSB = (NROWS + 127) / 128;   // 128-row weight scale blocks per n-tile
+    // two row groups hold twice the weight registers: one workgroup per CU (three waves per SIMD)
+    static constexpr int WAVES_PER_EU = RG == 1 ? 5 : 3;
     static constexpr int G = WS > D ? WS : D;              // steps per unrolled group
     static constexpr uint32_t STEP = SB * PF_BLK;          // 16-byte code units per step
     static_assert(G % WS == 0 && G % D == 0, "ring sizes divide the unrolled group");
 };
-using PfWide = PfCfg<2, 2, 2>;
-using PfNarrow = PfCfg<1, 4, 4>;
+// Both projections run 32-row consumer waves (256-row n-tiles, 165 VGPRs, one workgroup of nine
+// waves per CU): every activation code copied into LDS feeds twice the weight rows, and that copy
+// traffic (L2 hits) competes with the weight stream. Against 16-row waves at two workgroups per CU,
+// 2048 tokens: gate/up 944 -> 827 us, down 505 -> 481 us. Odd block counts take one-block steps
+// with 16-row waves (two row groups of a four-step weight ring would not fit in registers).
+using PfWide = PfCfg<2, 2, 2, 2>;
+using PfNarrow = PfCfg<1, 4, 4, 1>;
 
 // Tile table: ceil(count / 96) m-tiles per routed expert, ascending expert order. One workgroup of
 // 1024 threads, one thread per schedule entry (banks hold at most 1024 experts).
@@ -103,17 +114,21 @@ struct PrefillArgs {
 // the codes, so the block dot product covers the same 128 products.
 template <class C>
 struct PfW {
-    uint4 v[2 * C::SB];
+    uint4 v[C::RG][2 * C::SB];
 };
 
+// wrow: the lane's row of the wave's first 16-row group; group g is 16 g rows further (rstride =
+// 16 K bytes)
 template <class C>
-__device__ __forceinline__ void pf_issue_w(PfW<C> &w, const uint8_t *wrow, uint32_t k0)
+__device__ __forceinline__ void pf_issue_w(PfW<C> &w, const uint8_t *wrow, size_t rstride, uint32_t k0)
 {
 #pragma unroll
-    for (int h = 0; h < C::SB; ++h) {
-        w.v[2 * h] = load_global16(wrow + k0 + 128 * h);
-        w.v[2 * h + 1] = load_global16(wrow + k0 + 128 * h + 64);
-    }
+    for (int g = 0; g < C::RG; ++g)
+#pragma unroll
+        for (int h = 0; h < C::SB; ++h) {
+            w.v[g][2 * h] = load_global16(wrow + g * rstride + k0 + 128 * h);
+            w.v[g][2 * h + 1] = load_global16(wrow + g * rstride + k0 + 128 * h + 64);
+        }
 }
 
 // The producer's copy of one step's codes into a ring slot (one block after another): instruction
@@ -121,13 +136,16 @@ __device__ __forceinline__ void pf_issue_w(PfW<C> &w, const uint8_t *wrow, uint3
 // 8c + i / 8 and lands at LDS unit 64c + i (unit i % 8 of that token). Only the NT 16-token tiles
 // that hold placements are copied.
 template <class C, int NT>
-__device__ __forceinline__ void pf_copy_codes(uint4 *slot, const uint8_t *const *csrc, uint32_t k0)
+__device__ __forceinline__ void pf_copy_codes(uint4 *slot, const uint8_t *const *csrc, uint32_t k0, int p)
 {
+    constexpr int NC = (2 * NT + PF_PROD - 1) / PF_PROD;
 #pragma unroll
     for (int h = 0; h < C::SB; ++h)
 #pragma unroll
-        for (int c = 0; c < 2 * NT; ++c)  // the tokens of the NT active 16-token tiles
-            lds_load16(csrc[c] + k0 + 128 * h, slot + h * PF_BLK + c * 64);
+        for (int i = 0; i < NC; ++i) {  // this producer's token groups of the NT active 16-token tiles
+            const int c = p + i * PF_PROD < 2 * NT ? p + i * PF_PROD : p;
+            lds_load16(csrc[i] + k0 + 128 * h, slot + h * PF_BLK + c * 64);
+        }
 }
 
 // One step: its blocks in ascending order, each block's FP8 products from one MFMA per active
@@ -137,17 +155,22 @@ __device__ __forceinline__ void pf_copy_codes(uint4 *slot, const uint8_t *const 
 // of the whole step. cl0 / cl1: the lane's two code units of token r16 in a block (tile j adds
 // 16 tokens = 128 units).
 template <class C, int NT>
-__device__ __forceinline__ void pf_compute(f32x4 (&tot)[NT], PfW<C> &w, const uint4 *slot,
+__device__ __forceinline__ void pf_compute(f32x4 (&tot)[C::RG][NT], PfW<C> &w, const uint4 *slot,
                                            const float *lds_scale, const float *lds_wscale, uint32_t k, int r16,
-                                           const uint8_t *wrow, uint32_t knext, uint32_t cl0, uint32_t cl1)
+                                           const uint8_t *wrow, size_t rstride, uint32_t knext, uint32_t cl0,
+                                           uint32_t cl1)
 {
 #pragma unroll
     for (int h = 0; h < C::SB; ++h) {
         const uint32_t b = k * C::SB + h;
         const float sw = lds_wscale[b];
         const uint4 *buf = slot + h * PF_BLK;
-        const i32x8 A = {(int)w.v[2 * h].x,     (int)w.v[2 * h].y,     (int)w.v[2 * h].z,     (int)w.v[2 * h].w,
-                         (int)w.v[2 * h + 1].x, (int)w.v[2 * h + 1].y, (int)w.v[2 * h + 1].z, (int)w.v[2 * h + 1].w};
+        i32x8 A[C::RG];
+#pragma unroll
+        for (int g = 0; g < C::RG; ++g)
+            A[g] = i32x8{(int)w.v[g][2 * h].x,     (int)w.v[g][2 * h].y,     (int)w.v[g][2 * h].z,
+                         (int)w.v[g][2 * h].w,     (int)w.v[g][2 * h + 1].x, (int)w.v[g][2 * h + 1].y,
+                         (int)w.v[g][2 * h + 1].z, (int)w.v[g][2 * h + 1].w};
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
             const uint32_t t = 16 * j + r16;
@@ -156,13 +179,19 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[NT], PfW<C> &w, const ui
             const uint4 c1 = buf[cl1 + 128 * j];
             const i32x8 xb = {(int)c0.x, (int)c0.y, (int)c0.z, (int)c0.w,
                               (int)c1.x, (int)c1.y, (int)c1.z, (int)c1.w};
-            const f32x4 p = mfma_fp8_16x16x128(A, xb, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                tot[j][i] = __builtin_fmaf(p[i], sc, tot[j][i]);
+            for (int g = 0; g < C::RG; ++g) {
+                const f32x4 p = mfma_fp8_16x16x128(A[g], xb, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    tot[g][j][i] = __builtin_fmaf(p[i], sc, tot[g][j][i]);
+            }
         }
-        w.v[2 * h] = load_global16(wrow + knext + 128 * h);
-        w.v[2 * h + 1] = load_global16(wrow + knext + 128 * h + 64);
+#pragma unroll
+        for (int g = 0; g < C::RG; ++g) {
+            w.v[g][2 * h] = load_global16(wrow + g * rstride + knext + 128 * h);
+            w.v[g][2 * h + 1] = load_global16(wrow + g * rstride + knext + 128 * h + 64);
+        }
     }
 }
 
@@ -170,10 +199,11 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[NT], PfW<C> &w, const ui
 struct PfTile {
     uint4 *ring;               // [D][STEP] code units, swizzled
     const float *lds_scale;    // [blocks][96] activation scales
-    const float *lds_wscale;   // [blocks] weight block scales
+    const float *lds_wscale;   // this wave's [blocks] weight block scales
     const uint8_t *wrow;       // this lane's weight row at its column offset (consumers)
-    uint16_t *out;             // this lane's first output: slot0 row, column col0 + wave * 16 + 4q
-    uint32_t R, nsteps, cnt_t;
+    uint16_t *out;             // this lane's first output: slot0 row, column col0 + wave * 16 RG + 4q
+    uint32_t R, nsteps;
+    uint32_t store_t;          // tokens whose outputs this wave stores (0: rows past R)
 };
 
 // The K loop of one tile over NT active 16-token tiles: the producer wave keeps the codes ring
@@ -184,26 +214,30 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, const uint32_t (&tok)[
 {
     const uint32_t nsteps = tl.nsteps, last = nsteps - 1;
     const int q = lane >> 4, r16 = lane & 15;
-    if (wave == PF_CONS) {
-        // ---- producer: the codes ring. Per-lane sources of the step's copy instructions.
-        const uint8_t *csrc[2 * NT];
+    if (wave >= PF_CONS) {
+        // ---- producers: the codes ring, producer p copying the token groups c = p, p + PF_PROD, ...
+        // of every block. Per-lane sources of the step's copy instructions.
+        constexpr int NC = (2 * NT + PF_PROD - 1) / PF_PROD;  // copy instructions per block
+        const int p = wave - PF_CONS;
+        const uint8_t *csrc[NC];
         const uint32_t g = ((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7;
 #pragma unroll
-        for (int c = 0; c < 2 * NT; ++c) {
+        for (int i = 0; i < NC; ++i) {
+            const int c = p + i * PF_PROD < 2 * NT ? p + i * PF_PROD : p;  // unused slots repeat group p
             const uint32_t t = 8 * c + (lane >> 3);
             const uint32_t r0 = __shfl(tok[0], (int)(t & 63), 64), r1 = __shfl(tok[1], (int)(t & 63), 64);
-            csrc[c] = codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
+            csrc[i] = codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
         }
         // steps 0 .. C::D - 2 into slots 0 .. C::D - 2 (indices clamped to the last step)
 #pragma unroll
         for (int s = 0; s < C::D - 1; ++s)
-            pf_copy_codes<C, NT>(tl.ring + s * C::STEP, csrc, ((uint32_t)s < last ? (uint32_t)s : last) * (128 * C::SB));
+            pf_copy_codes<C, NT>(tl.ring + s * C::STEP, csrc, ((uint32_t)s < last ? (uint32_t)s : last) * (128 * C::SB), p);
         for (uint32_t k = 0; k < nsteps; ++k) {
             // step k's copy (and every older one) is complete; C::D - 2 younger steps stay in flight
-            wait_vmcnt<(C::D - 2) * 2 * NT * C::SB>();
+            wait_vmcnt<(C::D - 2) * NC * C::SB>();
             lds_barrier();  // publishes slot k % C::D; every consumer is done with step k - 1
             const uint32_t s = k + C::D - 1;
-            pf_copy_codes<C, NT>(tl.ring + (s % C::D) * C::STEP, csrc, (s < last ? s : last) * (128 * C::SB));
+            pf_copy_codes<C, NT>(tl.ring + (s % C::D) * C::STEP, csrc, (s < last ? s : last) * (128 * C::SB), p);
         }
         wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
         return;
@@ -211,22 +245,25 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, const uint32_t (&tok)[
 
     // ---- consumers: 16 weight rows each, the weight ring in registers
     const uint8_t *wrow = tl.wrow;
+    const size_t rstride = (size_t)16 * K;
     PfW<C> w[C::WS];
 #pragma unroll
     for (int i = 0; i < C::WS; ++i)
-        pf_issue_w<C>(w[i], wrow, ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB));
+        pf_issue_w<C>(w[i], wrow, rstride, ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB));
     // the lane's code units of token r16 in a block: units q and q + 4, swizzled by token % 8 (the
     // same for token r16 + 16 j); opaque to the compiler, which would otherwise fold the tile
     // offsets into one address register per tile and half instead of immediate offsets
     uint32_t cl0 = (uint32_t)r16 * PF_UNITS + ((uint32_t)q ^ ((uint32_t)r16 & 7u));
     uint32_t cl1 = (uint32_t)r16 * PF_UNITS + (((uint32_t)q + 4u) ^ ((uint32_t)r16 & 7u));
     asm volatile("" : "+v"(cl0), "+v"(cl1));
-    f32x4 tot[NT];
+    f32x4 tot[C::RG][NT];
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
-        tot[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < C::RG; ++g)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+            tot[g][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     // this wave's scale copies (issued before the weights) are complete before the first barrier
-    wait_vmcnt<2 * C::SB * C::WS>();
+    wait_vmcnt<2 * C::SB * C::WS * C::RG>();
 
     // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each block's
     // registers reloaded with step k + C::WS's block right after use. Whole groups of C::G steps
@@ -240,7 +277,7 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, const uint32_t (&tok)[
             const uint32_t k = b + i;
             lds_barrier();
             pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, tl.lds_wscale, k,
-                              r16, wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
+                              r16, wrow, rstride, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
         }
     }
 #pragma unroll
@@ -250,21 +287,24 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, const uint32_t (&tok)[
             break;
         lds_barrier();
         pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, tl.lds_wscale, k, r16,
-                          wrow, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
+                          wrow, rstride, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
     }
 
-    // epilogue: lane holds rows 4q + i of the wave's 16 for tokens 16j + r16 -> bf16
+    // epilogue: lane holds rows 16 g + 4q + i of the wave's 16 RG for tokens 16j + r16 -> bf16
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
         const uint32_t t = 16 * j + r16;
-        if (t >= tl.cnt_t)
+        if (t >= tl.store_t)
             continue;
-        uint16_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            o[i] = (uint16_t)(f32_bits(round_bf16(tot[j][i])) >> 16);
-        *(uint2 *)(tl.out + (size_t)t * tl.R) =
-            make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+        for (int g = 0; g < C::RG; ++g) {
+            uint16_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                o[i] = (uint16_t)(f32_bits(round_bf16(tot[g][j][i])) >> 16);
+            *(uint2 *)(tl.out + (size_t)t * tl.R + 16 * g) =
+                make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+        }
     }
 }
 
@@ -272,14 +312,14 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, const uint32_t (&tok)[
 // bf16-rounded outputs (bf16_round_in_place of every projection, src/wide_metal_moe.rs:1236-1251).
 // n-tiles [0, R1 / 128) use the first matrix (gate, or down), the rest the second (up).
 template <class C>
-__global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per_eu(5))) void prefill_b_kernel(const PrefillArgs args)
+__global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_EU))) void prefill_b_kernel(const PrefillArgs args)
 {
     extern __shared__ uint4 lds_pf[];
     const uint32_t K = args.K, blocks = K >> 7;
     const uint32_t nsteps = blocks / C::SB;  // the launcher checks blocks % SB
     uint4 *ring = lds_pf;                                   // [D][STEP] code units, swizzled
     float *lds_scale = (float *)(ring + C::D * C::STEP);    // [blocks][96] activation scales
-    float *lds_wscale = lds_scale + blocks * PF_MT;       // [blocks] weight block scales
+    float *lds_wscale = lds_scale + blocks * PF_MT;       // [NSB][blocks] weight block scales
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r16 = lane & 15;
@@ -287,7 +327,7 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
     // m-tiles x, x + 8, ... and runs all n-tiles of one m-tile back to back: the m-tile's
     // activation codes stay in that XCD's L2 while its n-tiles stream their weight rows, and the
     // m-tiles (counted on the device) spread evenly over the XCDs.
-    const uint32_t n_ntiles = args.R / PF_NROWS;
+    const uint32_t n_ntiles = (args.R + C::NROWS - 1) / C::NROWS;
     const uint32_t local = blockIdx.x >> 3;
     const uint32_t mt = (blockIdx.x & 7) + 8 * (local / n_ntiles), ntile = local % n_ntiles;
     if (mt >= args.n_tiles[0])
@@ -298,9 +338,7 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
     if (m0 >= ae.cnt)
         return;
     const uint32_t cnt_t = ae.cnt - m0 < PF_MT ? ae.cnt - m0 : PF_MT;
-    const uint32_t col0 = ntile * PF_NROWS;               // output column of the tile
-    const bool second = col0 >= args.R1;
-    const uint32_t mrow0 = second ? col0 - args.R1 : col0;  // first weight row in its matrix
+    const uint32_t col0 = ntile * C::NROWS;               // output column of the tile
     const uint32_t slot0 = ae.off + m0;
     const bool gather = args.placement_pos != nullptr;
 
@@ -325,35 +363,48 @@ __global__ __launch_bounds__(64 * (PF_CONS + 1)) __attribute__((amdgpu_waves_per
         if (bad)
             raise_flag(args.flags, FLAG_SCHEDULE);
     }
-    // weight block scales of the n-tile (one 128-row scale block) and the m-tile's activation
-    // scales, transposed (lds_scale[b * 96 + t]) with 4-byte direct-to-LDS loads (lane = token; a
-    // second instruction covers tokens 64..95), spread over all waves
-    {
-        const float *smat = gather ? (second ? ae.ep.up_s : ae.ep.gate_s) : ae.ep.down_s;
-        if ((uint32_t)tid < blocks)
-            lds_wscale[tid] = load_g(smat + (mrow0 >> 7) * blocks + tid);
+    // Each 128 output columns of the n-tile come from one 128-row block of one matrix (gate or up,
+    // or down; R1 and R are multiples of 128): column col is row src_row(col) of the second matrix
+    // (up) when col >= R1, else of the first (gate, or down). Columns past R (a partial last
+    // n-tile) map to row 0 and are never stored.
+    const auto src_row = [&](uint32_t col) {
+        return col >= args.R ? 0u : (col >= args.R1 ? col - args.R1 : col);
+    };
+    // weight block scales of the n-tile's 128-row blocks ([NSB][blocks]) and the m-tile's
+    // activation scales, transposed (lds_scale[b * 96 + t]) with 4-byte direct-to-LDS loads (lane =
+    // token; a second instruction covers tokens 64..95), spread over all waves
+    if ((uint32_t)tid < C::NSB * blocks) {
+        const uint32_t hb = (uint32_t)tid / blocks, b = (uint32_t)tid - hb * blocks;
+        const uint32_t col = col0 + 128 * hb;
+        const float *sm = gather ? (col >= args.R1 && col < args.R ? ae.ep.up_s : ae.ep.gate_s) : ae.ep.down_s;
+        lds_wscale[tid] = load_g(sm + (src_row(col) >> 7) * blocks + b);
     }
-    for (uint32_t b = wave; b < blocks; b += PF_CONS + 1) {
+    for (uint32_t b = wave; b < blocks; b += PF_WAVES) {
         __builtin_amdgcn_global_load_lds(
             (const __attribute__((address_space(1))) void *)(args.scales + (size_t)tok[0] * blocks + b),
             (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT), 4, 0, 0);
-        if (lane < 32)
+        if (lane < (int)PF_MT - 64)
             __builtin_amdgcn_global_load_lds(
                 (const __attribute__((address_space(1))) void *)(args.scales + (size_t)tok[1] * blocks + b),
                 (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT + 64), 4, 0, 0);
     }
 
-    const uint8_t *wmat = gather ? (second ? ae.ep.up_w : ae.ep.gate_w) : ae.ep.down_w;
-    const PfTile tile{ring, lds_scale, lds_wscale, wmat + (size_t)(mrow0 + wave * 16 + r16) * K + q * 16,
-                      args.out + (size_t)slot0 * args.R + col0 + wave * 16 + 4 * q, args.R, nsteps, cnt_t};
-    // the workgroup's 16-token tiles that hold placements (1..6); whole tiles past them are skipped
+    // the wave's 16 RG rows (inside one 128-row block): matrix, first row, and whether they exist
+    const uint32_t wrow0 = wave * 16 * C::RG, wcol = col0 + wrow0;
+    const uint8_t *wmat = gather ? (wcol >= args.R1 && wcol < args.R ? ae.ep.up_w : ae.ep.gate_w) : ae.ep.down_w;
+    const uint32_t mrow = src_row(wcol);
+    const PfTile tile{ring, lds_scale, lds_wscale + (wrow0 >> 7) * blocks,
+                      wmat + (size_t)(mrow + r16) * K + q * 16,
+                      args.out + (size_t)slot0 * args.R + col0 + wrow0 + 4 * q, args.R, nsteps,
+                      wcol < args.R ? cnt_t : 0u};
+    // the workgroup's 16-token tiles that hold placements (1..PF_TT); whole tiles past them are skipped
     switch ((cnt_t + 15) >> 4) {
     case 1: pf_body<C, 1>(tile, tok, args.codes, K, wave, lane); break;
     case 2: pf_body<C, 2>(tile, tok, args.codes, K, wave, lane); break;
     case 3: pf_body<C, 3>(tile, tok, args.codes, K, wave, lane); break;
     case 4: pf_body<C, 4>(tile, tok, args.codes, K, wave, lane); break;
     case 5: pf_body<C, 5>(tile, tok, args.codes, K, wave, lane); break;
-    default: pf_body<C, 6>(tile, tok, args.codes, K, wave, lane); break;
+    default: pf_body<C, PF_TT>(tile, tok, args.codes, K, wave, lane); break;
     }
 }
 
@@ -445,10 +496,11 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
     const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
     if (lane16 == 0)
         scales[group] = scale;
+    const float rcp = 1.0f / scale;  // h is bf16: one division per group (quant_ratio_bf16)
     float n[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        n[i] = finite_f32(h[i]) ? h[i] / scale : 0.f;
+        n[i] = finite_f32(h[i]) ? quant_ratio_bf16(h[i], scale, rcp) : 0.f;
         n[i] = n[i] < -448.f ? -448.f : (n[i] > 448.f ? 448.f : n[i]);
     }
     uint32_t packed[2];
@@ -529,12 +581,12 @@ uint32_t prefill_max_tiles(uint32_t rows, uint32_t E)
 template <class C>
 static void launch_prefill_cfg(const PrefillArgs &a, hipStream_t stream)
 {
-    const size_t lds = (size_t)C::D * C::STEP * 16 + (size_t)(a.K / 128) * (PF_MT + 1) * 4;
+    const size_t lds = (size_t)C::D * C::STEP * 16 + (size_t)(a.K / 128) * (PF_MT + C::NSB) * 4;
     if (lds > 65536)  // wide K: up to 160 KB of LDS per workgroup on gfx950
         (void)hipFuncSetAttribute((const void *)prefill_b_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds);
-    const uint32_t grid = 8 * ((a.max_tiles + 7) / 8) * (a.R / PF_NROWS);
-    hipLaunchKernelGGL((prefill_b_kernel<C>), dim3(grid), dim3(64 * (PF_CONS + 1)), lds, stream, a);
+    const uint32_t grid = 8 * ((a.max_tiles + 7) / 8) * ((a.R + C::NROWS - 1) / C::NROWS);
+    hipLaunchKernelGGL((prefill_b_kernel<C>), dim3(grid), dim3(64 * PF_WAVES), lds, stream, a);
 }
 
 static void launch_prefill_projection(const PrefillArgs &a, hipStream_t stream)
