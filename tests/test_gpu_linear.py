@@ -174,6 +174,51 @@ def test_quantiser_encoder_sweep(rt):
     assert np.array_equal(codes, codes_ref)
 
 
+def _bf16_division_sweep():
+    """bf16 groups whose first value is the group absmax m (sign alternating) and whose other 127
+    values are bf16 numbers with |a| <= m: for 1,528 absmaxes (every bf16 exponent with six
+    mantissas, subnormals and values below the 1e-10 scale clamp), every bf16 magnitude from m down
+    twenty binades (quotients a / scale from 448 to below the smallest e4m3 subnormal), both signs."""
+    ms = [(e << 7) | mant for e in range(1, 255) for mant in (0x00, 0x01, 0x3F, 0x40, 0x55, 0x7F)]
+    ms += [0x0001, 0x0040, 0x007F, 0x2EDB, 0x2E00]  # subnormal bf16 and absmaxes under 1e-10
+    groups = []
+    for mb in ms:
+        e = mb >> 7
+        lo = max(0, (e - 20)) << 7
+        mags = np.arange(lo, mb + 1, dtype=np.uint32)
+        vals = np.concatenate([mags, mags | 0x8000])
+        pad = (-vals.size) % 127
+        vals = np.concatenate([vals, np.zeros(pad, np.uint32)]).reshape(-1, 127)
+        head = np.full((vals.shape[0], 1), mb, np.uint32)
+        head[1::2] |= 0x8000
+        groups.append(np.concatenate([head, vals], axis=1))
+    bits = np.concatenate(groups).astype(np.uint16)
+    return bits.reshape(-1, 512) if bits.shape[0] % 4 == 0 else np.concatenate(
+        [bits, np.zeros(((-bits.shape[0]) % 4, 128), np.uint16)]).reshape(-1, 512)
+
+
+def test_quantiser_bf16_division_sweep(rt):
+    """bf16 activations are quantised through one correctly rounded reciprocal per group (a
+    Markstein-corrected quotient): codes and scales equal the oracle's IEEE division bit for bit
+    over ~8.6M values around every binade of the absmax."""
+    torch = _torch()
+    bits = _bf16_division_sweep()
+    rows, k = bits.shape
+    x32 = (bits.astype(np.uint32) << 16).view(np.float32)
+    codes_ref, scales_ref, _ = O.dynamic_fp8(x32)
+    xt = torch.from_numpy(bits.view(np.int16)).cuda()
+    codes = torch.empty((rows, k), dtype=torch.uint8, device="cuda")
+    scales = torch.empty((rows, k // 128), dtype=torch.float32, device="cuda")
+    rt.quantize_fp8_group128_device(xt, rows, k, codes, scales, x_dtype=P.DTYPE_BF16,
+                                    stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    assert np.array_equal(scales.cpu().numpy().view(np.uint32), scales_ref.view(np.uint32))
+    got = codes.cpu().numpy()
+    bad = np.argwhere(got != codes_ref)
+    assert bad.size == 0, (bad[:4], x32[tuple(bad[0])] if bad.size else None)
+
+
 def quantize_device(rt, data):
     torch = _torch()
     rows, k = data.shape
