@@ -55,6 +55,13 @@ def upload(torch, WL, batches):
     return dev
 
 
+def placement_histogram(sel, experts=256):
+    """{placements per routed expert: number of experts} over a batch's routes."""
+    counts = np.bincount(np.asarray(sel).reshape(-1), minlength=experts)
+    vals, freq = np.unique(counts[counts > 0], return_counts=True)
+    return {int(v): int(f) for v, f in zip(vals, freq)}
+
+
 def step_bytes(sel, rows, hidden=4096):
     u = int(np.unique(sel).size)
     return u, u * (EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES) + rows * hidden * 2 * 2 + rows * 8 * 8
@@ -98,7 +105,8 @@ def time_layer(torch, rt, bank, P, dev_batches, rows, steps, warmup, mode, settl
         settle(torch, run)
     for i in range(warmup):
         run(i)
-    torch.cuda.synchronize()
+    # the start event queues behind the warm-up steps: the timed steps start on a busy GPU, with
+    # no drained queue or idle gap in front of them
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for i in range(steps):
@@ -148,7 +156,6 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
     settle(torch, run)
     for _ in range(warmup):
         run()
-    torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(steps):
@@ -171,10 +178,13 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
     flops = 2.0 * rows * 8 * EXPERT_MACS
     wbytes = u * (EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES)
     tflops = flops / (ms * 1e-3) / 1e12
+    counts = np.bincount(sel.reshape(-1), minlength=256)
     return {"layer_us": round(ms * 1000, 2), "TFLOP/s": round(tflops, 1),
             "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
             "weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1), "unique_experts": u,
-            "max_count": int(np.bincount(sel.reshape(-1), minlength=256).max()), "kernels_us": kt}
+            "max_count": int(counts.max()), "m_tiles_96": int(np.sum((counts + 95) // 96)),
+            "top_counts": sorted(counts.tolist(), reverse=True)[:8],
+            "count_quartiles": [int(v) for v in np.percentile(counts, [0, 25, 50, 75, 100])], "kernels_us": kt}
 
 
 def _time_calls(torch, rt, run, n_calls, warmup=3):
@@ -183,7 +193,6 @@ def _time_calls(torch, rt, run, n_calls, warmup=3):
     settle(torch, lambda i: run(i, stream.cuda_stream), 0.1)
     for i in range(warmup):
         run(i, stream.cuda_stream)
-    torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for i in range(n_calls):
@@ -306,6 +315,25 @@ def projection_legs(torch, rt, bank, P, WL, calls=200):
     return out
 
 
+def layer_with_router(torch, rt, bank, P, WL, rows=8, steps=200, warmup=20):
+    """One decode step including its routing: the device router (logits, sigmoid + bias, top-8,
+    weights) on the batch's activations, then the width-8 layer on those routes, per step."""
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    wt = torch.from_numpy(WL.bf16_bits_np(rw).view(np.int16)).cuda()
+    bt = torch.from_numpy(bias).cuda()
+    xs = [_bf16_x(torch, WL, rows, 4096, WL.SEED_BASE + 100 + b) for b in range(8)]
+    ids = torch.empty((rows, 8), dtype=torch.int32, device="cuda")
+    wts = torch.empty((rows, 8), dtype=torch.float32, device="cuda")
+    out = torch.empty((rows, 4096), dtype=torch.int16, device="cuda")
+
+    def run(i, st):
+        x = xs[i % len(xs)]
+        rt.route_device(x, rows, 4096, wt, 256, bt, ids, wts, stream=st)
+        rt.moe_layer_device(bank.bank, x, rows, ids, wts, out, mode=P.MODE_A, out_dtype=P.DTYPE_BF16, stream=st)
+
+    return {"us": round(_time_calls(torch, rt, run, steps, warmup), 2), "rows": rows}
+
+
 def router_leg(torch, rt, P, WL, rows=8, calls=200):
     """On-device router (logits, sigmoid, top-8, weights) for one decode batch: x [8 x 4096] bf16,
     router weights [256 x 4096] bf16."""
@@ -420,6 +448,8 @@ def main():
                     help="run only the 2048-token prefill leg and print its line (for profiling)")
     ap.add_argument("--router-only", action="store_true",
                     help="run only the on-device router leg and print its line (for profiling)")
+    ap.add_argument("--routing", choices=("uniform", "zipf"), default="uniform",
+                    help="routing of the headline decode leg and of --prefill-only (zipf: for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -450,13 +480,13 @@ def main():
     log("synthesising the 256-expert bank (6.4 GB) on the device")
     bank = WL.synth_bank(rt, 256, seed=WL.SEED_BASE + 2)
     if args.prefill_only:
-        res = prefill_leg(torch, rt, bank, P, WL, zipf=False)
-        print(json.dumps({"workload": "routed-MoE prefill, 2048 tokens, top-8 of 256 experts, mode B",
-                          **res}), flush=True)
+        res = prefill_leg(torch, rt, bank, P, WL, zipf=args.routing == "zipf")
+        print(json.dumps({"workload": "routed-MoE prefill, 2048 tokens, top-8 of 256 experts, mode B, "
+                                      f"{args.routing} routing", **res}), flush=True)
         rt.close()
         return
     rows = 8
-    batches = build_batches(P, WL, args.batches, rows, zipf=False)
+    batches = build_batches(P, WL, args.batches, rows, zipf=args.routing == "zipf")
     dev_batches = upload(torch, WL, batches)
     sizes = [step_bytes(sel, rows) for _, sel, _ in batches]
     avg_u = float(np.mean([u for u, _ in sizes]))
@@ -478,7 +508,8 @@ def main():
 
     extras = {"kernels_us": {k: round(v["avg_us"], 2) for k, v in kt.items()},
               "layer_us": round(ms * 1000, 2), "tokens_per_s": round(rows / (ms * 1e-3), 1),
-              "hbm_frac": round(value / HBM_PEAK_GBS, 4), "avg_unique_experts": avg_u}
+              "hbm_frac": round(value / HBM_PEAK_GBS, 4), "avg_unique_experts": avg_u,
+              "placement_histogram": placement_histogram(np.concatenate([s for _, s, _ in batches]))}
     if not args.no_extras:
         zb = build_batches(P, WL, args.batches, rows, zipf=True)
         zd = upload(torch, WL, zb)
@@ -486,7 +517,9 @@ def main():
         zms = time_layer(torch, rt, bank, P, zd, rows, args.steps, args.warmup, P.MODE_A)
         extras["zipf_w8"] = {"layer_us": round(zms * 1000, 2),
                              "avg_unique_experts": float(np.mean([u for u, _ in zs])),
-                             "GB/s": round(float(np.mean([b for _, b in zs])) / (zms * 1e-3) / 1e9, 1)}
+                             "GB/s": round(float(np.mean([b for _, b in zs])) / (zms * 1e-3) / 1e9, 1),
+                             "zipf_s": WL.ZIPF_S, "zipf_kappa": WL.ZIPF_KAPPA,
+                             "placement_histogram": placement_histogram(np.concatenate([s for _, s, _ in zb]))}
         bms = time_layer(torch, rt, bank, P, dev_batches, rows, args.steps, args.warmup, P.MODE_B)
         extras["mode_b_w8"] = {"layer_us": round(bms * 1000, 2),
                                "GB/s": round(avg_bytes / (bms * 1e-3) / 1e9, 1)}
@@ -501,6 +534,7 @@ def main():
         for zipf in (False, True):
             extras["prefill_t2048" + ("_zipf" if zipf else "")] = prefill_leg(torch, rt, bank, P, WL, zipf)
         extras["router_w8"] = router_leg(torch, rt, P, WL)
+        extras["layer_plus_router_w8"] = layer_with_router(torch, rt, bank, P, WL)
         extras.update(projection_legs(torch, rt, bank, P, WL))
         for k, v in extras.items():
             if isinstance(v, dict) and k != "kernels_us":
@@ -519,8 +553,10 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp8-e4m3 x bf16 (f32 acc)",
         "data": "synthetic (seeded; weights, scales, activations, router)",
         "config": {"workload": "routed-MoE decode layer, 8 token rows, top-8 of 256 experts, hidden 4096, "
-                               "intermediate 2048, block-FP8 128x128, mode A, uniform routing",
-                   "rows": rows, "experts": 256, "top_k": 8, "hidden": 4096, "intermediate": 2048},
+                               f"intermediate 2048, block-FP8 128x128, mode A, {args.routing} routing",
+                   "rows": rows, "experts": 256, "top_k": 8, "hidden": 4096, "intermediate": 2048,
+                   "routing": "routes computed before the timed steps and resident in HBM; the device router is "
+                              "timed alone (extras.router_w8) and with the layer (extras.layer_plus_router_w8)"},
         "roofline": roofline, "cpu_baseline": cpu, "extras": extras,
     }
     print(json.dumps(line), flush=True)
