@@ -124,6 +124,9 @@ void launch_bf16_linear(const Bf16Args &a, int planes, int bpw, float *y32, uint
 
 // Gate/up with the SwiGLU fused and no split partials (pw_moe_a.hip), when the routed rows fit the
 // LDS stage; returns false (nothing launched) otherwise.
+// The one-expert forward's whole-K down projection with the output rounding fused (K = I of 1024
+// or 2048, at most eight rows); false when the shape does not fit it.
+bool launch_moe_a_down_out(const SplitArgs &args, float *out_f32, uint16_t *out_bf16, bool raw, hipStream_t stream);
 bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_active, uint16_t *hidden_planes,
                                hipStream_t stream);
 void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t I, uint16_t *hidden_planes,

@@ -1072,9 +1072,17 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
 }
 
 // Mode A: gate/up (+SwiGLU) then down, both as split-K expert projections (pw_moe_a.hip).
+// Where the one-expert forward's rounded output goes when its down projection writes it directly.
+struct DirectOut {
+    float *f32;
+    uint16_t *bf16;
+    bool raw;
+};
+
 static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, uint32_t rows,
                               uint32_t placements, uint32_t max_active, uint32_t max_count, uint32_t H,
-                              uint32_t I, uint32_t *flags, hipStream_t stream, const ActiveExpert *one = nullptr)
+                              uint32_t I, uint32_t *flags, hipStream_t stream, const ActiveExpert *one = nullptr,
+                              const DirectOut *direct = nullptr)
 {
     const int nt = max_count > 16 ? 2 : 1;
     const uint32_t cnt = max_count < 16u * nt ? max_count : 16u * nt;
@@ -1136,9 +1144,14 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
         da.active = mb.pieces;
         da.cap = PIECE_ROWS;
     }
+    t = timer_begin(K_MOE_DOWN, stream);
+    // one expert: the whole-K down writes the rounded output rows itself
+    if (one && direct && launch_moe_a_down_out(da, direct->f32, direct->bf16, direct->raw, stream)) {
+        timer_end(t, stream);
+        return ExpertOut{nullptr, 0, 0};
+    }
     const SplitPlan dp = plan_split(I, 1, 3, pieces ? PIECE_ROWS : cnt);
     da.KS = dp.ks;
-    t = timer_begin(K_MOE_DOWN, stream);
     launch_moe_a_split(1, 3, pieces ? 1 : nt, da, dp, pieces ? placements : max_active, stream);
     timer_end(t, stream);
     return ExpertOut{mb.partial, dp.ks, (size_t)placements * H};
@@ -1210,7 +1223,10 @@ void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, const ExpertPt
         one.cnt = rows;
         for (uint32_t k = 0; k < 16; ++k)
             one.tok[k] = (uint16_t)k;
-        eo = launch_a_moe(mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream, &one);
+        const DirectOut direct{out_f32, out_bf16, raw};
+        eo = launch_a_moe(mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream, &one, &direct);
+        if (!eo.y)
+            return;  // the down projection wrote the output
     } else {
         hipLaunchKernelGGL(moe_single_plan_kernel, dim3(1), dim3(256), 0, stream, bank, expert, rows, mb.plan,
                            mb.active_expert, mb.active_offset, mb.active, mb.placement_pos, mb.placement_w);

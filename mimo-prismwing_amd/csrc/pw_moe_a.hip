@@ -381,6 +381,151 @@ bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_activ
     return true;
 }
 
+// Down over the whole K in one workgroup for one expert's rows, output rounding fused: the
+// one-expert forward's last launch (dense MLP, complete expert). Work item: 16 rows of down.
+// Eight waves split K = I (wave w: blocks [w * BPW, (w + 1) * BPW)), each with all of its weight
+// loads in flight at once; the expert's three bf16 hidden planes (rows 0..cnt-1) go straight into
+// LDS; the eight split sums meet in LDS and are added in split order 0..7, then rounded to bf16 (or
+// kept as raw f32) and written as the output rows: no split partials through memory, no rounding
+// launch.
+template <int BPW>
+__global__ __launch_bounds__(512) void moe_a_down_out_kernel(const SplitArgs args, float *__restrict__ out_f32,
+                                                             uint16_t *__restrict__ out_bf16, uint32_t raw)
+{
+    extern __shared__ uint4 lds_x[];  // [3 * cnt][K/8 + 1]; then the split partials [8][64]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // split index, wave-uniform
+    const int q = lane >> 4, r16 = lane & 15;
+    const ActiveExpert &ae = args.one;
+    const uint32_t cnt = ae.cnt;
+    if (cnt == 0 || cnt > args.cap) {
+        if (tid == 0 && cnt != 0)
+            raise_flag(args.flags, FLAG_SCHEDULE);
+        return;
+    }
+    const uint32_t K = args.K, R = args.R;
+    constexpr uint32_t KC = BPW * 128;
+    const uint32_t k0 = wave * KC;
+    const uint32_t row0 = blockIdx.x * 16;
+
+    // 1. this wave's weight bytes, all in flight at once, and its block scales
+    uint4 wv[BPW][2];
+    const uint8_t *wrow = ae.ep.down_w + (size_t)(row0 + r16) * K + k0 + q * 16;
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            wv[j][h] = load_global16(wrow + j * 128 + h * 64);
+    const uint32_t blocks = K >> 7;
+    float sc[BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+        sc[j] = load_g(ae.ep.down_s + (row0 >> 7) * blocks + (k0 >> 7) + j);
+
+    // 2. the hidden rows (three planes, whole K) -> LDS: wave w copies its K split of every row and
+    //    plane (KC / 8 16-byte units per row, at most 64 lanes per instruction)
+    constexpr uint32_t PER_SPLIT = KC / 8, LANES = PER_SPLIT < 64 ? PER_SPLIT : 64, CPS = PER_SPLIT / LANES;
+    // (unrolled over the eight possible rows: a loop would make the compiler wait for every
+    // outstanding weight load before its first iteration)
+    const uint32_t stride = K / 8 + 1;
+#pragma unroll
+    for (uint32_t t = 0; t < 8; ++t)
+        if (t < cnt) {
+#pragma unroll
+            for (uint32_t p = 0; p < 3; ++p)
+#pragma unroll
+                for (uint32_t c = 0; c < CPS; ++c)
+                    if ((uint32_t)lane < LANES)
+                        lds_load16(args.x + p * args.x_plane + (size_t)t * K + k0 + (c * 64 + lane) * 8,
+                                   lds_x + (p * cnt + t) * stride + (k0 >> 3) + c * 64);
+        }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // 3. block partials on the MFMA, block scale in registers (as moe_a_split_kernel)
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool ok = (uint32_t)r16 < cnt;
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bf16x8 A0 = fp8x8_to_bf16x8(wv[j][h].x, wv[j][h].y);
+            const bf16x8 A1 = fp8x8_to_bf16x8(wv[j][h].z, wv[j][h].w);
+            const uint32_t cu = (k0 >> 3) + j * 16 + h * 8 + q * 2;
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+                if (ok) {
+                    const uint4 *xp = lds_x + (p * cnt + r16) * stride + cu;
+                    x0 = xp[0];
+                    x1 = xp[1];
+                }
+                acc = mfma_bf16_16x16x32(A0, bf16x8_from_u4(x0), acc);
+                acc = mfma_bf16_16x16x32(A1, bf16x8_from_u4(x1), acc);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            tot[i] = __builtin_fmaf(sc[j], acc[i], tot[i]);
+    }
+
+    // 4. the eight split partials meet in LDS (after every wave is done with the activations),
+    //    summed in split order; lane: rows 4q .. 4q + 3 of the 16, row r16 of the output
+    __syncthreads();
+    f32x4 *red = (f32x4 *)lds_x;  // [8 splits][64 lanes]
+    red[wave * 64 + lane] = tot;
+    __syncthreads();
+    if (wave != 0 || !ok)
+        return;
+    f32x4 sum = red[lane];
+#pragma unroll
+    for (int sp = 1; sp < 8; ++sp) {
+        const f32x4 o = red[sp * 64 + lane];
+        sum[0] += o[0];
+        sum[1] += o[1];
+        sum[2] += o[2];
+        sum[3] += o[3];
+    }
+    bool bad = false;
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        r[i] = round_bf16(sum[i]);
+        bad |= !finite_f32(r[i]);
+    }
+    const size_t at = (size_t)r16 * R + row0 + q * 4;
+    if (out_f32)
+        *(float4 *)(out_f32 + at) = raw ? make_float4(sum[0], sum[1], sum[2], sum[3]) : make_float4(r[0], r[1], r[2], r[3]);
+    if (out_bf16)
+        *(uint2 *)(out_bf16 + at) = make_uint2((f32_bits(r[0]) >> 16) | (f32_bits(r[1]) & 0xffff0000u),
+                                               (f32_bits(r[2]) >> 16) | (f32_bits(r[3]) & 0xffff0000u));
+    if (bad)
+        raise_flag(args.flags, FLAG_ROUND_NONFINITE);
+}
+
+bool launch_moe_a_down_out(const SplitArgs &args, float *out_f32, uint16_t *out_bf16, bool raw, hipStream_t stream)
+{
+    // eight K splits of one or two 128-column blocks each, output rows in whole 16-row tiles,
+    // the three hidden planes of up to eight rows within LDS
+    const uint32_t K = args.K;
+    if (!args.single || (K != 8 * 128 && K != 16 * 128) || args.R % 16 != 0 || args.one.cnt > 8)
+        return false;
+    const size_t stage = (size_t)3 * args.one.cnt * (K / 8 + 1) * 16, red = (size_t)8 * 64 * 16;
+    const size_t lds = stage > red ? stage : red;
+    const dim3 grid(args.R >> 4), block(512);
+    if (K == 16 * 128) {
+        if (lds > 65536)
+            (void)hipFuncSetAttribute((const void *)moe_a_down_out_kernel<2>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)lds);
+        hipLaunchKernelGGL((moe_a_down_out_kernel<2>), grid, block, lds, stream, args, out_f32, out_bf16, raw ? 1u : 0u);
+    } else {
+        hipLaunchKernelGGL((moe_a_down_out_kernel<1>), grid, block, lds, stream, args, out_f32, out_bf16, raw ? 1u : 0u);
+    }
+    return true;
+}
+
 // Gate/up split sums (in split order 0..KS-1) -> h = (g / (1 + e^-g)) * u in f32 (swiglu_f32,
 // kernels/block_fp8_gemv.metal:241-252; CPU src/lib.rs:5840-5844), written as three exact bf16
 // planes for the down projection's MFMA. One thread per (slot, 4 rows). With KS known at compile
