@@ -203,15 +203,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
 // are added in split order 0..7 -- the same order and the same arithmetic as the split kernel
 // followed by moe_a_swiglu_kernel, so the hidden planes are bit-identical -- and the SwiGLU is
 // written as three exact bf16 planes. No split partials go through memory.
-template <int NS, int BPW>
+// RM = 8 (the one-expert forward): a work item is 8 rows of gate and the same 8 rows of up, stacked
+// into one 16-row MFMA operand (lanes 0..7 of a row group read gate rows, 8..15 up rows), so a lone
+// expert spreads over twice the workgroups; output rows 0..7 are gate, 8..15 up, and each gate
+// lane takes its up values from the lane 32 above. The sums are the same as with RM = 16.
+template <int NS, int BPW, int RM>
 __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs args, uint16_t *__restrict__ hidden)
 {
+    constexpr int MATS = RM == 16 ? 2 : 1;  // 16-row MFMA operands per block
     extern __shared__ uint4 lds_x[];  // [NS * cnt][K/8 + 1]; then the split partials [8][2][64]
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // split index, wave-uniform
     const int q = lane >> 4, r16 = lane & 15;
-    const uint32_t G = args.R >> 4;
+    const uint32_t G = args.R / RM;
     const uint32_t g = blockIdx.x % G, a = blockIdx.x / G;
     const ActiveExpert ae = args.single ? args.one : args.active[a];
     if (ae.cnt == 0)
@@ -224,28 +229,44 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     const uint32_t K = args.K;
     constexpr uint32_t KC = BPW * 128;
     const uint32_t k0 = wave * KC;
-    const uint32_t row0 = g * 16;
+    const uint32_t row0 = g * RM;
 
     // 1. this wave's weight bytes of gate and up, all in flight at once
-    const uint8_t *wbase[2] = {ae.ep.gate_w, ae.ep.up_w};
-    const float *sbase[2] = {ae.ep.gate_s, ae.ep.up_s};
-    uint4 wv[2][BPW][2];
+    uint4 wv[MATS][BPW][2];
+    const uint32_t blocks = K >> 7;
+    float sc[MATS][BPW];
+    if constexpr (RM == 16) {
+        const uint8_t *wbase[2] = {ae.ep.gate_w, ae.ep.up_w};
+        const float *sbase[2] = {ae.ep.gate_s, ae.ep.up_s};
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-        const uint8_t *wrow = wbase[m] + (size_t)(row0 + r16) * K + k0 + q * 16;
+        for (int m = 0; m < 2; ++m) {
+            const uint8_t *wrow = wbase[m] + (size_t)(row0 + r16) * K + k0 + q * 16;
+#pragma unroll
+            for (int j = 0; j < BPW; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    wv[m][j][h] = load_global16(wrow + j * 128 + h * 64);
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int j = 0; j < BPW; ++j)
+                sc[m][j] = load_g(sbase[m] + (row0 >> 7) * blocks + (k0 >> 7) + j);
+    } else {
+        // operand row r16: gate row row0 + r16 (r16 < 8) or up row row0 + r16 - 8; output rows
+        // 4q..4q+3 are gate rows for q < 2 and up rows for q >= 2, so each lane scales by its
+        // output rows' matrix
+        const uint8_t *wrow = (r16 < 8 ? ae.ep.gate_w : ae.ep.up_w) + (size_t)(row0 + (r16 & 7)) * K + k0 + q * 16;
 #pragma unroll
         for (int j = 0; j < BPW; ++j)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                wv[m][j][h] = load_global16(wrow + j * 128 + h * 64);
-    }
-    const uint32_t blocks = K >> 7;
-    float sc[2][BPW];
-#pragma unroll
-    for (int m = 0; m < 2; ++m)
+                wv[0][j][h] = load_global16(wrow + j * 128 + h * 64);
+        const float *srow = (q < 2 ? ae.ep.gate_s : ae.ep.up_s) + (row0 >> 7) * blocks + (k0 >> 7);
 #pragma unroll
         for (int j = 0; j < BPW; ++j)
-            sc[m][j] = load_g(sbase[m] + (row0 >> 7) * blocks + (k0 >> 7) + j);
+            sc[0][j] = load_g(srow + j);
+    }
 
     // 2. the routed activation rows, whole K (= 8 * KC), planes -> LDS: wave w copies the 64
     //    16-byte units of its own K split of every row and plane, fully unrolled (one instruction
@@ -273,16 +294,22 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     __syncthreads();
 
     // 3. block partials on the MFMA, block scale in registers (as moe_a_split_kernel)
-    f32x4 tot[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 tot[MATS];
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+        tot[m] = f32x4{0.f, 0.f, 0.f, 0.f};
     const bool ok = (uint32_t)r16 < ae.cnt;
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
-        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        f32x4 acc[MATS];
+#pragma unroll
+        for (int m = 0; m < MATS; ++m)
+            acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            bf16x8 A[2][2];
+            bf16x8 A[MATS][2];
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
+            for (int m = 0; m < MATS; ++m) {
                 A[m][0] = fp8x8_to_bf16x8(wv[m][j][h].x, wv[m][j][h].y);
                 A[m][1] = fp8x8_to_bf16x8(wv[m][j][h].z, wv[m][j][h].w);
             }
@@ -296,14 +323,14 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
                     x1 = xp[1];
                 }
 #pragma unroll
-                for (int m = 0; m < 2; ++m) {
+                for (int m = 0; m < MATS; ++m) {
                     acc[m] = mfma_bf16_16x16x32(A[m][0], bf16x8_from_u4(x0), acc[m]);
                     acc[m] = mfma_bf16_16x16x32(A[m][1], bf16x8_from_u4(x1), acc[m]);
                 }
             }
         }
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
+        for (int m = 0; m < MATS; ++m)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 tot[m][i] = __builtin_fmaf(sc[m][j], acc[m][i], tot[m][i]);
@@ -311,27 +338,39 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
 
     // 4. the eight split partials meet in LDS (after every wave is done with the activations)
     __syncthreads();
-    f32x4 *red = (f32x4 *)lds_x;  // [8 splits][2 mats][64 lanes]
-    red[(wave * 2 + 0) * 64 + lane] = tot[0];
-    red[(wave * 2 + 1) * 64 + lane] = tot[1];
+    f32x4 *red = (f32x4 *)lds_x;  // [8 splits][MATS][64 lanes]
+#pragma unroll
+    for (int m = 0; m < MATS; ++m)
+        red[(wave * MATS + m) * 64 + lane] = tot[m];
     __syncthreads();
-    if (wave != 0 || !ok)
+    if (wave != 0)
         return;
     // lane: rows 4q .. 4q + 3 of the 16, token r16; split sums in order 0..7, then the SwiGLU
-    float v[2][4];
+    float s[MATS][4];
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
+    for (int m = 0; m < MATS; ++m) {
         f32x4 sum = red[m * 64 + lane];
 #pragma unroll
         for (int sp = 1; sp < 8; ++sp) {
-            const f32x4 o = red[(sp * 2 + m) * 64 + lane];
+            const f32x4 o = red[(sp * MATS + m) * 64 + lane];
             sum[0] += o[0];
             sum[1] += o[1];
             sum[2] += o[2];
             sum[3] += o[3];
         }
-        v[m][0] = sum[0]; v[m][1] = sum[1]; v[m][2] = sum[2]; v[m][3] = sum[3];
+        s[m][0] = sum[0]; s[m][1] = sum[1]; s[m][2] = sum[2]; s[m][3] = sum[3];
     }
+    float v[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[0][i] = s[0][i];
+        if constexpr (RM == 16)
+            v[1][i] = s[1][i];
+        else
+            v[1][i] = __shfl(s[0][i], (lane + 32) & 63, 64);  // the up rows of this lane's gate rows
+    }
+    if (!ok || (RM == 8 && q >= 2))
+        return;
     uint16_t hp[3][4];
     bool bad = false;
 #pragma unroll
@@ -366,18 +405,22 @@ bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_activ
     if (args.K != 8 * 4 * 128 || args.R % 16 != 0 || (uint32_t)ns * args.cap > 8)
         return false;
     const size_t lds = fused_lds(ns, args.cap, args.K);
-    const dim3 grid(max_active * (args.R >> 4)), block(512);
+    // a lone expert (the one-expert forward) takes 8 + 8-row work items: twice the workgroups
+    const bool half = args.single && args.R % 8 == 0;
+    const dim3 grid(max_active * (args.R / (half ? 8 : 16))), block(512);
+#define PW_FUSED(NS, RM)                                                                                     \
+    do {                                                                                                      \
+        if (lds > 65536)                                                                                      \
+            (void)hipFuncSetAttribute((const void *)moe_a_gateup_fused_kernel<NS, 4, RM>,                     \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                  \
+        hipLaunchKernelGGL((moe_a_gateup_fused_kernel<NS, 4, RM>), grid, block, lds, stream, args, hidden_planes); \
+    } while (0)
     if (ns == 3) {
-        if (lds > 65536)
-            (void)hipFuncSetAttribute((const void *)moe_a_gateup_fused_kernel<3, 4>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL((moe_a_gateup_fused_kernel<3, 4>), grid, block, lds, stream, args, hidden_planes);
+        if (half) PW_FUSED(3, 8); else PW_FUSED(3, 16);
     } else {
-        if (lds > 65536)
-            (void)hipFuncSetAttribute((const void *)moe_a_gateup_fused_kernel<1, 4>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        hipLaunchKernelGGL((moe_a_gateup_fused_kernel<1, 4>), grid, block, lds, stream, args, hidden_planes);
+        if (half) PW_FUSED(1, 8); else PW_FUSED(1, 16);
     }
+#undef PW_FUSED
     return true;
 }
 
