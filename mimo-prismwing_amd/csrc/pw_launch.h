@@ -127,6 +127,12 @@ void launch_bf16_linear(const Bf16Args &a, int planes, int bpw, float *y32, uint
 // The one-expert forward's whole-K down projection with the output rounding fused (K = I of 1024
 // or 2048, at most eight rows); false when the shape does not fit it.
 bool launch_moe_a_down_out(const SplitArgs &args, float *out_f32, uint16_t *out_bf16, bool raw, hipStream_t stream);
+// Down and combine of a one-token decode batch in one launch (mode A, I = 2048, eight routed
+// experts; args are the down projection's, whose rows are the eight placement slots): the same
+// arithmetic as the split-K down followed by the combine; false when the batch does not fit it.
+// Only for batches of one token.
+bool launch_moe_a_down_combine1(const SplitArgs &args, const MoePlan *plan, const float *placement_w, float *out_f32,
+                                uint16_t *out_bf16, bool raw, hipStream_t stream);
 bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_active, uint16_t *hidden_planes,
                                hipStream_t stream);
 void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t I, uint16_t *hidden_planes,

@@ -1145,8 +1145,11 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
         da.cap = PIECE_ROWS;
     }
     t = timer_begin(K_MOE_DOWN, stream);
-    // one expert: the whole-K down writes the rounded output rows itself
-    if (one && direct && launch_moe_a_down_out(da, direct->f32, direct->bf16, direct->raw, stream)) {
+    // one expert: the whole-K down writes the rounded output rows itself; a one-token batch: down
+    // and combine in one launch
+    if (direct && (one ? launch_moe_a_down_out(da, direct->f32, direct->bf16, direct->raw, stream)
+                       : launch_moe_a_down_combine1(da, mb.plan, mb.placement_w, direct->f32, direct->bf16,
+                                                    direct->raw, stream))) {
         timer_end(t, stream);
         return ExpertOut{nullptr, 0, 0};
     }
@@ -1177,11 +1180,13 @@ static void launch_b_moe(const ExpertPtrs *bank, const MoeBuffers &mb, uint32_t 
 
 static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                                 bool x_f32, uint32_t rows, uint32_t placements, uint32_t max_active,
-                                uint32_t max_count, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream)
+                                uint32_t max_count, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream,
+                                const DirectOut *direct = nullptr)
 {
     const bool wide = max_count > 16;
     if (mode == 0)
-        return launch_a_moe(mb, x, x_f32, rows, placements, max_active, max_count, H, I, flags, stream);
+        return launch_a_moe(mb, x, x_f32, rows, placements, max_active, max_count, H, I, flags, stream, nullptr,
+                            direct);
     launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
     if (wide) launch_b_moe<4, 2>(bank, mb, rows, placements, max_active, H, I, flags, stream);
     else launch_b_moe<4, 1>(bank, mb, rows, placements, max_active, H, I, flags, stream);
@@ -1193,8 +1198,11 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
                       hipStream_t stream)
 {
-    const ExpertOut eo =
-        launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, max_active, max_count, H, I, flags, stream);
+    const DirectOut direct{out_f32, out_bf16, raw};
+    const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, max_active, max_count, H, I, flags,
+                                        stream, rows == 1 ? &direct : nullptr);
+    if (!eo.y)
+        return;  // the one-token down wrote the combined output
     const uint32_t n4 = rows * (H >> 2);
     const int t = timer_begin(K_MOE_COMBINE, stream);
 #define PW_COMBINE(KS)                                                                                         \

@@ -231,7 +231,31 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     const uint32_t k0 = wave * KC;
     const uint32_t row0 = g * RM;
 
-    // 1. this wave's weight bytes of gate and up, all in flight at once
+    // 1. the routed activation rows, whole K (= 8 * KC), planes -> LDS: wave w copies the 64
+    //    16-byte units of its own K split of every row and plane, fully unrolled (one instruction
+    //    per row and plane, since KC / 8 = 64 units), and reads nothing else of the stage
+    static_assert(KC / 8 == 64, "one 64-lane copy per row and split");
+    constexpr uint32_t per_row = 8 * KC / 8, stride = per_row + 1;
+    bool bad_row = false;
+#pragma unroll
+    for (uint32_t t = 0; t < 16u; ++t) {
+        if (t < ae.cnt) {
+            uint32_t src = ae.tok[t];
+            if (src >= args.rows) {
+                bad_row = true;
+                src = args.rows - 1;
+            }
+#pragma unroll
+            for (uint32_t p = 0; p < (uint32_t)NS; ++p)
+                lds_load16(args.x + p * args.x_plane + (size_t)src * K + k0 + lane * 8,
+                           lds_x + (p * ae.cnt + t) * stride + wave * 64);
+        }
+    }
+    if (bad_row && tid == 0)
+        raise_flag(args.flags, FLAG_SCHEDULE);
+    asm volatile("" ::: "memory");  // the copies stay the oldest memory operations
+
+    // 2. this wave's weight bytes of gate and up, all in flight at once
     uint4 wv[MATS][BPW][2];
     const uint32_t blocks = K >> 7;
     float sc[MATS][BPW];
@@ -268,30 +292,9 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
             sc[0][j] = load_g(srow + j);
     }
 
-    // 2. the routed activation rows, whole K (= 8 * KC), planes -> LDS: wave w copies the 64
-    //    16-byte units of its own K split of every row and plane, fully unrolled (one instruction
-    //    per row and plane, since KC / 8 = 64 units)
-    static_assert(KC / 8 == 64, "one 64-lane copy per row and split");
-    constexpr uint32_t per_row = 8 * KC / 8, stride = per_row + 1;
-    bool bad_row = false;
-#pragma unroll
-    for (uint32_t t = 0; t < 16u; ++t) {
-        if (t < ae.cnt) {
-            uint32_t src = ae.tok[t];
-            if (src >= args.rows) {
-                bad_row = true;
-                src = args.rows - 1;
-            }
-#pragma unroll
-            for (uint32_t p = 0; p < (uint32_t)NS; ++p)
-                lds_load16(args.x + p * args.x_plane + (size_t)src * K + k0 + lane * 8,
-                           lds_x + (p * ae.cnt + t) * stride + wave * 64);
-        }
-    }
-    if (bad_row && tid == 0)
-        raise_flag(args.flags, FLAG_SCHEDULE);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // the copies are the oldest loads: once all but the weight loads are done they are in LDS, and
+    // block j's MFMAs then start as soon as its weights arrive, while later blocks are in flight
+    wait_vmcnt<MATS * BPW * 2>();
 
     // 3. block partials on the MFMA, block scale in registers (as moe_a_split_kernel)
     f32x4 tot[MATS];
@@ -405,8 +408,9 @@ bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_activ
     if (args.K != 8 * 4 * 128 || args.R % 16 != 0 || (uint32_t)ns * args.cap > 8)
         return false;
     const size_t lds = fused_lds(ns, args.cap, args.K);
-    // a lone expert (the one-expert forward) takes 8 + 8-row work items: twice the workgroups
-    const bool half = args.single && args.R % 8 == 0;
+    // a lone expert (the one-expert forward) and one-row experts (a one-token batch) take 8 + 8-row
+    // work items: twice the workgroups
+    const bool half = args.R % 8 == 0 && (args.single || args.cap == 1);
     const dim3 grid(max_active * (args.R / (half ? 8 : 16))), block(512);
 #define PW_FUSED(NS, RM)                                                                                     \
     do {                                                                                                      \
@@ -452,22 +456,8 @@ __global__ __launch_bounds__(512) void moe_a_down_out_kernel(const SplitArgs arg
     const uint32_t k0 = wave * KC;
     const uint32_t row0 = blockIdx.x * 16;
 
-    // 1. this wave's weight bytes, all in flight at once, and its block scales
-    uint4 wv[BPW][2];
-    const uint8_t *wrow = ae.ep.down_w + (size_t)(row0 + r16) * K + k0 + q * 16;
-#pragma unroll
-    for (int j = 0; j < BPW; ++j)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-            wv[j][h] = load_global16(wrow + j * 128 + h * 64);
-    const uint32_t blocks = K >> 7;
-    float sc[BPW];
-#pragma unroll
-    for (int j = 0; j < BPW; ++j)
-        sc[j] = load_g(ae.ep.down_s + (row0 >> 7) * blocks + (k0 >> 7) + j);
-
-    // 2. the hidden rows (three planes, whole K) -> LDS: wave w copies its K split of every row and
-    //    plane (KC / 8 16-byte units per row, at most 64 lanes per instruction)
+    // 1. the hidden rows (three planes, whole K) -> LDS: wave w copies its K split of every row and
+    //    plane (KC / 8 16-byte units per row, at most 64 lanes per instruction) and reads only that
     constexpr uint32_t PER_SPLIT = KC / 8, LANES = PER_SPLIT < 64 ? PER_SPLIT : 64, CPS = PER_SPLIT / LANES;
     // (unrolled over the eight possible rows: a loop would make the compiler wait for every
     // outstanding weight load before its first iteration)
@@ -483,8 +473,24 @@ __global__ __launch_bounds__(512) void moe_a_down_out_kernel(const SplitArgs arg
                         lds_load16(args.x + p * args.x_plane + (size_t)t * K + k0 + (c * 64 + lane) * 8,
                                    lds_x + (p * cnt + t) * stride + (k0 >> 3) + c * 64);
         }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    asm volatile("" ::: "memory");  // the copies stay the oldest memory operations
+
+    // 2. this wave's weight bytes, all in flight at once, and its block scales
+    uint4 wv[BPW][2];
+    const uint8_t *wrow = ae.ep.down_w + (size_t)(row0 + r16) * K + k0 + q * 16;
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            wv[j][h] = load_global16(wrow + j * 128 + h * 64);
+    const uint32_t blocks = K >> 7;
+    float sc[BPW];
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+        sc[j] = load_g(ae.ep.down_s + (row0 >> 7) * blocks + (k0 >> 7) + j);
+
+    // the copies are done once all but the weight loads are; block j's MFMAs start when its weights arrive
+    wait_vmcnt<BPW * 2>();
 
     // 3. block partials on the MFMA, block scale in registers (as moe_a_split_kernel)
     f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -566,6 +572,129 @@ bool launch_moe_a_down_out(const SplitArgs &args, float *out_f32, uint16_t *out_
     } else {
         hipLaunchKernelGGL((moe_a_down_out_kernel<1>), grid, block, lds, stream, args, out_f32, out_bf16, raw ? 1u : 0u);
     }
+    return true;
+}
+
+// Down and combine of a one-token batch in one launch (the decode layer at width 1: eight routed
+// experts with one slot each). Work item: 16 output rows. Sixteen waves: wave w takes routed
+// expert w / 2 (ascending id, the schedule's order) and K half w % 2, which is exactly the split-K
+// down's work for those rows (KS = 2, eight 128-column blocks per split, the same MFMA sequence and
+// block-scale order), so each split sum is the same f32 value. The sums meet in LDS; lanes 0..15
+// of wave 0 then form each output row as the combine does: per expert in ascending id, the split
+// sums added in split order, times the route weight, added to the row in f32 without fused
+// multiply-add, then rounded to bf16. No per-placement outputs go through memory and no combine
+// launch follows.
+__global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitArgs args, const MoePlan *__restrict__ plan,
+                                                                   const float *__restrict__ placement_w,
+                                                                   float *__restrict__ out_f32,
+                                                                   uint16_t *__restrict__ out_bf16, uint32_t raw)
+{
+    constexpr int BPW = 8;
+    constexpr uint32_t KC = BPW * 128, PER_SPLIT = KC / 8, STRIDE = PER_SPLIT + 1;
+    extern __shared__ uint4 lds_x[];  // per wave [3][KC/8 + 1]; then the split sums [16 waves][16 rows]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    const uint32_t n_active = plan->n_active;
+    const uint32_t a = (uint32_t)wave >> 1, s = (uint32_t)wave & 1;
+    const uint32_t K = args.K, H = args.R;
+    const uint32_t row0 = blockIdx.x * 16;
+    float *red = (float *)(lds_x + 16 * 3 * STRIDE);  // [16 waves][16 rows]
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (a < n_active) {
+        const ActiveExpert ae = args.active[a];
+        if (ae.cnt != 1 && lane == 0)
+            raise_flag(args.flags, FLAG_SCHEDULE);
+        const uint32_t k0 = s * KC;
+        // 1. the expert's hidden row (its one slot) for this K half, three planes -> this wave's own
+        //    LDS region; then the block scales; then this wave's weight bytes (16 rows x K half), all
+        //    in flight. In that order the in-order memory counter lets the MFMAs of block j start
+        //    when block j's weights arrive, while the later blocks are still on their way.
+        uint4 *xs = lds_x + wave * 3 * STRIDE;
+        const uint32_t slot = ae.off < args.P ? ae.off : 0;
+#pragma unroll
+        for (uint32_t p = 0; p < 3; ++p)
+#pragma unroll
+            for (uint32_t c = 0; c < PER_SPLIT / 64; ++c)
+                lds_load16(args.x + p * args.x_plane + (size_t)slot * K + k0 + (c * 64 + lane) * 8,
+                           xs + p * STRIDE + c * 64);
+        asm volatile("" ::: "memory");  // the copies stay the oldest memory operations
+        const uint32_t blocks = K >> 7;
+        float sc[BPW];
+#pragma unroll
+        for (int j = 0; j < BPW; ++j)
+            sc[j] = load_g(ae.ep.down_s + (row0 >> 7) * blocks + (k0 >> 7) + j);
+        uint4 wv[BPW][2];
+        const uint8_t *wrow = ae.ep.down_w + (size_t)(row0 + r16) * K + k0 + q * 16;
+#pragma unroll
+        for (int j = 0; j < BPW; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                wv[j][h] = load_global16(wrow + j * 128 + h * 64);
+        wait_vmcnt<2 * BPW>();  // every load but the youngest 2 * BPW: this wave's copies (its own region)
+        // 2. block partials on the MFMA (token column 0; the other columns multiply zeros)
+#pragma unroll
+        for (int j = 0; j < BPW; ++j) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const bf16x8 A0 = fp8x8_to_bf16x8(wv[j][h].x, wv[j][h].y);
+                const bf16x8 A1 = fp8x8_to_bf16x8(wv[j][h].z, wv[j][h].w);
+                const uint32_t cu = j * 16 + h * 8 + q * 2;
+#pragma unroll
+                for (int p = 0; p < 3; ++p) {
+                    uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+                    if (r16 == 0) {
+                        x0 = xs[p * STRIDE + cu];
+                        x1 = xs[p * STRIDE + cu + 1];
+                    }
+                    acc = mfma_bf16_16x16x32(A0, bf16x8_from_u4(x0), acc);
+                    acc = mfma_bf16_16x16x32(A1, bf16x8_from_u4(x1), acc);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                tot[i] = __builtin_fmaf(sc[j], acc[i], tot[i]);
+        }
+        if (r16 == 0)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                red[wave * 16 + q * 4 + i] = tot[i];
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= 16)
+        return;
+    // 4. the combine for output row row0 + lane
+    float acc = 0.f;
+    for (uint32_t e = 0; e < n_active && e < 8; ++e) {
+        const float y = red[(2 * e) * 16 + lane] + red[(2 * e + 1) * 16 + lane];
+        const uint32_t slot = args.active[e].off;
+        const float w = placement_w[slot < args.P ? slot : 0];
+        acc = __fadd_rn(acc, __fmul_rn(y, w));
+    }
+    const float r = round_bf16(acc);
+    const size_t at = row0 + lane;
+    if (out_f32)
+        out_f32[at] = raw ? acc : r;
+    if (out_bf16)
+        out_bf16[at] = (uint16_t)(f32_bits(r) >> 16);
+    if (!finite_f32(r))
+        raise_flag(args.flags, FLAG_ROUND_NONFINITE);
+}
+
+bool launch_moe_a_down_combine1(const SplitArgs &args, const MoePlan *plan, const float *placement_w, float *out_f32,
+                                uint16_t *out_bf16, bool raw, hipStream_t stream)
+{
+    // the split-K down's plan at I = 2048 (two splits of eight blocks); the caller's batch is one
+    // token, so its eight placements are the rows
+    if (args.P != 8 || args.rows != 8 || args.K != 2048 || args.R % 16 != 0)
+        return false;
+    const size_t lds = (size_t)16 * 3 * (1024 / 8 + 1) * 16 + 16 * 16 * 4;
+    (void)hipFuncSetAttribute((const void *)moe_a_down_combine1_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+    hipLaunchKernelGGL(moe_a_down_combine1_kernel, dim3(args.R >> 4), dim3(1024), lds, stream, args, plan,
+                       placement_w, out_f32, out_bf16, raw ? 1u : 0u);
     return true;
 }
 
