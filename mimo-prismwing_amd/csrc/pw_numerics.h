@@ -18,17 +18,15 @@ PW_HD float f32_from(uint32_t u) { return __builtin_bit_cast(float, u); }
 PW_HD bool finite_f32_bits(float v) { return (f32_bits(v) & 0x7f800000u) != 0x7f800000u; }
 
 // f32 -> bf16 round-to-nearest-even, returned as the widened f32 value. NaNs keep their sign and
-// high payload and get the quiet bit 0x40 (src/text_endpoint.rs:2960-2971); infinities pass.
+// high payload and get the quiet bit 0x40 (src/text_endpoint.rs:2960-2971); infinities pass (the
+// rounding bias cannot carry out of a zero mantissa). Written as one select, not a branch: in
+// GPU code a branch here becomes exec-mask control flow around every call.
 PW_HD float round_bf16(float value)
 {
     const uint32_t bits = f32_bits(value);
-    if ((bits & 0x7f800000u) == 0x7f800000u) {
-        if ((bits & 0x007fffffu) == 0u)
-            return value;
-        return f32_from(((bits >> 16) | 0x0040u) << 16);
-    }
-    const uint32_t bias = 0x7fffu + ((bits >> 16) & 1u);
-    return f32_from((bits + bias) & 0xffff0000u);
+    const uint32_t rounded = (bits + 0x7fffu + ((bits >> 16) & 1u)) & 0xffff0000u;
+    const uint32_t quiet = (bits | 0x00400000u) & 0xffff0000u;
+    return f32_from((bits & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 
 PW_HD uint16_t bf16_bits(float value) { return (uint16_t)(f32_bits(round_bf16(value)) >> 16); }

@@ -161,14 +161,21 @@ def fp8_blocks_exact(q: np.ndarray, w: np.ndarray) -> bool:
     return True
 
 
+def peak_offset(e, j):
+    """Row, within hidden group j of expert e, of the closed-form layer's h = 448 entry."""
+    return (41 * e + 67 * j + 5) % 128
+
+
 def closed_form_mode_b(seed, rows, n_experts, hidden=256, inter=256, top_k=8, check=False):
     """A routed layer whose mode-B result is fixed bit for bit, whatever the summation order.
 
     Every activation group holds +-448 (so its dynamic scale is exactly 1 and the codes are the
     values), weights are e4m3 codes in [1, 2) times power-of-two block scales, and the columns that
-    hold the +-448 entries carry no weight, so every gate/up sum is exact in f32. Hidden row 128 j of
-    every expert has gate 32 and up 14 (silu(32) rounds to 32 in f32), so h = 448 there and every
-    hidden group's scale is exactly 1 too; the down weights skip those rows and hold one code per
+    hold the +-448 entries carry no weight, so every gate/up sum is exact in f32. One hidden row of
+    each 128-row group j of every expert, row 128 j + peak_offset(e, j) (spread over the whole group,
+    so a group maximum taken over part of the group gets another scale), has gate 32 and up 14
+    (silu(32) rounds to 32 in f32), so h = 448 there and every hidden group's scale is exactly 1
+    too; the down weights skip those rows and hold one code per
     128-column block (hidden codes span e4m3's range, and one product per block keeps the FP8
     MFMA's block sums exact, see fp8_blocks_exact). Gate rows whose silu
     lies within 16 f32 steps of a bf16 rounding boundary are zeroed (an exp evaluated one step
@@ -191,7 +198,7 @@ def closed_form_mode_b(seed, rows, n_experts, hidden=256, inter=256, top_k=8, ch
         us = (2.0 ** rng.integers(-5, -3, (inter // 128, hidden // 128))).astype(np.float32)
         ds = (2.0 ** rng.integers(-5, -3, (hidden // 128, inter // 128))).astype(np.float32)
         for j in range(inter // 128):
-            r = 128 * j
+            r = 128 * j + peak_offset(e, j)
             gw[r, :] = 0
             uw[r, :] = 0
             # x[:, 0] = 32: code * scale * 32 = 32 (gate) and 14 (up)
@@ -216,13 +223,14 @@ def closed_form_mode_b(seed, rows, n_experts, hidden=256, inter=256, top_k=8, ch
         silu = (g / (1.0 + np.exp(-g))).astype(np.float32)
         low = (silu.view(np.uint32) & 0xFFFF).astype(np.int64)
         near = np.any(np.abs(low - 0x8000) <= 16, axis=0)
-        near[::128] = False
+        peaks = [128 * j + peak_offset(e, j) for j in range(inter // 128)]
+        near[peaks] = False
         gw[near, :] = 0
         g = bf16_round((xs @ dequant(gw, gs).T).astype(np.float32)).astype(np.float64)
         u = bf16_round((xs @ dequant(uw, us).T).astype(np.float32)).astype(np.float32)
         h = bf16_round(bf16_round((g / (1.0 + np.exp(-g))).astype(np.float32)) * u).astype(np.float64)
         if check:
-            assert np.all(np.abs(h[:, ::128]) == 448.0) and np.all(np.abs(h) <= 448.0)
+            assert np.all(np.abs(h[:, peaks]) == 448.0) and np.all(np.abs(h) <= 448.0)
             hd = decode_table()[encode_e4m3(h)]
             assert exact_in_f32(hd, dequant(dw, ds))
             assert fp8_blocks_exact(hd, decode_table()[dw])

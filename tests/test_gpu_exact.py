@@ -233,9 +233,29 @@ def test_closed_form_mode_b_device_layer_bit_exact(rt, closed_form, rows):
 
 @pytest.mark.parametrize("rows", [1, 40, 192])
 def test_closed_form_prefill_bit_exact(rt, closed_form, rows):
-    """The grouped FP8 GEMM prefill (table silu, fused SwiGLU re-quantisation) on closed-form data,
-    up to 192 rows (128 placements per expert: two 96-slot m-tiles)."""
+    """The grouped FP8 GEMM prefill (table silu, fused SwiGLU re-quantisation, each hidden group's
+    maximum at another of its 128 rows) on closed-form data, up to 192 rows (128 placements per
+    expert: two 96-slot m-tiles)."""
     experts, x, sel, w, _, bank = closed_form
+    x, sel, w = x[:rows], sel[:rows], w[:rows]
+    want, want_raw = O.moe_layer("b", x, experts, 12, sel, w, raw=True)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW, prefill=True), want_raw)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16, prefill=True), want)
+
+
+@pytest.fixture(scope="module")
+def closed_form_odd(rt):
+    experts, x, sel, w = closed_form_mode_b(0x50570200, 96, 12, hidden=384)
+    projs, bank = _bank_from(rt, experts, 12)
+    return experts, x, sel, w, projs, bank
+
+
+@pytest.mark.parametrize("rows", [1, 96])
+def test_closed_form_prefill_odd_blocks_bit_exact(rt, closed_form_odd, rows):
+    """Hidden 384 (an odd count of 128-column blocks): the prefill's gate/up takes one-block K
+    steps with 128-row tiles (hidden 256 takes two-block steps with 256-row tiles); bit for bit the
+    oracle's layer."""
+    experts, x, sel, w, _, bank = closed_form_odd
     x, sel, w = x[:rows], sel[:rows], w[:rows]
     want, want_raw = O.moe_layer("b", x, experts, 12, sel, w, raw=True)
     _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW, prefill=True), want_raw)

@@ -49,3 +49,11 @@ def test_closed_form_layer_data_meets_its_preconditions():
     experts, x, sel, w = closed_form_mode_b(0x50570100, 192, 12, check=True)
     out = O.moe_layer("b", x[:8], experts, 12, sel[:8], w[:8])
     assert np.all(np.isfinite(out)) and np.any(out)
+
+
+def test_closed_form_odd_hidden_blocks_meets_its_preconditions():
+    """The hidden-384 closed form (three 128-column blocks: the prefill's one-block K steps and its
+    separate SwiGLU kernel) at the GPU test's seed and size."""
+    experts, x, sel, w = closed_form_mode_b(0x50570200, 96, 12, hidden=384, check=True)
+    out = O.moe_layer("b", x[:4], experts, 12, sel[:4], w[:4])
+    assert np.all(np.isfinite(out)) and np.any(out)
