@@ -182,7 +182,7 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
     return {"layer_us": round(ms * 1000, 2), "TFLOP/s": round(tflops, 1),
             "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
             "weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1), "unique_experts": u,
-            "max_count": int(counts.max()), "m_tiles_96": int(np.sum((counts + 95) // 96)),
+            "max_count": int(counts.max()), "m_tiles_128": int(np.sum((counts + 127) // 128)),
             "top_counts": sorted(counts.tolist(), reverse=True)[:8],
             "count_quartiles": [int(v) for v in np.percentile(counts, [0, 25, 50, 75, 100])], "kernels_us": kt}
 

@@ -12,9 +12,11 @@
 // v_mfma_scale_f32_16x16x128_f8f6f4 (unit E8M0 scales) forms each block's FP8 products; the two
 // scales are multiplied together and applied in f32, sequentially over b.
 //
-// Tiles: (96 placement slots of one routed expert = an m-tile) x (256 weight rows = an n-tile);
-// 96 slots hold a whole expert's placements at the uniform-routing count (64 on average), so its
-// weights stream once, and 16-token MFMA tiles past the m-tile's placements are skipped. Gate and
+// Tiles: (128 placement slots of one routed expert = an m-tile) x (256 weight rows = an n-tile);
+// 128 slots hold a whole expert's placements at the uniform-routing count (64 on average, 93 at
+// most for 2048 tokens), so its weights stream once, and a skewed routing's busiest experts need
+// few m-tiles (each of which streams the expert's weights again); 16-token MFMA tiles past the
+// m-tile's placements are skipped. Gate and
 // up run as one stacked projection (2I output columns per slot), then a SwiGLU + re-quantisation
 // kernel, then down. A workgroup walks K in 256-column steps with two kinds of waves, so the two
 // streams never wait on each other in the in-order memory counter: eight consumer waves (32 weight
@@ -34,8 +36,11 @@
 
 namespace pw {
 
-constexpr uint32_t PF_MT = 96;                    // placement slots per m-tile
+// Against 96-slot m-tiles, 2048 tokens: uniform routing unchanged (256 m-tiles either way), Zipf
+// routing 341 -> 311 m-tiles, layer 1693 -> 1595 us.
+constexpr uint32_t PF_MT = 128;                   // placement slots per m-tile
 constexpr int PF_TT = (int)PF_MT / 16;            // 16-token MFMA tiles per m-tile
+static_assert(PF_MT % 16 == 0 && PF_MT > 64 && PF_MT <= 128, "two 64-slot token lanes cover an m-tile");
 constexpr uint32_t PF_UNITS = 8;                  // 16-byte units per 128-byte token row of a step
 constexpr int PF_CONS = 8;                        // consumer waves per workgroup, 16 weight rows each
 constexpr int PF_PROD = 1;                        // producer waves per workgroup (the codes ring)
@@ -53,8 +58,9 @@ struct PfCfg {
     static constexpr int RG = RG_;                         // 16-row groups per consumer wave
     static constexpr uint32_t NROWS = 16 * RG * PF_CONS;   // weight rows per n-tile
     static constexpr uint32_t NSB = (NROWS + 127) / 128;   // 128-row weight scale blocks per n-tile
-    // two row groups hold twice the weight registers: one workgroup per CU (three waves per SIMD)
-    static constexpr int WAVES_PER_EU = RG == 1 ? 5 : 3;
+    // two row groups hold twice the weight registers: one workgroup per CU (three waves per SIMD);
+    // one row group fits five waves per SIMD with up to six 16-token tiles, four with more
+    static constexpr int WAVES_PER_EU = RG == 1 ? (PF_TT > 6 ? 4 : 5) : 3;
     static constexpr int G = WS > D ? WS : D;              // steps per unrolled group
     static constexpr uint32_t STEP = SB * PF_BLK;          // 16-byte code units per step
     static_assert(G % WS == 0 && G % D == 0, "ring sizes divide the unrolled group");
@@ -67,7 +73,7 @@ struct PfCfg {
 using PfWide = PfCfg<2, 2, 2, 2>;
 using PfNarrow = PfCfg<1, 4, 4, 1>;
 
-// Tile table: ceil(count / 96) m-tiles per routed expert, ascending expert order. One workgroup of
+// Tile table: ceil(count / 128) m-tiles per routed expert, ascending expert order. One workgroup of
 // 1024 threads, one thread per schedule entry (banks hold at most 1024 experts).
 __global__ __launch_bounds__(1024) void prefill_tiles_kernel(const MoePlan *__restrict__ plan,
                                                              const ActiveExpert *__restrict__ active,
@@ -198,7 +204,7 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[C::RG][NT], PfW<C> &w, c
 // What the producer and consumer waves of one tile share (set up by prefill_b_kernel).
 struct PfTile {
     uint4 *ring;               // [D][STEP] code units, swizzled
-    const float *lds_scale;    // [blocks][96] activation scales
+    const float *lds_scale;    // [blocks][PF_MT] activation scales
     const float *lds_wscale;   // this wave's [blocks] weight block scales
     const uint8_t *wrow;       // this lane's weight row at its column offset (consumers)
     uint16_t *out;             // this lane's first output: slot0 row, column col0 + wave * 16 RG + 4q
@@ -318,7 +324,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
     const uint32_t K = args.K, blocks = K >> 7;
     const uint32_t nsteps = blocks / C::SB;  // the launcher checks blocks % SB
     uint4 *ring = lds_pf;                                   // [D][STEP] code units, swizzled
-    float *lds_scale = (float *)(ring + C::D * C::STEP);    // [blocks][96] activation scales
+    float *lds_scale = (float *)(ring + C::D * C::STEP);    // [blocks][PF_MT] activation scales
     float *lds_wscale = lds_scale + blocks * PF_MT;       // [NSB][blocks] weight block scales
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -342,13 +348,13 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
     const uint32_t slot0 = ae.off + m0;
     const bool gather = args.placement_pos != nullptr;
 
-    // token rows of the m-tile's slots (lane: slots lane and 64 + lane, the second only below 96;
+    // token rows of the m-tile's slots (lane: slots lane and 64 + lane, the second only below PF_MT;
     // slots past the tile's count repeat its last slot: in-bounds loads whose output columns are
     // never stored)
     uint32_t tok[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const uint32_t t = 64 * h + (h ? lane & 31 : lane);
+        const uint32_t t = 64 * h + (h ? (uint32_t)lane % (PF_MT - 64) : (uint32_t)lane);
         tok[h] = slot0 + (t < cnt_t ? t : cnt_t - 1);
         if (gather)
             tok[h] = load_g(args.placement_pos + tok[h]);
@@ -371,8 +377,8 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
         return col >= args.R ? 0u : (col >= args.R1 ? col - args.R1 : col);
     };
     // weight block scales of the n-tile's 128-row blocks ([NSB][blocks]) and the m-tile's
-    // activation scales, transposed (lds_scale[b * 96 + t]) with 4-byte direct-to-LDS loads (lane =
-    // token; a second instruction covers tokens 64..95), spread over all waves
+    // activation scales, transposed (lds_scale[b * PF_MT + t]) with 4-byte direct-to-LDS loads (lane =
+    // token; a second instruction covers tokens 64 .. PF_MT - 1), spread over all waves
     if ((uint32_t)tid < C::NSB * blocks) {
         const uint32_t hb = (uint32_t)tid / blocks, b = (uint32_t)tid - hb * blocks;
         const uint32_t col = col0 + 128 * hb;
@@ -404,6 +410,8 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
     case 3: pf_body<C, 3>(tile, tok, args.codes, K, wave, lane); break;
     case 4: pf_body<C, 4>(tile, tok, args.codes, K, wave, lane); break;
     case 5: pf_body<C, 5>(tile, tok, args.codes, K, wave, lane); break;
+    case 6: pf_body<C, (PF_TT > 6 ? 6 : PF_TT)>(tile, tok, args.codes, K, wave, lane); break;
+    case 7: pf_body<C, (PF_TT > 7 ? 7 : PF_TT)>(tile, tok, args.codes, K, wave, lane); break;
     default: pf_body<C, PF_TT>(tile, tok, args.codes, K, wave, lane); break;
     }
 }

@@ -203,7 +203,7 @@ def _device_layer(rt, bank, x, sel, w, out_dtype, prefill=False):
 
 @pytest.fixture(scope="module")
 def closed_form(rt):
-    experts, x, sel, w = closed_form_mode_b(0x50570100, 192, 12)
+    experts, x, sel, w = closed_form_mode_b(0x50570100, 256, 12)
     projs, bank = _bank_from(rt, experts, 12)
     return experts, x, sel, w, projs, bank
 
@@ -231,11 +231,12 @@ def test_closed_form_mode_b_device_layer_bit_exact(rt, closed_form, rows):
     _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16), want)
 
 
-@pytest.mark.parametrize("rows", [1, 40, 192])
+@pytest.mark.parametrize("rows", [1, 40, 192, 256])
 def test_closed_form_prefill_bit_exact(rt, closed_form, rows):
     """The grouped FP8 GEMM prefill (table silu, fused SwiGLU re-quantisation, each hidden group's
-    maximum at another of its 128 rows) on closed-form data, up to 192 rows (128 placements per
-    expert: two 96-slot m-tiles)."""
+    maximum at another of its 128 rows) on closed-form data, up to 256 rows (117 to 141 placements
+    per expert at 192 rows: one full 128-slot m-tile or a second with a few slots; 152 to 187 at
+    256 rows: two m-tiles each)."""
     experts, x, sel, w, _, bank = closed_form
     x, sel, w = x[:rows], sel[:rows], w[:rows]
     want, want_raw = O.moe_layer("b", x, experts, 12, sel, w, raw=True)

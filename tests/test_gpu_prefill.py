@@ -68,10 +68,10 @@ def small_bank(rt):
     return _SmallBank(rt, 16, 256, 128, WL.SEED_BASE + 40)
 
 
-@pytest.mark.parametrize("rows", [1, 7, 64, 200])
+@pytest.mark.parametrize("rows", [1, 7, 64, 200, 300])
 def test_prefill_matches_oracle(rt, small_bank, rows):
-    """Random top-8 of 16 experts: 8 * rows / 16 placements per expert (up to 100 at 200 rows: two
-    96-slot m-tiles)."""
+    """Random top-8 of 16 experts: 8 * rows / 16 placements per expert (100 at 200 rows: one 128-slot
+    m-tile with seven 16-token tiles; 150 at 300 rows: two m-tiles)."""
     import torch
     rng = np.random.default_rng(100 + rows)
     x = WL.activations(rows, WL.SEED_BASE + 50 + rows, hidden=256)
@@ -83,8 +83,8 @@ def test_prefill_matches_oracle(rt, small_bank, rows):
 
 
 def test_prefill_skewed_routes_f32_input(rt, small_bank):
-    """Every token on the same eight experts (count = rows = 300: four 96-slot m-tiles each), f32
-    input."""
+    """Every token on the same eight experts (count = rows = 300: three 128-slot m-tiles each, the
+    last one partial), f32 input."""
     import torch
     rows = 300
     rng = np.random.default_rng(7)

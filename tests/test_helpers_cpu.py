@@ -46,7 +46,7 @@ def test_closed_form_layer_data_meets_its_preconditions():
     """The closed-form mode-B data the GPU tests use (seed and size as there): every gate, up and
     down sum is exact in f32 in any order and inside the FP8 MFMA window, hidden groups have
     absmax 448, and the oracle's layer runs on it."""
-    experts, x, sel, w = closed_form_mode_b(0x50570100, 192, 12, check=True)
+    experts, x, sel, w = closed_form_mode_b(0x50570100, 256, 12, check=True)
     out = O.moe_layer("b", x[:8], experts, 12, sel[:8], w[:8])
     assert np.all(np.isfinite(out)) and np.any(out)
 
