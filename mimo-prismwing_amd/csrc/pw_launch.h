@@ -179,8 +179,18 @@ void launch_router(const void *x, bool x_f32, const void *w, bool w_f32, const f
                    uint32_t *flags, hipStream_t stream);
 
 // Routed-MoE prefill (mode B grouped block-FP8 GEMM, pw_prefill.hip) after launch_moe_schedule.
+// One m-tile of the prefill's grouped GEMM (up to 128 placement slots of one routed expert): the
+// expert's weights and the tile's slots, so a GEMM workgroup finds its operands in one load.
+struct PfTileDesc {
+    ExpertPtrs ep;
+    uint32_t slot0;  // first placement slot
+    uint32_t cnt;    // placement slots of the tile
+    uint32_t pad[2];
+};
+static_assert(sizeof(PfTileDesc) == 64, "a tile descriptor is one 64-byte scalar load");
+
 struct PrefillBuffers {
-    uint2 *tiles;       // [prefill_max_tiles] (schedule entry, first slot of a 96-slot m-tile)
+    PfTileDesc *tiles;  // [prefill_max_tiles]
     uint32_t *n_tiles;  // [1]
     uint16_t *hidden;   // [rows * 8][2I] bf16 gate and up outputs
     uint16_t *y;        // [rows * 8][H] bf16 expert outputs

@@ -39,14 +39,17 @@ namespace pw {
 // Against 96-slot m-tiles, 2048 tokens: uniform routing unchanged (256 m-tiles either way), Zipf
 // routing 341 -> 311 m-tiles, layer 1693 -> 1595 us.
 constexpr uint32_t PF_MT = 128;                   // placement slots per m-tile
+// n-tiles per workgroup, where they divide evenly. Consecutive n-tiles share the workgroup's
+// set-up and run the weight stream on across n-tiles, but put more m-tiles' activation codes in an
+// XCD's L2 at once (32 CUs / (n-tiles per m-tile / PF_NSUB) m-tiles): the down projection's codes
+// (128 slots x I bytes) take four, the gate/up projection's (128 token rows x H bytes) one.
+constexpr uint32_t PF_NSUB_GATEUP = 1, PF_NSUB_DOWN = 4;
 constexpr int PF_TT = (int)PF_MT / 16;            // 16-token MFMA tiles per m-tile
 static_assert(PF_MT % 16 == 0 && PF_MT > 64 && PF_MT <= 128, "two 64-slot token lanes cover an m-tile");
 constexpr uint32_t PF_UNITS = 8;                  // 16-byte units per 128-byte token row of a step
-constexpr int PF_CONS = 8;                        // consumer waves per workgroup, 16 weight rows each
-constexpr int PF_PROD = 1;                        // producer waves per workgroup (the codes ring)
-constexpr int PF_WAVES = PF_CONS + PF_PROD;
+constexpr int PF_CONS = 8;                        // consumer waves per workgroup, 16 RG weight rows each
+constexpr int PF_WAVES = PF_CONS + 1;             // and one producer wave (the codes ring)
 constexpr uint32_t PF_BLK = PF_MT * PF_UNITS;     // 16-byte code units per 128-column block
-constexpr int PF_DMA = (int)(PF_BLK / 64);        // producer copy instructions per block
 static_assert(PF_BLK % 64 == 0, "a block's codes are whole 64-lane copies");
 
 // K-step shape: SB 128-column blocks per step, WS weight steps in flight per consumer lane, D code
@@ -73,24 +76,35 @@ struct PfCfg {
 using PfWide = PfCfg<2, 2, 2, 2>;
 using PfNarrow = PfCfg<1, 4, 4, 1>;
 
-// Tile table: ceil(count / 128) m-tiles per routed expert, ascending expert order. One workgroup of
-// 1024 threads, one thread per schedule entry (banks hold at most 1024 experts).
+// Tile table: ceil(count / 128) m-tiles per routed expert, ascending expert order, each with its
+// expert's weights and its slots. One workgroup of 1024 threads, one thread per schedule entry
+// (banks hold at most 1024 experts).
 __global__ __launch_bounds__(1024) void prefill_tiles_kernel(const MoePlan *__restrict__ plan,
                                                              const ActiveExpert *__restrict__ active,
-                                                             uint32_t max_active, uint2 *__restrict__ tiles,
+                                                             uint32_t max_active, PfTileDesc *__restrict__ tiles,
                                                              uint32_t max_tiles, uint32_t *__restrict__ n_tiles,
                                                              uint32_t *flags)
 {
     __shared__ uint32_t s_scan[48];
     const uint32_t a = threadIdx.x;
     const uint32_t n_active = plan->n_active;
-    const uint32_t cnt = (a < max_active && a < n_active) ? active[a].cnt : 0u;
+    const bool live = a < max_active && a < n_active;
+    const uint32_t cnt = live ? active[a].cnt : 0u;
     const uint32_t nt = (cnt + PF_MT - 1) / PF_MT;
     uint32_t total;
     const uint32_t off = block_exclusive_scan(nt, s_scan, &total);
-    for (uint32_t i = 0; i < nt; ++i)
-        if (off + i < max_tiles)
-            tiles[off + i] = make_uint2(a, i * PF_MT);
+    if (live) {
+        const ActiveExpert ae = active[a];
+        for (uint32_t i = 0; i < nt; ++i)
+            if (off + i < max_tiles) {
+                PfTileDesc td;
+                td.ep = ae.ep;
+                td.slot0 = ae.off + i * PF_MT;
+                td.cnt = cnt - i * PF_MT < PF_MT ? cnt - i * PF_MT : PF_MT;
+                td.pad[0] = td.pad[1] = 0;
+                tiles[off + i] = td;
+            }
+    }
     if (a == 0) {
         n_tiles[0] = total < max_tiles ? total : max_tiles;
         if (total > max_tiles)
@@ -99,8 +113,7 @@ __global__ __launch_bounds__(1024) void prefill_tiles_kernel(const MoePlan *__re
 }
 
 struct PrefillArgs {
-    const ActiveExpert *active;
-    const uint2 *tiles;             // [max_tiles] (schedule entry, first slot of the m-tile)
+    const PfTileDesc *tiles;        // [max_tiles]
     const uint32_t *n_tiles;
     const uint32_t *placement_pos;  // gate/up: token row of each placement slot (down: null)
     const uint8_t *codes;           // activation codes [rows][K] (down: rows = placement slots)
@@ -109,6 +122,7 @@ struct PrefillArgs {
     uint32_t R;                     // output columns per slot: 2I (gate then up) or H
     uint32_t R1;                    // rows of the first matrix (gate/up: I; down: H)
     uint32_t rows, max_tiles;
+    uint32_t n_sub;                 // consecutive n-tiles per workgroup (divides the n-tile count)
     uint16_t *out;                  // [P][R] bf16
     uint32_t *flags;
 };
@@ -123,47 +137,30 @@ struct PfW {
     uint4 v[C::RG][2 * C::SB];
 };
 
-// wrow: the lane's row of the wave's first 16-row group; group g is 16 g rows further (rstride =
-// 16 K bytes)
+// src: the wave's first weight row at the step's first column (wave-uniform); loff: the lane's row
+// and column offset (r16 rows, 16 q columns); group g is 16 g rows further (rstride = 16 K bytes)
 template <class C>
-__device__ __forceinline__ void pf_issue_w(PfW<C> &w, const uint8_t *wrow, size_t rstride, uint32_t k0)
+__device__ __forceinline__ void pf_issue_w(PfW<C> &w, const uint8_t *src, uint32_t loff, size_t rstride)
 {
 #pragma unroll
     for (int g = 0; g < C::RG; ++g)
 #pragma unroll
         for (int h = 0; h < C::SB; ++h) {
-            w.v[g][2 * h] = load_global16(wrow + g * rstride + k0 + 128 * h);
-            w.v[g][2 * h + 1] = load_global16(wrow + g * rstride + k0 + 128 * h + 64);
-        }
-}
-
-// The producer's copy of one step's codes into a ring slot (one block after another): instruction
-// c of a block covers tokens 8c .. 8c + 7; lane i reads global unit (i % 8) ^ (token % 8) of token
-// 8c + i / 8 and lands at LDS unit 64c + i (unit i % 8 of that token). Only the NT 16-token tiles
-// that hold placements are copied.
-template <class C, int NT>
-__device__ __forceinline__ void pf_copy_codes(uint4 *slot, const uint8_t *const *csrc, uint32_t k0, int p)
-{
-    constexpr int NC = (2 * NT + PF_PROD - 1) / PF_PROD;
-#pragma unroll
-    for (int h = 0; h < C::SB; ++h)
-#pragma unroll
-        for (int i = 0; i < NC; ++i) {  // this producer's token groups of the NT active 16-token tiles
-            const int c = p + i * PF_PROD < 2 * NT ? p + i * PF_PROD : p;
-            lds_load16(csrc[i] + k0 + 128 * h, slot + h * PF_BLK + c * 64);
+            w.v[g][2 * h] = load_global16(src + g * rstride + 128 * h + loff);
+            w.v[g][2 * h + 1] = load_global16(src + g * rstride + 128 * h + 64 + loff);
         }
 }
 
 // One step: its blocks in ascending order, each block's FP8 products from one MFMA per active
 // 16-token tile, then tot += p * (S_w * a) in f32 (the two scales multiplied once per token and
-// block, four fused multiply-adds per tile). Each block's weight registers are refilled from column
-// knext (the step WS ahead) as soon as its MFMAs have read them, half a step earlier than a refill
-// of the whole step. cl0 / cl1: the lane's two code units of token r16 in a block (tile j adds
-// 16 tokens = 128 units).
+// block, four fused multiply-adds per tile). Each block's weight registers are refilled from next
+// (the wave's rows at the step WS ahead, possibly of the workgroup's next n-tile) as soon as its
+// MFMAs have read them, half a step earlier than a refill of the whole step. cl0 / cl1: the lane's
+// two code units of token r16 in a block (tile j adds 16 tokens = 128 units).
 template <class C, int NT>
 __device__ __forceinline__ void pf_compute(f32x4 (&tot)[C::RG][NT], PfW<C> &w, const uint4 *slot,
                                            const float *lds_scale, const float *lds_wscale, uint32_t k, int r16,
-                                           const uint8_t *wrow, size_t rstride, uint32_t knext, uint32_t cl0,
+                                           const uint8_t *next, uint32_t loff, size_t rstride, uint32_t cl0,
                                            uint32_t cl1)
 {
 #pragma unroll
@@ -195,128 +192,208 @@ __device__ __forceinline__ void pf_compute(f32x4 (&tot)[C::RG][NT], PfW<C> &w, c
         }
 #pragma unroll
         for (int g = 0; g < C::RG; ++g) {
-            w.v[g][2 * h] = load_global16(wrow + g * rstride + knext + 128 * h);
-            w.v[g][2 * h + 1] = load_global16(wrow + g * rstride + knext + 128 * h + 64);
+            w.v[g][2 * h] = load_global16(next + g * rstride + 128 * h + loff);
+            w.v[g][2 * h + 1] = load_global16(next + g * rstride + 128 * h + 64 + loff);
         }
     }
 }
 
-// What the producer and consumer waves of one tile share (set up by prefill_b_kernel).
+// What the producer and consumer waves of one workgroup share (set up by prefill_b_kernel): one
+// m-tile and n_sub consecutive n-tiles, run one after another.
 struct PfTile {
     uint4 *ring;               // [D][STEP] code units, swizzled
     const float *lds_scale;    // [blocks][PF_MT] activation scales
-    const float *lds_wscale;   // this wave's [blocks] weight block scales
-    const uint8_t *wrow;       // this lane's weight row at its column offset (consumers)
-    uint16_t *out;             // this lane's first output: slot0 row, column col0 + wave * 16 RG + 4q
-    uint32_t R, nsteps;
-    uint32_t store_t;          // tokens whose outputs this wave stores (0: rows past R)
+    const float *lds_wscale;   // [n_sub * NSB][blocks] weight block scales of the n-tiles' 128-row blocks
+    const uint8_t *mat0, *mat1; // output columns [0, R1): rows of mat0 (gate or down), [R1, R): mat1 (up)
+    uint16_t *out;             // the wave's first output: slot0 row, column col0 + wave * 16 RG
+    uint32_t K, R, R1, nsteps, n_sub;
+    uint32_t wcol;             // the wave's first output column in the first n-tile
+    uint32_t loff;             // the lane's weight offset: r16 rows and 16 q columns
+    uint32_t cnt;              // placement slots of the m-tile
+    const uint8_t *codes;      // activation codes [rows][K] (the producer's)
+    uint32_t *lds_tok;         // [PF_MT] token rows of the m-tile's slots, written by the producer
 };
 
-// The K loop of one tile over NT active 16-token tiles: the producer wave keeps the codes ring
-// filled, the consumer waves run the MFMAs and write the bf16 outputs.
-template <class C, int NT>
-__device__ __forceinline__ void pf_body(const PfTile &tl, const uint32_t (&tok)[2], const uint8_t *codes, uint32_t K,
-                                        int wave, int lane)
+// Wave-uniform address of the wave's first weight row in n-tile sub: column wcol + sub * NROWS is
+// row col - R1 of mat1 when col >= R1, else row col of mat0 (columns past R, of a partial last
+// n-tile, read row 0 and are never stored).
+template <class C>
+__device__ __forceinline__ const uint8_t *pf_wave_rows(const PfTile &tl, uint32_t sub)
 {
-    const uint32_t nsteps = tl.nsteps, last = nsteps - 1;
-    const int q = lane >> 4, r16 = lane & 15;
+    const uint32_t col = tl.wcol + sub * C::NROWS;
+    const uint32_t row = col >= tl.R ? 0u : (col >= tl.R1 ? col - tl.R1 : col);
+    return (col >= tl.R1 && col < tl.R ? tl.mat1 : tl.mat0) + (size_t)row * tl.K;
+}
+
+// Waits until at most (C::D - 2) steps of copies (2 nt token groups per block) are outstanding.
+template <class C>
+__device__ __forceinline__ void pf_wait_copies(uint32_t nt)
+{
+    if constexpr (C::D == 2) {
+        wait_vmcnt<0>();
+    } else {
+        static_assert((C::D - 2) * 2 * PF_TT * C::SB < 64, "vmcnt has six bits");
+        switch (nt) {
+        case 1: wait_vmcnt<(C::D - 2) * 2 * 1 * C::SB>(); break;
+        case 2: wait_vmcnt<(C::D - 2) * 2 * 2 * C::SB>(); break;
+        case 3: wait_vmcnt<(C::D - 2) * 2 * 3 * C::SB>(); break;
+        case 4: wait_vmcnt<(C::D - 2) * 2 * 4 * C::SB>(); break;
+        case 5: wait_vmcnt<(C::D - 2) * 2 * 5 * C::SB>(); break;
+        case 6: wait_vmcnt<(C::D - 2) * 2 * 6 * C::SB>(); break;
+        case 7: wait_vmcnt<(C::D - 2) * 2 * 7 * C::SB>(); break;
+        default: wait_vmcnt<(C::D - 2) * 2 * PF_TT * C::SB>(); break;
+        }
+    }
+}
+
+// The producer wave: the codes ring over the workgroup's n-tiles (the m-tile's codes again for
+// every n-tile), the nt active 16-token tiles' codes of each step. Step k's copy of block h covers
+// token groups c = 0 .. 2 nt - 1 of 8 tokens: lane i reads global unit (i % 8) ^ (token % 8) of
+// token 8c + i / 8 (its row from the token rows tok, lane t of tok[0] or tok[1]) and lands at LDS
+// unit 64c + i (unit i % 8 of that token).
+template <class C>
+__device__ __forceinline__ void pf_produce(const PfTile &tl, const uint32_t (&tok)[2], uint32_t nt, int lane)
+{
+    const uint32_t K = tl.K, nsteps = tl.nsteps;
+    const uint32_t nc = 2 * nt;
+    const uint32_t unit = (((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7) * 16;
+    // global steps k = 0 .. n_sub * nsteps - 1 (column step k % nsteps), indices clamped to the
+    // last step
+    const uint32_t total = tl.n_sub * nsteps, tlast = total - 1;
+    const auto copy_step = [&](uint32_t s) {
+        uint4 *slot = tl.ring + (s % C::D) * C::STEP;
+        const uint32_t k0 = ((s < tlast ? s : tlast) % nsteps) * (128 * C::SB);
+        for (uint32_t c = 0; c < nc; ++c) {
+            const uint32_t t = 8 * c + ((uint32_t)lane >> 3);
+            const uint32_t row = __shfl(c < 8 ? tok[0] : tok[1], (int)(t & 63), 64);
+            const uint8_t *src = tl.codes + (size_t)row * K + unit + k0;
+#pragma unroll
+            for (int h = 0; h < C::SB; ++h)
+                lds_load16(src + 128 * h, slot + h * PF_BLK + c * 64);
+        }
+    };
+    // steps 0 .. C::D - 2 into slots 0 .. C::D - 2
+    for (uint32_t s = 0; s + 1 < (uint32_t)C::D; ++s)
+        copy_step(s);
+    for (uint32_t k = 0; k < total; ++k) {
+        // step k's copy (and every older one) is complete; C::D - 2 younger steps stay in flight
+        pf_wait_copies<C>(nt);
+        lds_barrier();  // publishes slot k % C::D; every consumer is done with step k - 1
+        copy_step(k + C::D - 1);
+    }
+    wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
+}
+
+// One workgroup's waves over NT active 16-token tiles. The producer wave takes its token rows
+// back from LDS (it stored them there itself), so they are not held in registers through the
+// consumers' code. The consumer waves run the K loops of the workgroup's n-tiles, the MFMAs and
+// each n-tile's bf16 outputs; the last WS steps of an n-tile load the next n-tile's first weight
+// steps, so the weight stream runs on across n-tiles.
+template <class C, int NT>
+__device__ __forceinline__ void pf_body(const PfTile &tl, int wave, int lane)
+{
     if (wave >= PF_CONS) {
-        // ---- producers: the codes ring, producer p copying the token groups c = p, p + PF_PROD, ...
-        // of every block. Per-lane sources of the step's copy instructions.
-        constexpr int NC = (2 * NT + PF_PROD - 1) / PF_PROD;  // copy instructions per block
-        const int p = wave - PF_CONS;
-        const uint8_t *csrc[NC];
-        const uint32_t g = ((uint32_t)lane ^ ((uint32_t)lane >> 3)) & 7;
-#pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            const int c = p + i * PF_PROD < 2 * NT ? p + i * PF_PROD : p;  // unused slots repeat group p
-            const uint32_t t = 8 * c + (lane >> 3);
-            const uint32_t r0 = __shfl(tok[0], (int)(t & 63), 64), r1 = __shfl(tok[1], (int)(t & 63), 64);
-            csrc[i] = codes + (size_t)(t < 64 ? r0 : r1) * K + g * 16;
-        }
-        // steps 0 .. C::D - 2 into slots 0 .. C::D - 2 (indices clamped to the last step)
-#pragma unroll
-        for (int s = 0; s < C::D - 1; ++s)
-            pf_copy_codes<C, NT>(tl.ring + s * C::STEP, csrc, ((uint32_t)s < last ? (uint32_t)s : last) * (128 * C::SB), p);
-        for (uint32_t k = 0; k < nsteps; ++k) {
-            // step k's copy (and every older one) is complete; C::D - 2 younger steps stay in flight
-            wait_vmcnt<(C::D - 2) * NC * C::SB>();
-            lds_barrier();  // publishes slot k % C::D; every consumer is done with step k - 1
-            const uint32_t s = k + C::D - 1;
-            pf_copy_codes<C, NT>(tl.ring + (s % C::D) * C::STEP, csrc, (s < last ? s : last) * (128 * C::SB), p);
-        }
-        wait_vmcnt<0>();  // no copy may land in LDS after the workgroup ends
+        asm volatile("" ::: "memory");
+        const uint32_t tok[2] = {tl.lds_tok[lane], tl.lds_tok[64 + lane]};
+        pf_produce<C>(tl, tok, NT, lane);
         return;
     }
-
-    // ---- consumers: 16 weight rows each, the weight ring in registers
-    const uint8_t *wrow = tl.wrow;
+    const uint32_t K = tl.K, nsteps = tl.nsteps, last = nsteps - 1;
+    const int q = lane >> 4, r16 = lane & 15;
     const size_t rstride = (size_t)16 * K;
+    const uint32_t loff = tl.loff;
+    const uint32_t lane_out = (uint32_t)r16 * tl.R + 4 * (uint32_t)q;  // the lane's output offset
+    const uint8_t *rows = pf_wave_rows<C>(tl, 0);
     PfW<C> w[C::WS];
 #pragma unroll
     for (int i = 0; i < C::WS; ++i)
-        pf_issue_w<C>(w[i], wrow, rstride, ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB));
+        pf_issue_w<C>(w[i], rows + ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB), loff, rstride);
     // the lane's code units of token r16 in a block: units q and q + 4, swizzled by token % 8 (the
     // same for token r16 + 16 j); opaque to the compiler, which would otherwise fold the tile
     // offsets into one address register per tile and half instead of immediate offsets
     uint32_t cl0 = (uint32_t)r16 * PF_UNITS + ((uint32_t)q ^ ((uint32_t)r16 & 7u));
     uint32_t cl1 = (uint32_t)r16 * PF_UNITS + (((uint32_t)q + 4u) ^ ((uint32_t)r16 & 7u));
     asm volatile("" : "+v"(cl0), "+v"(cl1));
-    f32x4 tot[C::RG][NT];
-#pragma unroll
-    for (int g = 0; g < C::RG; ++g)
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-            tot[g][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // this wave's scale copies (issued before the weights) are complete before the first barrier
+    // this wave's activation scale copies (issued before the weights) are complete before the
+    // first barrier publishes them
     wait_vmcnt<2 * C::SB * C::WS * C::RG>();
 
-    // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each block's
-    // registers reloaded with step k + C::WS's block right after use. Whole groups of C::G steps
-    // run without early exits (static ring indices, one loop state at the loop head); the last
-    // steps are peeled. Load indices are clamped to the last step (the tail reloads it: cache
-    // hits), keeping every load unconditional.
-    const uint32_t nfull = nsteps - nsteps % C::G;
-    for (uint32_t b = 0; b < nfull; b += C::G) {
+    const uint32_t blocks = K >> 7;
+    for (uint32_t sub = 0; sub < tl.n_sub; ++sub) {
+        // the next n-tile's rows (this one's for the last n-tile: the tail reloads its last step,
+        // cache hits, keeping every load unconditional)
+        const bool more = sub + 1 < tl.n_sub;
+        const uint8_t *nrows = more ? pf_wave_rows<C>(tl, sub + 1) : rows;
+        const float *wsc = tl.lds_wscale + ((sub * C::NROWS + (uint32_t)wave * 16 * C::RG) >> 7) * blocks;
+        f32x4 tot[C::RG][NT];
 #pragma unroll
-        for (int i = 0; i < C::G; ++i) {
-            const uint32_t k = b + i;
-            lds_barrier();
-            pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, tl.lds_wscale, k,
-                              r16, wrow, rstride, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
-        }
-    }
+        for (int g = 0; g < C::RG; ++g)
 #pragma unroll
-    for (int i = 0; i < C::G - 1; ++i) {
-        const uint32_t k = nfull + i;
-        if (k >= nsteps)
-            break;
-        lds_barrier();
-        pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, tl.lds_wscale, k, r16,
-                          wrow, rstride, (k + C::WS < last ? k + C::WS : last) * (128 * C::SB), cl0, cl1);
-    }
+            for (int j = 0; j < NT; ++j)
+                tot[g][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // weights of step kk: this n-tile's, or past its last step the next n-tile's first ones
+        const auto next_src = [&](uint32_t k) {
+            const uint32_t kk = k + C::WS;
+            return kk <= last ? rows + kk * (128 * C::SB)
+                              : (more ? nrows + (kk - nsteps) * (128 * C::SB) : rows + last * (128 * C::SB));
+        };
 
-    // epilogue: lane holds rows 16 g + 4q + i of the wave's 16 RG for tokens 16j + r16 -> bf16
+        // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each
+        // block's registers reloaded with step k + C::WS's block right after use. Whole groups of
+        // C::G steps run without early exits (static ring indices, one loop state at the loop
+        // head); the last steps are peeled (one n-tile per workgroup: the launcher gives several
+        // only where the steps are whole groups, so every n-tile starts at ring slot 0).
+        const uint32_t nfull = nsteps - nsteps % C::G;
+        for (uint32_t b = 0; b < nfull; b += C::G) {
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const uint32_t t = 16 * j + r16;
-        if (t >= tl.store_t)
-            continue;
-#pragma unroll
-        for (int g = 0; g < C::RG; ++g) {
-            uint16_t o[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                o[i] = (uint16_t)(f32_bits(round_bf16(tot[g][j][i])) >> 16);
-            *(uint2 *)(tl.out + (size_t)t * tl.R + 16 * g) =
-                make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+            for (int i = 0; i < C::G; ++i) {
+                const uint32_t k = b + i;
+                lds_barrier();
+                pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, wsc, k, r16,
+                                  next_src(k), loff, rstride, cl0, cl1);
+            }
         }
+#pragma unroll
+        for (int i = 0; i < C::G - 1; ++i) {
+            const uint32_t k = nfull + i;
+            if (k >= nsteps)
+                break;
+            lds_barrier();
+            pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, wsc, k, r16,
+                              next_src(k), loff, rstride, cl0, cl1);
+        }
+
+        // epilogue: lane holds rows 16 g + 4q + i of the wave's 16 RG for tokens 16j + r16 -> bf16,
+        // stored at the wave's base (token 16 j, row 16 g) plus the lane's offset
+        const uint32_t store_t = tl.wcol + sub * C::NROWS < tl.R ? tl.cnt : 0u;
+        // opaque per n-tile, or the compiler hoists every token tile's 64-bit lane address out of
+        // the n-tile loop (sixteen registers, spilled)
+        uint32_t lo = lane_out;
+        asm volatile("" : "+v"(lo));
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            const uint32_t t = 16 * j + r16;
+            if (t >= store_t)
+                continue;
+#pragma unroll
+            for (int g = 0; g < C::RG; ++g) {
+                uint16_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    o[i] = (uint16_t)(f32_bits(round_bf16(tot[g][j][i])) >> 16);
+                uint16_t *dst = tl.out + sub * C::NROWS + (size_t)(16 * j) * tl.R + 16 * g;
+                *(uint2 *)(dst + lo) =
+                    make_uint2((uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16));
+            }
+        }
+        rows = nrows;
     }
 }
 
-// One projection tile: 128 weight rows (of gate, up or down) x one m-tile of placement slots,
-// bf16-rounded outputs (bf16_round_in_place of every projection, src/wide_metal_moe.rs:1236-1251).
-// n-tiles [0, R1 / 128) use the first matrix (gate, or down), the rest the second (up).
+// One projection workgroup: n_sub consecutive n-tiles of NROWS weight rows (of gate, up or down)
+// x one m-tile of placement slots, bf16-rounded outputs (bf16_round_in_place of every projection,
+// src/wide_metal_moe.rs:1236-1251). Output columns [0, R1) come from the first matrix (gate, or
+// down), the rest from the second (up).
 template <class C>
 __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C::WAVES_PER_EU))) void prefill_b_kernel(const PrefillArgs args)
 {
@@ -325,27 +402,29 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
     const uint32_t nsteps = blocks / C::SB;  // the launcher checks blocks % SB
     uint4 *ring = lds_pf;                                   // [D][STEP] code units, swizzled
     float *lds_scale = (float *)(ring + C::D * C::STEP);    // [blocks][PF_MT] activation scales
-    float *lds_wscale = lds_scale + blocks * PF_MT;       // [NSB][blocks] weight block scales
+    uint32_t *lds_tok = (uint32_t *)(lds_scale + blocks * PF_MT);  // [PF_MT] token rows (producer)
+    float *lds_wscale = (float *)(lds_tok + PF_MT);       // [n_sub * NSB][blocks] weight block scales
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r16 = lane & 15;
     // XCD-aware order: workgroups go round-robin to the 8 XCDs (blockIdx % 8), so XCD x takes
-    // m-tiles x, x + 8, ... and runs all n-tiles of one m-tile back to back: the m-tile's
+    // m-tiles x, x + 8, ... and runs all n-tile groups of one m-tile back to back: the m-tile's
     // activation codes stay in that XCD's L2 while its n-tiles stream their weight rows, and the
     // m-tiles (counted on the device) spread evenly over the XCDs.
-    const uint32_t n_ntiles = (args.R + C::NROWS - 1) / C::NROWS;
+    const uint32_t n_sub = args.n_sub;
+    const uint32_t n_groups = (args.R + C::NROWS - 1) / C::NROWS / n_sub;  // the launcher checks n_sub
     const uint32_t local = blockIdx.x >> 3;
-    const uint32_t mt = (blockIdx.x & 7) + 8 * (local / n_ntiles), ntile = local % n_ntiles;
-    if (mt >= args.n_tiles[0])
+    const uint32_t mt = (blockIdx.x & 7) + 8 * (local / n_groups), group = local % n_groups;
+    // the tile count and the tile's descriptor in one round trip (the descriptor index clamped:
+    // the grid holds whole groups of eight m-tiles)
+    const uint32_t n_mtiles = args.n_tiles[0];
+    const PfTileDesc td = args.tiles[mt < args.max_tiles ? mt : args.max_tiles - 1];
+    if (mt >= n_mtiles || td.cnt == 0)
         return;
-    const uint2 tl = args.tiles[mt];
-    const ActiveExpert ae = args.active[tl.x];
-    const uint32_t m0 = tl.y;
-    if (m0 >= ae.cnt)
-        return;
-    const uint32_t cnt_t = ae.cnt - m0 < PF_MT ? ae.cnt - m0 : PF_MT;
-    const uint32_t col0 = ntile * C::NROWS;               // output column of the tile
-    const uint32_t slot0 = ae.off + m0;
+    const ExpertPtrs &ep = td.ep;
+    const uint32_t cnt_t = td.cnt < PF_MT ? td.cnt : PF_MT;
+    const uint32_t col0 = group * n_sub * C::NROWS;       // first output column of the workgroup
+    const uint32_t slot0 = td.slot0;
     const bool gather = args.placement_pos != nullptr;
 
     // token rows of the m-tile's slots (lane: slots lane and 64 + lane, the second only below PF_MT;
@@ -369,21 +448,17 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
         if (bad)
             raise_flag(args.flags, FLAG_SCHEDULE);
     }
-    // Each 128 output columns of the n-tile come from one 128-row block of one matrix (gate or up,
-    // or down; R1 and R are multiples of 128): column col is row src_row(col) of the second matrix
-    // (up) when col >= R1, else of the first (gate, or down). Columns past R (a partial last
-    // n-tile) map to row 0 and are never stored.
-    const auto src_row = [&](uint32_t col) {
-        return col >= args.R ? 0u : (col >= args.R1 ? col - args.R1 : col);
-    };
-    // weight block scales of the n-tile's 128-row blocks ([NSB][blocks]) and the m-tile's
-    // activation scales, transposed (lds_scale[b * PF_MT + t]) with 4-byte direct-to-LDS loads (lane =
-    // token; a second instruction covers tokens 64 .. PF_MT - 1), spread over all waves
-    if ((uint32_t)tid < C::NSB * blocks) {
-        const uint32_t hb = (uint32_t)tid / blocks, b = (uint32_t)tid - hb * blocks;
+    // weight block scales of the n-tiles' 128-row blocks ([n_sub * NSB][blocks]; each 128 output
+    // columns come from one 128-row block of one matrix, R1 and R being multiples of 128) and the
+    // m-tile's activation scales, transposed (lds_scale[b * PF_MT + t]) with 4-byte direct-to-LDS
+    // loads (lane = token; a second instruction covers tokens 64 .. PF_MT - 1), spread over all
+    // waves
+    for (uint32_t i = tid; i < n_sub * C::NSB * blocks; i += 64 * PF_WAVES) {
+        const uint32_t hb = i / blocks, b = i - hb * blocks;
         const uint32_t col = col0 + 128 * hb;
-        const float *sm = gather ? (col >= args.R1 && col < args.R ? ae.ep.up_s : ae.ep.gate_s) : ae.ep.down_s;
-        lds_wscale[tid] = load_g(sm + (src_row(col) >> 7) * blocks + b);
+        const uint32_t row = col >= args.R ? 0u : (col >= args.R1 ? col - args.R1 : col);
+        const float *sm = gather ? (col >= args.R1 && col < args.R ? ep.up_s : ep.gate_s) : ep.down_s;
+        lds_wscale[i] = load_g(sm + (row >> 7) * blocks + b);
     }
     for (uint32_t b = wave; b < blocks; b += PF_WAVES) {
         __builtin_amdgcn_global_load_lds(
@@ -394,25 +469,40 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
                 (const __attribute__((address_space(1))) void *)(args.scales + (size_t)tok[1] * blocks + b),
                 (__attribute__((address_space(3))) void *)(lds_scale + b * PF_MT + 64), 4, 0, 0);
     }
+    if (wave >= PF_CONS) {  // the producer's token rows, read back in its loop
+        lds_tok[lane] = tok[0];
+        lds_tok[64 + lane] = tok[1];
+    }
 
-    // the wave's 16 RG rows (inside one 128-row block): matrix, first row, and whether they exist
-    const uint32_t wrow0 = wave * 16 * C::RG, wcol = col0 + wrow0;
-    const uint8_t *wmat = gather ? (wcol >= args.R1 && wcol < args.R ? ae.ep.up_w : ae.ep.gate_w) : ae.ep.down_w;
-    const uint32_t mrow = src_row(wcol);
-    const PfTile tile{ring, lds_scale, lds_wscale + (wrow0 >> 7) * blocks,
-                      wmat + (size_t)(mrow + r16) * K + q * 16,
-                      args.out + (size_t)slot0 * args.R + col0 + wrow0 + 4 * q, args.R, nsteps,
-                      wcol < args.R ? cnt_t : 0u};
+    // the wave's 16 RG rows (inside one 128-row block) in each n-tile
+    const uint32_t wrow0 = wave * 16 * C::RG;
+    PfTile tile;
+    tile.ring = ring;
+    tile.lds_scale = lds_scale;
+    tile.lds_wscale = lds_wscale;
+    tile.mat0 = gather ? ep.gate_w : ep.down_w;
+    tile.mat1 = gather ? ep.up_w : ep.down_w;
+    tile.out = args.out + (size_t)slot0 * args.R + col0 + wrow0;
+    tile.K = K;
+    tile.R = args.R;
+    tile.R1 = args.R1;
+    tile.nsteps = nsteps;
+    tile.n_sub = n_sub;
+    tile.wcol = col0 + wrow0;
+    tile.loff = (uint32_t)r16 * K + (uint32_t)q * 16;
+    tile.cnt = cnt_t;
+    tile.codes = args.codes;
+    tile.lds_tok = lds_tok;
     // the workgroup's 16-token tiles that hold placements (1..PF_TT); whole tiles past them are skipped
     switch ((cnt_t + 15) >> 4) {
-    case 1: pf_body<C, 1>(tile, tok, args.codes, K, wave, lane); break;
-    case 2: pf_body<C, 2>(tile, tok, args.codes, K, wave, lane); break;
-    case 3: pf_body<C, 3>(tile, tok, args.codes, K, wave, lane); break;
-    case 4: pf_body<C, 4>(tile, tok, args.codes, K, wave, lane); break;
-    case 5: pf_body<C, 5>(tile, tok, args.codes, K, wave, lane); break;
-    case 6: pf_body<C, (PF_TT > 6 ? 6 : PF_TT)>(tile, tok, args.codes, K, wave, lane); break;
-    case 7: pf_body<C, (PF_TT > 7 ? 7 : PF_TT)>(tile, tok, args.codes, K, wave, lane); break;
-    default: pf_body<C, PF_TT>(tile, tok, args.codes, K, wave, lane); break;
+    case 1: pf_body<C, 1>(tile, wave, lane); break;
+    case 2: pf_body<C, 2>(tile, wave, lane); break;
+    case 3: pf_body<C, 3>(tile, wave, lane); break;
+    case 4: pf_body<C, 4>(tile, wave, lane); break;
+    case 5: pf_body<C, 5>(tile, wave, lane); break;
+    case 6: pf_body<C, (PF_TT > 6 ? 6 : PF_TT)>(tile, wave, lane); break;
+    case 7: pf_body<C, (PF_TT > 7 ? 7 : PF_TT)>(tile, wave, lane); break;
+    default: pf_body<C, PF_TT>(tile, wave, lane); break;
     }
 }
 
@@ -586,23 +676,27 @@ uint32_t prefill_max_tiles(uint32_t rows, uint32_t E)
     return max_active + (P + PF_MT - 1) / PF_MT;
 }
 
+// n-tiles per workgroup: nsub where it divides the n-tile count, every n-tile is whole and the K
+// steps are whole unrolled groups (each n-tile's loop then starts at ring slot 0), else one
 template <class C>
-static void launch_prefill_cfg(const PrefillArgs &a, hipStream_t stream)
+static void launch_prefill_cfg(PrefillArgs a, uint32_t nsub, hipStream_t stream)
 {
-    const size_t lds = (size_t)C::D * C::STEP * 16 + (size_t)(a.K / 128) * (PF_MT + C::NSB) * 4;
+    const uint32_t blocks = a.K / 128, n_ntiles = (a.R + C::NROWS - 1) / C::NROWS;
+    a.n_sub = (n_ntiles % nsub == 0 && a.R % C::NROWS == 0 && (blocks / C::SB) % C::G == 0) ? nsub : 1;
+    const size_t lds = (size_t)C::D * C::STEP * 16 + (size_t)blocks * (PF_MT + a.n_sub * C::NSB) * 4 + PF_MT * 4;
     if (lds > 65536)  // wide K: up to 160 KB of LDS per workgroup on gfx950
         (void)hipFuncSetAttribute((const void *)prefill_b_kernel<C>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)lds);
-    const uint32_t grid = 8 * ((a.max_tiles + 7) / 8) * ((a.R + C::NROWS - 1) / C::NROWS);
+    const uint32_t grid = 8 * ((a.max_tiles + 7) / 8) * (n_ntiles / a.n_sub);
     hipLaunchKernelGGL((prefill_b_kernel<C>), dim3(grid), dim3(64 * PF_WAVES), lds, stream, a);
 }
 
-static void launch_prefill_projection(const PrefillArgs &a, hipStream_t stream)
+static void launch_prefill_projection(const PrefillArgs &a, uint32_t nsub, hipStream_t stream)
 {
     if ((a.K / 128) % PfWide::SB == 0)
-        launch_prefill_cfg<PfWide>(a, stream);
+        launch_prefill_cfg<PfWide>(a, nsub, stream);
     else
-        launch_prefill_cfg<PfNarrow>(a, stream);
+        launch_prefill_cfg<PfNarrow>(a, nsub, stream);
 }
 
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
@@ -619,7 +713,6 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
 
     // gate and up as one stacked projection of 2I output columns per slot
     PrefillArgs ga{};
-    ga.active = mb.active;
     ga.tiles = pb.tiles;
     ga.n_tiles = pb.n_tiles;
     ga.placement_pos = mb.placement_pos;
@@ -633,7 +726,7 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     ga.out = pb.hidden;
     ga.flags = flags;
     int t = timer_begin(K_PREFILL_GATEUP, stream);
-    launch_prefill_projection(ga, stream);
+    launch_prefill_projection(ga, PF_NSUB_GATEUP, stream);
     timer_end(t, stream);
     // bf16-staged SwiGLU + re-quantisation of the hidden per (placement, 128 group)
     const uint32_t groups = P * (I >> 7);
@@ -652,7 +745,7 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     da.rows = P;
     da.out = pb.y;
     t = timer_begin(K_PREFILL_DOWN, stream);
-    launch_prefill_projection(da, stream);
+    launch_prefill_projection(da, PF_NSUB_DOWN, stream);
     timer_end(t, stream);
 
     const uint32_t n8 = rows * (H >> 3);

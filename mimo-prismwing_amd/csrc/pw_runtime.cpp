@@ -1384,10 +1384,10 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
     PW_HIP(order.err);
     PW_TRY(ensure_moe(rt, rows, E, H, I, false));
     const uint32_t max_tiles = pw::prefill_max_tiles(rows, E);
-    PW_HIP(rt->pf_tiles.ensure((size_t)max_tiles * 8 + 16));
+    PW_HIP(rt->pf_tiles.ensure((size_t)max_tiles * sizeof(pw::PfTileDesc) + 16));
     pw::PrefillBuffers pb{};
-    pb.tiles = (uint2 *)rt->pf_tiles.p;
-    pb.n_tiles = (uint32_t *)((char *)rt->pf_tiles.p + (size_t)max_tiles * 8);
+    pb.tiles = (pw::PfTileDesc *)rt->pf_tiles.p;
+    pb.n_tiles = (uint32_t *)((char *)rt->pf_tiles.p + (size_t)max_tiles * sizeof(pw::PfTileDesc));
     pb.hidden = (uint16_t *)rt->moe_hidden.p;  // [P][I] f32 scratch holds the bf16 hidden
     pb.y = (uint16_t *)rt->moe_y.p;            // [P][H] f32 scratch holds the bf16 outputs
     PW_TRY(ensure_silu_table(rt));

@@ -245,6 +245,26 @@ def test_closed_form_prefill_bit_exact(rt, closed_form, rows):
 
 
 @pytest.fixture(scope="module")
+def closed_form_two_step(rt):
+    experts, x, sel, w = closed_form_mode_b(0x50570300, 144, 8, hidden=512, inter=512)
+    projs, bank = _bank_from(rt, experts, 8)
+    return experts, x, sel, w, projs, bank
+
+
+@pytest.mark.parametrize("rows", [9, 144])
+def test_closed_form_prefill_two_steps_bit_exact(rt, closed_form_two_step, rows):
+    """Hidden 512, intermediate 512, top-8 of 8 experts: two 256-column K steps per projection, so
+    a prefill workgroup runs two n-tiles of its m-tile in a row (gate/up four n-tiles, down two),
+    the second n-tile's first weights loaded during the first one's last steps; 144 rows give each
+    expert a full 128-slot m-tile and a 16-slot one. Bit for bit the oracle's layer."""
+    experts, x, sel, w, _, bank = closed_form_two_step
+    x, sel, w = x[:rows], sel[:rows], w[:rows]
+    want, want_raw = O.moe_layer("b", x, experts, 8, sel, w, raw=True)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW, prefill=True), want_raw)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16, prefill=True), want)
+
+
+@pytest.fixture(scope="module")
 def closed_form_odd(rt):
     experts, x, sel, w = closed_form_mode_b(0x50570200, 96, 12, hidden=384)
     projs, bank = _bank_from(rt, experts, 12)

@@ -51,6 +51,14 @@ def test_closed_form_layer_data_meets_its_preconditions():
     assert np.all(np.isfinite(out)) and np.any(out)
 
 
+def test_closed_form_two_step_layer_meets_its_preconditions():
+    """The hidden-512, intermediate-512 closed form (two K steps per projection, several n-tiles
+    per prefill workgroup) at the GPU test's seed and size."""
+    experts, x, sel, w = closed_form_mode_b(0x50570300, 144, 8, hidden=512, inter=512, check=True)
+    out = O.moe_layer("b", x[:2], experts, 8, sel[:2], w[:2])
+    assert np.all(np.isfinite(out)) and np.any(out)
+
+
 def test_closed_form_odd_hidden_blocks_meets_its_preconditions():
     """The hidden-384 closed form (three 128-column blocks: the prefill's one-block K steps and its
     separate SwiGLU kernel) at the GPU test's seed and size."""
