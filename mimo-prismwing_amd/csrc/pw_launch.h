@@ -159,12 +159,31 @@ void launch_linear_b(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *cod
 void launch_quant_group128(const void *x, bool x_f32, uint32_t rows, uint32_t K, uint8_t *codes,
                            float *scales, uint32_t *flags, hipStream_t stream);
 
+// One m-tile of the prefill's grouped GEMM (up to PREFILL_MT placement slots of one routed
+// expert, in ascending expert order): the expert's weights and the tile's slots, so a GEMM
+// workgroup finds its operands in one load.
+constexpr uint32_t PREFILL_MT = 128;
+struct PfTileDesc {
+    ExpertPtrs ep;
+    uint32_t slot0;  // first placement slot
+    uint32_t cnt;    // placement slots of the tile
+    uint32_t pad[2];
+};
+static_assert(sizeof(PfTileDesc) == 64, "a tile descriptor is one 64-byte scalar load");
+struct PfTileTable {
+    PfTileDesc *tiles;  // [max_tiles]
+    uint32_t *n_tiles;  // [1]
+    uint32_t max_tiles;
+};
+
 // Bytes of MoeBuffers::sched the schedule of `rows` token rows over E experts needs (0 for the
 // batches scheduled in one workgroup).
 size_t moe_sched_scratch_bytes(uint32_t rows, uint32_t E);
-void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
+// With tiles, the schedules of long batches also write the prefill's m-tile table (returns true;
+// false: the caller builds it).
+bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
                          uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
-                         uint32_t *flags, hipStream_t stream);
+                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles = nullptr);
 // expert_offsets [E + 1]: expert e's placement slots are [off[e], off[e + 1]) (after a schedule).
 void launch_expert_offsets(const MoeBuffers &mb, uint32_t E, uint32_t *expert_offsets, hipStream_t stream);
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
@@ -179,16 +198,6 @@ void launch_router(const void *x, bool x_f32, const void *w, bool w_f32, const f
                    uint32_t *flags, hipStream_t stream);
 
 // Routed-MoE prefill (mode B grouped block-FP8 GEMM, pw_prefill.hip) after launch_moe_schedule.
-// One m-tile of the prefill's grouped GEMM (up to 128 placement slots of one routed expert): the
-// expert's weights and the tile's slots, so a GEMM workgroup finds its operands in one load.
-struct PfTileDesc {
-    ExpertPtrs ep;
-    uint32_t slot0;  // first placement slot
-    uint32_t cnt;    // placement slots of the tile
-    uint32_t pad[2];
-};
-static_assert(sizeof(PfTileDesc) == 64, "a tile descriptor is one 64-byte scalar load");
-
 struct PrefillBuffers {
     PfTileDesc *tiles;  // [prefill_max_tiles]
     uint32_t *n_tiles;  // [1]
@@ -201,9 +210,10 @@ void launch_silu_table(uint16_t *table, hipStream_t stream);
 void launch_swiglu_staged(const float *gate, const float *up, uint32_t n, const uint16_t *silu_table, float *out,
                           uint32_t *flags, hipStream_t stream);
 uint32_t prefill_max_tiles(uint32_t rows, uint32_t E);
+// tiles_built: the schedule wrote pb's m-tile table (launch_moe_schedule returned true).
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,
-                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream);
+                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream, bool tiles_built);
 
 void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, const ExpertPtrs &ep, uint32_t expert,
                            const MoeBuffers &mb,

@@ -306,11 +306,14 @@ __global__ __launch_bounds__(64) void moe_sched_mark_kernel(const uint32_t *__re
         ss.badw[blockIdx.x] = any ? 1u : 0u;
 }
 
+// With a tile table (tt.tiles non-null), also the prefill's m-tiles: ceil(count / PREFILL_MT) per
+// routed expert in ascending expert order, each with the expert's weights and its slots (none
+// when the routes are rejected).
 __global__ __launch_bounds__(1024) void moe_sched_plan_kernel(
     const ExpertPtrs *__restrict__ bank, uint32_t rows, uint32_t E, uint32_t max_active, SchedScratch ss,
     MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
     ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
-    uint32_t *__restrict__ row_slots, uint32_t *flags)
+    uint32_t *__restrict__ row_slots, uint32_t *flags, PfTileTable tt)
 {
     __shared__ uint32_t s_scan[48], s_bad, s_max;
     const uint32_t tid = threadIdx.x, e = tid;
@@ -393,6 +396,26 @@ __global__ __launch_bounds__(1024) void moe_sched_plan_kernel(
     }
     __syncthreads();
     const bool rejected = s_bad != 0 || total != P;
+    if (tt.tiles) {
+        const uint32_t live = e < E && c && act < max_active ? c : 0u;
+        const uint32_t nt = (live + PREFILL_MT - 1) / PREFILL_MT;
+        uint32_t n_tiles;
+        const uint32_t first = block_exclusive_scan(nt, s_scan, &n_tiles);
+        for (uint32_t i = 0; i < nt; ++i)
+            if (first + i < tt.max_tiles) {
+                u32x4 *dst = (u32x4 *)(tt.tiles + first + i);
+                dst[0] = ep0;
+                dst[1] = ep1;
+                dst[2] = ep2;
+                dst[3] = u32x4{off + i * PREFILL_MT, live - i * PREFILL_MT < PREFILL_MT ? live - i * PREFILL_MT
+                                                                                       : PREFILL_MT, 0u, 0u};
+            }
+        if (tid == 0) {
+            tt.n_tiles[0] = rejected ? 0u : (n_tiles < tt.max_tiles ? n_tiles : tt.max_tiles);
+            if (n_tiles > tt.max_tiles)
+                raise_flag(flags, FLAG_SCHEDULE);
+        }
+    }
     if (rejected)
         for (uint32_t i = tid; i < P; i += blockDim.x) {
             placement_pos[i] = 0;
@@ -1029,10 +1052,11 @@ __global__ __launch_bounds__(256) void round_output_kernel(const float *__restri
 }
 
 // ------------------------------------------------------------------------------- launchers
-void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
+bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
                          uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
-                         uint32_t *flags, hipStream_t stream)
+                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles)
 {
+    bool tiles_built = false;
     const uint32_t words = (rows + 31) >> 5;
     size_t lds = (size_t)(E * words + E) * sizeof(uint32_t);
     const size_t with_prefix_lds = lds + (size_t)E * words * sizeof(uint16_t);
@@ -1062,13 +1086,16 @@ void launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
         const uint32_t nwg = (rows + 63) / 64;
         hipLaunchKernelGGL(moe_sched_mark_kernel, dim3(nwg), dim3(64), (size_t)E * 8, stream, ids, weights, rows, E,
                            ss);
+        const PfTileTable tt = tiles ? *tiles : PfTileTable{nullptr, nullptr, 0};
         hipLaunchKernelGGL(moe_sched_plan_kernel, dim3(1), dim3(1024), 0, stream, bank, rows, E, max_active, ss,
                            mb.plan, mb.active_expert, mb.active_offset, mb.active, mb.placement_pos,
-                           mb.placement_w, mb.row_slots, flags);
+                           mb.placement_w, mb.row_slots, flags, tt);
+        tiles_built = tiles != nullptr;
         hipLaunchKernelGGL(moe_sched_place_kernel, dim3(nwg), dim3(64), 0, stream, ids, weights, rows, E, max_active,
                            ss, mb.plan, mb.active, mb.placement_pos, mb.placement_w, mb.row_slots);
     }
     timer_end(t, stream);
+    return tiles_built;
 }
 
 // Mode A: gate/up (+SwiGLU) then down, both as split-K expert projections (pw_moe_a.hip).

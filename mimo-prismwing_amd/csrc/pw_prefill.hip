@@ -38,7 +38,7 @@ namespace pw {
 
 // Against 96-slot m-tiles, 2048 tokens: uniform routing unchanged (256 m-tiles either way), Zipf
 // routing 341 -> 311 m-tiles, layer 1693 -> 1595 us.
-constexpr uint32_t PF_MT = 128;                   // placement slots per m-tile
+constexpr uint32_t PF_MT = PREFILL_MT;            // placement slots per m-tile
 // n-tiles per workgroup, where they divide evenly. Consecutive n-tiles share the workgroup's
 // set-up and run the weight stream on across n-tiles, but put more m-tiles' activation codes in an
 // XCD's L2 at once (32 CUs / (n-tiles per m-tile / PF_NSUB) m-tiles): the down projection's codes
@@ -572,17 +572,21 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
 #pragma unroll
     for (int i = 0; i < 8; ++i)
         sb[i] = load_g(silu_table + ((i & 1) ? (gw[i >> 1] >> 16) : (gw[i >> 1] & 0xffffu)));
+    // non-finite gate / up values: a bf16 half whose exponent field is all ones carries into its
+    // bit 15 when 0x80 is added to the masked field (two values per word, no carry between them)
+    uint32_t nf = 0, emax = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        nf |= ((gw[i] & 0x7f807f80u) + 0x00800080u) | ((uw[i] & 0x7f807f80u) + 0x00800080u);
     float h[8];
-    bool bad = false;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const uint32_t gb = gw[i >> 1], ub = uw[i >> 1];
-        const float gv = f32_from((i & 1) ? (gb & 0xffff0000u) : (gb << 16));
+        const uint32_t ub = uw[i >> 1];
         const float uv = f32_from((i & 1) ? (ub & 0xffff0000u) : (ub << 16));
         h[i] = round_bf16(f32_from(sb[i] << 16) * uv);
-        bad |= !finite_f32(gv) || !finite_f32(uv) || !finite_f32(h[i]);
+        emax = max(emax, f32_bits(h[i]) & 0x7f800000u);
     }
-    if (bad)
+    if ((nf & 0x80008000u) || emax == 0x7f800000u)
         raise_flag(flags, FLAG_SWIGLU_NONFINITE);
     float m = 0.f;
 #pragma unroll
@@ -599,7 +603,7 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         n[i] = finite_f32(h[i]) ? quant_ratio_bf16(h[i], scale, rcp) : 0.f;
-        n[i] = n[i] < -448.f ? -448.f : (n[i] > 448.f ? 448.f : n[i]);
+        n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
     }
     uint32_t packed[2];
 #pragma unroll
@@ -701,15 +705,16 @@ static void launch_prefill_projection(const PrefillArgs &a, uint32_t nsub, hipSt
 
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,
-                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream)
+                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream, bool tiles_built)
 {
     (void)bank;
     const uint32_t P = rows * 8;
     const uint32_t max_active = E < P ? E : P;
     const uint32_t max_tiles = prefill_max_tiles(rows, E);
     launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
-    hipLaunchKernelGGL(prefill_tiles_kernel, dim3(1), dim3(1024), 0, stream, mb.plan, mb.active, max_active,
-                       pb.tiles, max_tiles, pb.n_tiles, flags);
+    if (!tiles_built)
+        hipLaunchKernelGGL(prefill_tiles_kernel, dim3(1), dim3(1024), 0, stream, mb.plan, mb.active, max_active,
+                           pb.tiles, max_tiles, pb.n_tiles, flags);
 
     // gate and up as one stacked projection of 2I output columns per slot
     PrefillArgs ga{};
