@@ -86,6 +86,12 @@ struct SplitArgs {
     uint32_t *flags;
     uint32_t single;                // 1: one expert on rows 0..rows-1, its entry is `one` (no schedule)
     ActiveExpert one;
+    // One token's routes with no schedule (route_ids non-null): work item a is the token's route a,
+    // expert route_ids[a] of the bank's E, on placement slot a (see moe_a_one_token_direct)
+    const ExpertPtrs *bank;
+    const uint32_t *route_ids;
+    const float *route_w;
+    uint32_t E;
 };
 
 // Where a launch left the per-placement expert outputs: `ks` split-K partial sums of [P][H] f32,
@@ -130,9 +136,14 @@ bool launch_moe_a_down_out(const SplitArgs &args, float *out_f32, uint16_t *out_
 // Down and combine of a one-token decode batch in one launch (mode A, I = 2048, eight routed
 // experts; args are the down projection's, whose rows are the eight placement slots): the same
 // arithmetic as the split-K down followed by the combine; false when the batch does not fit it.
-// Only for batches of one token.
+// Only for batches of one token. With args.route_ids (no schedule) it ranks the token's eight
+// routes by expert id for the combine and checks them as the schedule would (ids inside the bank,
+// no expert twice, finite weights; FLAG_SCHEDULE otherwise); plan and placement_w are then unused.
 bool launch_moe_a_down_combine1(const SplitArgs &args, const MoePlan *plan, const float *placement_w, float *out_f32,
                                 uint16_t *out_bf16, bool raw, hipStream_t stream);
+// Whether a one-token mode A layer of hidden H and intermediate I runs as the fused gate/up and the
+// one-token down+combine (both reading the token's routes directly, no schedule launch).
+bool moe_a_one_token_direct(uint32_t H, uint32_t I);
 bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_active, uint16_t *hidden_planes,
                                hipStream_t stream);
 void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t I, uint16_t *hidden_planes,
@@ -186,10 +197,18 @@ bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
                          uint32_t *flags, hipStream_t stream, const PfTileTable *tiles = nullptr);
 // expert_offsets [E + 1]: expert e's placement slots are [off[e], off[e + 1]) (after a schedule).
 void launch_expert_offsets(const MoeBuffers &mb, uint32_t E, uint32_t *expert_offsets, hipStream_t stream);
+// One token's routes for a mode A layer launched without a schedule (moe_a_one_token_direct).
+struct OneTokenRoutes {
+    const uint32_t *ids;  // [8]
+    const float *w;       // [8]
+    uint32_t E;           // experts in the bank
+};
+// routes: a one-token mode A batch that moe_a_one_token_direct accepts, with no schedule launched
+// before (mb's schedule tables are not read).
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                       bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
-                      hipStream_t stream);
+                      hipStream_t stream, const OneTokenRoutes *routes = nullptr);
 
 // Device router (pw_router.hip): x [rows][K] (f32 or bf16) and router weights [E][K] (f32 or bf16)
 // -> scores [rows][E], selected / weights [rows][8]; tie_rows (optional) counts boundary ties.

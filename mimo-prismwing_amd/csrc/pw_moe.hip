@@ -1109,7 +1109,8 @@ struct DirectOut {
 static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, uint32_t rows,
                               uint32_t placements, uint32_t max_active, uint32_t max_count, uint32_t H,
                               uint32_t I, uint32_t *flags, hipStream_t stream, const ActiveExpert *one = nullptr,
-                              const DirectOut *direct = nullptr)
+                              const DirectOut *direct = nullptr, const ExpertPtrs *bank = nullptr,
+                              const OneTokenRoutes *routes = nullptr)
 {
     const int nt = max_count > 16 ? 2 : 1;
     const uint32_t cnt = max_count < 16u * nt ? max_count : 16u * nt;
@@ -1133,6 +1134,12 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     if (one) {
         ga.single = 1;
         ga.one = *one;
+    }
+    if (routes) {  // the fused gate/up and the one-token down+combine read the routes themselves
+        ga.bank = bank;
+        ga.route_ids = routes->ids;
+        ga.route_w = routes->w;
+        ga.E = routes->E;
     }
     const SplitPlan gp = plan_split(H, 2, x_f32 ? 3 : 1, cnt);
     ga.KS = gp.ks;
@@ -1208,12 +1215,12 @@ static void launch_b_moe(const ExpertPtrs *bank, const MoeBuffers &mb, uint32_t 
 static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                                 bool x_f32, uint32_t rows, uint32_t placements, uint32_t max_active,
                                 uint32_t max_count, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream,
-                                const DirectOut *direct = nullptr)
+                                const DirectOut *direct = nullptr, const OneTokenRoutes *routes = nullptr)
 {
     const bool wide = max_count > 16;
     if (mode == 0)
         return launch_a_moe(mb, x, x_f32, rows, placements, max_active, max_count, H, I, flags, stream, nullptr,
-                            direct);
+                            direct, bank, routes);
     launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
     if (wide) launch_b_moe<4, 2>(bank, mb, rows, placements, max_active, H, I, flags, stream);
     else launch_b_moe<4, 1>(bank, mb, rows, placements, max_active, H, I, flags, stream);
@@ -1223,11 +1230,12 @@ static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const Moe
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                       bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
-                      hipStream_t stream)
+                      hipStream_t stream, const OneTokenRoutes *routes)
 {
     const DirectOut direct{out_f32, out_bf16, raw};
-    const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, max_active, max_count, H, I, flags,
-                                        stream, rows == 1 ? &direct : nullptr);
+    const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, routes ? 8 : max_active,
+                                        routes ? 1 : max_count, H, I, flags, stream, rows == 1 ? &direct : nullptr,
+                                        routes);
     if (!eo.y)
         return;  // the one-token down wrote the combined output
     const uint32_t n4 = rows * (H >> 2);

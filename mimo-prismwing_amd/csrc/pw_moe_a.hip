@@ -207,6 +207,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
 // into one 16-row MFMA operand (lanes 0..7 of a row group read gate rows, 8..15 up rows), so a lone
 // expert spreads over twice the workgroups; output rows 0..7 are gate, 8..15 up, and each gate
 // lane takes its up values from the lane 32 above. The sums are the same as with RM = 16.
+// Route a of a one-token batch as a schedule entry: expert route_ids[a] (ids past the bank take its
+// last expert; the down+combine flags them), placement slot a, token row 0.
+__device__ __forceinline__ ActiveExpert route_entry(const SplitArgs &args, uint32_t a)
+{
+    const uint32_t id = load_g(args.route_ids + a);
+    ActiveExpert ae{};
+    ae.ep = args.bank[id < args.E ? id : args.E - 1];
+    ae.off = a;
+    ae.cnt = 1;
+    ae.tok[0] = 0;
+    return ae;
+}
+
 template <int NS, int BPW, int RM>
 __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs args, uint16_t *__restrict__ hidden)
 {
@@ -218,7 +231,7 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     const int q = lane >> 4, r16 = lane & 15;
     const uint32_t G = args.R / RM;
     const uint32_t g = blockIdx.x % G, a = blockIdx.x / G;
-    const ActiveExpert ae = args.single ? args.one : args.active[a];
+    const ActiveExpert ae = args.single ? args.one : (args.route_ids ? route_entry(args, a) : args.active[a]);
     if (ae.cnt == 0)
         return;
     if (ae.cnt > 16u || ae.cnt > args.cap) {
@@ -596,14 +609,40 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r16 = lane & 15;
-    const uint32_t n_active = plan->n_active;
     const uint32_t a = (uint32_t)wave >> 1, s = (uint32_t)wave & 1;
     const uint32_t K = args.K, H = args.R;
     const uint32_t row0 = blockIdx.x * 16;
     float *red = (float *)(lds_x + 16 * 3 * STRIDE);  // [16 waves][16 rows]
+    uint32_t *rank_slot = (uint32_t *)(red + 16 * 16);  // [8] routes: the slot of each expert rank
+    // routes without a schedule: lane i < 8 ranks route i by (expert id, route index), so the
+    // waves and the combine take the experts in ascending id like the schedule; duplicates, ids
+    // past the bank and non-finite weights are rejected
+    uint32_t n_active, slot_of_a = a;
+    if (args.route_ids) {
+        const uint32_t li = (uint32_t)lane & 7;
+        const uint32_t id = load_g(args.route_ids + li);
+        uint32_t rank = 0;
+        bool dup = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t idj = __shfl(id, j, 64);
+            rank += idj < id || (idj == id && (uint32_t)j < li);
+            dup |= idj == id && (uint32_t)j != li;
+        }
+        slot_of_a = __builtin_ctzll(__ballot(lane < 8 && rank == a));
+        if (wave == 0 && lane < 8) {
+            rank_slot[rank] = li;
+            const bool bad = dup || id >= args.E || !finite_f32(load_g(args.route_w + li));
+            if (bad)
+                raise_flag(args.flags, FLAG_SCHEDULE);
+        }
+        n_active = 8;
+    } else {
+        n_active = plan->n_active;
+    }
     f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
     if (a < n_active) {
-        const ActiveExpert ae = args.active[a];
+        const ActiveExpert ae = args.route_ids ? route_entry(args, slot_of_a) : args.active[a];
         if (ae.cnt != 1 && lane == 0)
             raise_flag(args.flags, FLAG_SCHEDULE);
         const uint32_t k0 = s * KC;
@@ -669,8 +708,13 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
     float acc = 0.f;
     for (uint32_t e = 0; e < n_active && e < 8; ++e) {
         const float y = red[(2 * e) * 16 + lane] + red[(2 * e + 1) * 16 + lane];
-        const uint32_t slot = args.active[e].off;
-        const float w = placement_w[slot < args.P ? slot : 0];
+        float w;
+        if (args.route_ids) {
+            w = load_g(args.route_w + rank_slot[e]);
+        } else {
+            const uint32_t slot = args.active[e].off;
+            w = placement_w[slot < args.P ? slot : 0];
+        }
         acc = __fadd_rn(acc, __fmul_rn(y, w));
     }
     const float r = round_bf16(acc);
@@ -683,6 +727,12 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
         raise_flag(args.flags, FLAG_ROUND_NONFINITE);
 }
 
+bool moe_a_one_token_direct(uint32_t H, uint32_t I)
+{
+    // the fused gate/up's K (eight splits of four blocks) and the one-token down's (I = 2048)
+    return H == 8 * 4 * 128 && I == 2048 && I % 16 == 0 && H % 16 == 0;
+}
+
 bool launch_moe_a_down_combine1(const SplitArgs &args, const MoePlan *plan, const float *placement_w, float *out_f32,
                                 uint16_t *out_bf16, bool raw, hipStream_t stream)
 {
@@ -690,7 +740,7 @@ bool launch_moe_a_down_combine1(const SplitArgs &args, const MoePlan *plan, cons
     // token, so its eight placements are the rows
     if (args.P != 8 || args.rows != 8 || args.K != 2048 || args.R % 16 != 0)
         return false;
-    const size_t lds = (size_t)16 * 3 * (1024 / 8 + 1) * 16 + 16 * 16 * 4;
+    const size_t lds = (size_t)16 * 3 * (1024 / 8 + 1) * 16 + 16 * 16 * 4 + 8 * 4;
     (void)hipFuncSetAttribute((const void *)moe_a_down_combine1_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds);
     hipLaunchKernelGGL(moe_a_down_combine1_kernel, dim3(args.R >> 4), dim3(1024), lds, stream, args, plan,

@@ -1286,6 +1286,29 @@ int pw_expert_bank_shape(const pw_expert_bank *b, uint32_t *n, uint32_t *h, uint
     return PW_OK;
 }
 
+// A routed layer of `rows` token rows from device route arrays [rows][8]: the schedule, then the
+// experts and the combine; a one-token mode A layer of the shape the fused kernels take reads its
+// eight routes in those kernels, with no schedule launch.
+static void launch_routed_layer(const MoeBuffers &mb, const pw_expert_bank *bank, uint32_t mode, const void *x,
+                                bool x_f32, uint32_t rows, const uint32_t *route_ids, const float *route_weights,
+                                uint32_t max_active, void *output, uint32_t out_dtype, uint32_t *flags,
+                                hipStream_t s)
+{
+    const uint32_t E = bank->n_experts, H = bank->hidden, I = bank->intermediate;
+    float *out_f32 = out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr;
+    uint16_t *out_bf16 = out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr;
+    const bool raw = out_dtype == PW_DTYPE_F32_RAW;
+    if (mode == PW_MODE_A && rows == 1 && pw::moe_a_one_token_direct(H, I)) {
+        const pw::OneTokenRoutes routes{route_ids, route_weights, E};
+        pw::launch_moe_layer(mode, bank->table, mb, x, x_f32, rows, max_active, rows, H, I, out_f32, out_bf16, raw,
+                             flags, s, &routes);
+        return;
+    }
+    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, max_active, mb, flags, s);
+    pw::launch_moe_layer(mode, bank->table, mb, x, x_f32, rows, max_active, rows, H, I, out_f32, out_bf16, raw, flags,
+                         s);
+}
+
 int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
                         uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
                         const float *route_weights, void *output, uint32_t out_dtype, void *stream)
@@ -1306,13 +1329,8 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
     StreamOrder order(rt, s);
     PW_HIP(order.err);
     PW_TRY(ensure_moe(rt, rows, bank->n_experts, bank->hidden, bank->intermediate));
-    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, bank->n_experts,
-                            std::min<uint32_t>(bank->n_experts, rows * 8), rt->mb, rt->d_flags, s);
-    pw::launch_moe_layer(mode, bank->table, rt->mb, x, x_dtype == PW_DTYPE_F32, rows,
-                         std::min<uint32_t>(bank->n_experts, rows * 8), rows, bank->hidden,
-                         bank->intermediate, out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
-                         out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
-                         out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s);
+    launch_routed_layer(rt->mb, bank, mode, x, x_dtype == PW_DTYPE_F32, rows, route_ids, route_weights,
+                        std::min<uint32_t>(bank->n_experts, rows * 8), output, out_dtype, rt->d_flags, s);
     PW_HIP(hipGetLastError());
     return PW_OK;
 }
@@ -1350,12 +1368,8 @@ int pw_moe_layer_device_noalloc(pw_runtime *rt, const pw_expert_bank *bank, uint
     StreamOrder order(rt, s);
     PW_HIP(order.err);
     carve_moe((char *)g_scratch_ptr[rt->device], rows, E, H, I, mb);
-    const uint32_t max_active = std::min<uint32_t>(E, rows * 8);
-    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, max_active, mb, rt->d_flags, s);
-    pw::launch_moe_layer(mode, bank->table, mb, x, x_dtype == PW_DTYPE_F32, rows, max_active, rows, H, I,
-                         out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
-                         out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr, out_dtype == PW_DTYPE_F32_RAW,
-                         rt->d_flags, s);
+    launch_routed_layer(mb, bank, mode, x, x_dtype == PW_DTYPE_F32, rows, route_ids, route_weights,
+                        std::min<uint32_t>(E, rows * 8), output, out_dtype, rt->d_flags, s);
     PW_HIP(hipGetLastError());
     return PW_OK;
 }

@@ -291,10 +291,13 @@ def test_pieces_match_one_workgroup_schedule(rt, full_bank, width):
     check_mode_a(outs[0], ref_raw, moe_condition(x[:width], experts, sel[:width], w[:width]), raw=True)
 
 
-def test_one_token_equals_two_copies(rt, full_bank):
+@pytest.mark.parametrize("x_f32", [False, True])
+def test_one_token_equals_two_copies(rt, full_bank, x_f32):
     """Each token's result depends only on its own row and routes: a two-row batch holding the
     same token twice (every routed expert then has two placements) gives the one-row result in both
-    rows, bit for bit, and that result matches the oracle."""
+    rows, bit for bit, and that result matches the oracle. The one-row layer reads its eight routes
+    in the fused gate/up and the one-token down+combine (no schedule launch); the two-row layer
+    goes through the schedule, so the two paths are held to the same bits."""
     import torch
     stream = torch.cuda.current_stream().cuda_stream
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
@@ -305,12 +308,14 @@ def test_one_token_equals_two_copies(rt, full_bank):
             outs = []
             for rows in (1, 2):
                 xr = np.repeat(x, rows, axis=0)
-                xt = torch.from_numpy(WL.bf16_bits_np(xr).view(np.int16)).cuda()
+                xt = (torch.from_numpy(np.ascontiguousarray(xr)).cuda() if x_f32
+                      else torch.from_numpy(WL.bf16_bits_np(xr).view(np.int16)).cuda())
                 ids = torch.from_numpy(np.repeat(sel, rows, axis=0).astype(np.int32)).cuda()
                 wts = torch.from_numpy(np.repeat(w, rows, axis=0)).cuda()
                 out = torch.empty((rows, 4096), dtype=torch.float32 if out_dtype == P.DTYPE_F32_RAW else torch.int16,
                                   device="cuda")
-                rt.moe_layer_device(full_bank.bank, xt, rows, ids, wts, out, mode=P.MODE_A, out_dtype=out_dtype,
+                rt.moe_layer_device(full_bank.bank, xt, rows, ids, wts, out, mode=P.MODE_A,
+                                    x_dtype=P.DTYPE_F32 if x_f32 else P.DTYPE_BF16, out_dtype=out_dtype,
                                     stream=stream)
                 torch.cuda.synchronize()
                 assert rt.take_flags() == 0
@@ -343,8 +348,9 @@ def test_device_layer_rejects_misaligned_activations(rt, full_bank):
 def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
     """Route buffers with an expert id outside the bank, one token naming an expert twice, or a NaN
     weight raise the schedule error bit (src/wide_metal_moe.rs:858-938 rejects such schedules) from
-    both schedule kernels (1 and 8 rows: one wave; 9 rows: one workgroup) without faulting, and the
-    next valid call gives the same bytes as before."""
+    both schedule kernels (8 rows: one wave; 9 rows: one workgroup) and from the one-token layer's
+    own route checks (1 row, no schedule) without faulting, and the next valid call gives the same
+    bytes as before."""
     import torch
     x = WL.activations(rows, WL.SEED_BASE + 90)
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3)

@@ -30,7 +30,7 @@ def _inputs(torch, rows, seed, f32=False):
 def test_noalloc_layer_equals_allocating_layer(rt, bank, mode, out_dtype):
     import torch
     stream = torch.cuda.current_stream().cuda_stream
-    for rows, seed, f32 in ((8, 150, False), (3, 151, False), (5, 152, True)):
+    for rows, seed, f32 in ((8, 150, False), (3, 151, False), (5, 152, True), (1, 153, False), (1, 154, True)):
         xt, ids, wts = _inputs(torch, rows, seed, f32)
         x_dtype = P.DTYPE_F32 if f32 else P.DTYPE_BF16
         dt = torch.float32 if out_dtype == P.DTYPE_F32_RAW else torch.int16
