@@ -208,10 +208,11 @@ def _bf16_x(torch, WL, rows, hidden, seed):
     return torch.from_numpy(WL.bf16_bits_np(WL.activations(rows, seed, hidden=hidden)).view(np.int16)).cuda()
 
 
-def projection_legs(torch, rt, bank, P, WL, calls=200):
+def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
     """Configs 0, 1 and 3 (one projection, one complete expert, separate q/k/v segments), mode A,
     bf16 in and out. HBM-cold: calls rotate over distinct weights well beyond the 256 MB MALL;
-    MALL-warm: one weight copy reused."""
+    MALL-warm: one weight copy reused. small_only: configs 0, 1 (widths 1 and 8) and 3 (k 768)
+    only, for a kernel trace of the small calls."""
     out = {}
     # config 0: W [2048 x 4096] e4m3 + S [16 x 32], x [1 x 4096] -> y [1 x 2048]
     copies, n, k = 64, 2048, 4096
@@ -232,7 +233,7 @@ def projection_legs(torch, rt, bank, P, WL, calls=200):
     out["config0_w1"]["algorithmic_bytes"] = alg
     del projs, w, s
     # config 1: one complete expert (gate/up [2 x 2048 x 4096], down [4096 x 2048]) at widths 1..8
-    for width in (1, 2, 4, 8):
+    for width in ((1, 8) if small_only else (1, 2, 4, 8)):
         x = _bf16_x(torch, WL, width, 4096, WL.SEED_BASE + 510 + width)
         y = torch.empty((width, 4096), dtype=torch.int16, device="cuda")
         alg = EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES + width * 4096 * 2 * 2
@@ -243,7 +244,7 @@ def projection_legs(torch, rt, bank, P, WL, calls=200):
             rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
         out[f"config1_w{width}"] = rec
     # config 3: separate q [12288], k [768 or 1000], v [512] x 4096 with their own scale grids
-    for k_rows in (768, 1000):
+    for k_rows in ((768,) if small_only else (768, 1000)):
         seg_rows = (12288, k_rows, 512)
         copies = 10
         hosts = []
@@ -270,6 +271,8 @@ def projection_legs(torch, rt, bank, P, WL, calls=200):
                 rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
             out[f"config3_k{k_rows}_w{width}"] = rec
         del projs, hosts
+    if small_only:
+        return out
     # BF16 wide linear: attention o_proj [4096 x 8192] (64 MB), widths 1 and 8, f32 in, bf16-rounded f32 out
     copies, n, k = 10, 4096, 8192
     wb = torch.randn((copies, n, k), dtype=torch.bfloat16, device="cuda").view(torch.int16)
@@ -450,6 +453,8 @@ def main():
                     help="run only the on-device router leg and print its line (for profiling)")
     ap.add_argument("--routing", choices=("uniform", "zipf"), default="uniform",
                     help="routing of the headline decode leg and of --prefill-only (zipf: for profiling)")
+    ap.add_argument("--small-calls-only", action="store_true",
+                    help="run only configs 0, 1 and 3 and the one-token layer and print their line (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -483,6 +488,14 @@ def main():
         res = prefill_leg(torch, rt, bank, P, WL, zipf=args.routing == "zipf")
         print(json.dumps({"workload": "routed-MoE prefill, 2048 tokens, top-8 of 256 experts, mode B, "
                                       f"{args.routing} routing", **res}), flush=True)
+        rt.close()
+        return
+    if args.small_calls_only:
+        b1 = build_batches(P, WL, args.batches, 1, zipf=False)
+        ms1 = time_layer(torch, rt, bank, P, upload(torch, WL, b1), 1, args.steps, args.warmup, P.MODE_A)
+        res = {"w1_layer_us": round(ms1 * 1000, 2), **projection_legs(torch, rt, bank, P, WL, small_only=True)}
+        print(json.dumps({"workload": "small calls: configs 0, 1, 3 and the one-token routed layer, mode A", **res}),
+              flush=True)
         rt.close()
         return
     rows = 8
