@@ -162,6 +162,15 @@ __device__ __forceinline__ uint32_t encode2_e4m3fn(float a, float b)
 // a bf16 value and scale = max(m, 1e-10) / 448 for a bf16 group absmax m >= |a|: over that whole
 // domain (every such (a, m) pair, 1,065,402,238 of them) the clamped e4m3 codes equal those of the
 // IEEE quotient.
+// round_bf16 where a non-finite result is only flagged and never stored: the same bits for every
+// finite input and for infinities; a NaN may come out as an infinity of its sign (still
+// non-finite). Two instructions fewer than the select that keeps NaN payloads.
+__device__ __forceinline__ float round_bf16_or_nonfinite(float v)
+{
+    const uint32_t b = f32_bits(v);
+    return f32_from((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
+}
+
 __device__ __forceinline__ float quant_ratio_bf16(float a, float scale, float rcp)
 {
     const float q = a * rcp;

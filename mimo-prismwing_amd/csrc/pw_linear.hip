@@ -334,7 +334,7 @@ __global__ __launch_bounds__(256) void quant_group128_kernel(const T *__restrict
             n[i] = fin[i] ? quant_ratio_bf16(v[i], scale, rcp) : 0.f;
         else
             n[i] = fin[i] ? v[i] / scale : 0.f;
-        n[i] = n[i] < -448.f ? -448.f : (n[i] > 448.f ? 448.f : n[i]);
+        n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
     }
     const uint32_t lo = encode2_e4m3fn(n[0], n[1]) | (encode2_e4m3fn(n[2], n[3]) << 16);
     const uint32_t hi = encode2_e4m3fn(n[4], n[5]) | (encode2_e4m3fn(n[6], n[7]) << 16);

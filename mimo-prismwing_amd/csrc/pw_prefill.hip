@@ -546,70 +546,94 @@ void launch_swiglu_staged(const float *gate, const float *up, uint32_t n, const 
                        out, flags);
 }
 
+constexpr int SWQ_GPT = 2;  // 128-column groups per 16-lane team of prefill_swiglu_quant_kernel
+
 // bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343)
 // on the bf16 gate/up outputs, h = round(round(g / (1 + e^-g)) * u), fused with the dynamic
 // per-(slot, 128-column group) re-quantisation of h for the down projection
 // (dynamic_fp8_quantized_group128, kernels/block_fp8_gemv.metal:84-137). 16 lanes per group,
-// eight consecutive values per lane (16-byte loads of gate and up), four groups per wave;
+// eight consecutive values per lane (16-byte loads of gate and up), SWQ_GPT groups per team;
 // gu [P][2I] bf16 (gate columns, then up). The silu factor comes from silu_table (65,536 bf16
 // entries indexed by the gate's bits, built by silu_table_kernel), which keeps the exponential
 // and the division out of this VALU-bound kernel.
 __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_t *__restrict__ gu, uint32_t P,
-                                                                   uint32_t I, const uint16_t *__restrict__ silu_table,
+                                                                   uint32_t I, uint32_t gpr_shift,
+                                                                   const uint16_t *__restrict__ silu_table,
                                                                    uint8_t *__restrict__ codes,
                                                                    float *__restrict__ scales, uint32_t *flags)
 {
+    // a 16-lane team takes SWQ_GPT consecutive groups, all of their loads issued before the first
+    // table gather (the kernel is bound by that chain of latencies, not by its instructions)
     const uint32_t lane16 = threadIdx.x & 15;
-    const uint32_t groups_per_row = I >> 7;
-    const uint32_t group = blockIdx.x * 16 + (threadIdx.x >> 4);
-    if (group >= P * groups_per_row)  // whole 16-lane groups leave together
+    const uint32_t groups_per_row = I >> 7, n_groups = P * groups_per_row;
+    const uint32_t group0 = (blockIdx.x * 16 + (threadIdx.x >> 4)) * SWQ_GPT;
+    if (group0 >= n_groups)  // whole 16-lane teams leave together
         return;
-    const uint32_t slot = group / groups_per_row, c = (group - slot * groups_per_row) * 128 + lane16 * 8;
-    const uint16_t *row = gu + (size_t)slot * 2 * I;
-    const uint4 g4 = *(const uint4 *)(row + c), u4 = *(const uint4 *)(row + I + c);
-    const uint32_t gw[4] = {g4.x, g4.y, g4.z, g4.w}, uw[4] = {u4.x, u4.y, u4.z, u4.w};
-    uint32_t sb[8];
+    uint32_t gw[SWQ_GPT][4], uw[SWQ_GPT][4];
+    uint32_t slot[SWQ_GPT], col[SWQ_GPT];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        sb[i] = load_g(silu_table + ((i & 1) ? (gw[i >> 1] >> 16) : (gw[i >> 1] & 0xffffu)));
+    for (int j = 0; j < SWQ_GPT; ++j) {
+        const uint32_t group = group0 + j < n_groups ? group0 + j : group0;
+        // gpr_shift: log2 of the groups per row where that is a power of two (a shift, not a division)
+        slot[j] = gpr_shift < 32 ? group >> gpr_shift : group / groups_per_row;
+        col[j] = (group - slot[j] * groups_per_row) * 128 + lane16 * 8;
+        const uint16_t *row = gu + (size_t)slot[j] * 2 * I;
+        const uint4 g4 = *(const uint4 *)(row + col[j]), u4 = *(const uint4 *)(row + I + col[j]);
+        gw[j][0] = g4.x, gw[j][1] = g4.y, gw[j][2] = g4.z, gw[j][3] = g4.w;
+        uw[j][0] = u4.x, uw[j][1] = u4.y, uw[j][2] = u4.z, uw[j][3] = u4.w;
+    }
+    uint32_t sb[SWQ_GPT][8];
+#pragma unroll
+    for (int j = 0; j < SWQ_GPT; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            sb[j][i] = load_g(silu_table + ((i & 1) ? (gw[j][i >> 1] >> 16) : (gw[j][i >> 1] & 0xffffu)));
     // non-finite gate / up values: a bf16 half whose exponent field is all ones carries into its
     // bit 15 when 0x80 is added to the masked field (two values per word, no carry between them)
     uint32_t nf = 0, emax = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        nf |= ((gw[i] & 0x7f807f80u) + 0x00800080u) | ((uw[i] & 0x7f807f80u) + 0x00800080u);
-    float h[8];
+    for (int j = 0; j < SWQ_GPT; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t ub = uw[i >> 1];
-        const float uv = f32_from((i & 1) ? (ub & 0xffff0000u) : (ub << 16));
-        h[i] = round_bf16(f32_from(sb[i] << 16) * uv);
-        emax = max(emax, f32_bits(h[i]) & 0x7f800000u);
+        for (int i = 0; i < 4; ++i)
+            nf |= ((gw[j][i] & 0x7f807f80u) + 0x00800080u) | ((uw[j][i] & 0x7f807f80u) + 0x00800080u);
+#pragma unroll
+    for (int j = 0; j < SWQ_GPT; ++j) {
+        if (group0 + j >= n_groups)
+            break;
+        float h[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t ub = uw[j][i >> 1];
+            const float uv = f32_from((i & 1) ? (ub & 0xffff0000u) : (ub << 16));
+            // a non-finite h is flagged and coded 0, so its NaN payload never matters
+            h[i] = round_bf16_or_nonfinite(f32_from(sb[j][i] << 16) * uv);
+            emax = max(emax, f32_bits(h[i]) & 0x7f800000u);
+        }
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            m = fmaxf(m, finite_f32(h[i]) ? fabsf(h[i]) : 0.f);
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
+            m = fmaxf(m, __shfl_xor(m, off, 16));
+        const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
+        if (lane16 == 0)
+            scales[group0 + j] = scale;
+        const float rcp = 1.0f / scale;  // h is bf16: one division per group (quant_ratio_bf16)
+        float n[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            n[i] = finite_f32(h[i]) ? quant_ratio_bf16(h[i], scale, rcp) : 0.f;
+            n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
+        }
+        uint32_t packed[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            packed[i] = encode2_e4m3fn(n[4 * i], n[4 * i + 1]) | (encode2_e4m3fn(n[4 * i + 2], n[4 * i + 3]) << 16);
+        *(uint2 *)(codes + (size_t)slot[j] * I + col[j]) = make_uint2(packed[0], packed[1]);
     }
     if ((nf & 0x80008000u) || emax == 0x7f800000u)
         raise_flag(flags, FLAG_SWIGLU_NONFINITE);
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-        m = fmaxf(m, finite_f32(h[i]) ? fabsf(h[i]) : 0.f);
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
-        m = fmaxf(m, __shfl_xor(m, off, 16));
-    const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
-    if (lane16 == 0)
-        scales[group] = scale;
-    const float rcp = 1.0f / scale;  // h is bf16: one division per group (quant_ratio_bf16)
-    float n[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        n[i] = finite_f32(h[i]) ? quant_ratio_bf16(h[i], scale, rcp) : 0.f;
-        n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
-    }
-    uint32_t packed[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        packed[i] = encode2_e4m3fn(n[4 * i], n[4 * i + 1]) | (encode2_e4m3fn(n[4 * i + 2], n[4 * i + 3]) << 16);
-    *(uint2 *)(codes + (size_t)slot * I + c) = make_uint2(packed[0], packed[1]);
 }
 
 // route_weighted_scatter_add_f32 + final bf16 round over bf16 expert outputs: each token sums
@@ -736,8 +760,10 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     // bf16-staged SwiGLU + re-quantisation of the hidden per (placement, 128 group)
     const uint32_t groups = P * (I >> 7);
     t = timer_begin(K_MOE_SWIGLU, stream);
-    hipLaunchKernelGGL(prefill_swiglu_quant_kernel, dim3((groups + 15) / 16), dim3(256), 0, stream, pb.hidden, P,
-                       I, pb.silu, mb.hq, mb.hs, flags);
+    const uint32_t gpr = I >> 7;
+    const uint32_t gpr_shift = (gpr & (gpr - 1)) == 0 ? (uint32_t)__builtin_ctz(gpr) : 32u;
+    hipLaunchKernelGGL(prefill_swiglu_quant_kernel, dim3((groups + 16 * SWQ_GPT - 1) / (16 * SWQ_GPT)), dim3(256), 0,
+                       stream, pb.hidden, P, I, gpr_shift, pb.silu, mb.hq, mb.hs, flags);
     timer_end(t, stream);
 
     PrefillArgs da = ga;
