@@ -281,8 +281,10 @@ int pw_expert_bank_shape(const pw_expert_bank *bank, uint32_t *n_experts, uint32
 /* One routed-MoE layer with inputs already in device memory: x [rows x hidden] (x_dtype, 16-byte
  * aligned), route_ids / route_weights [rows x 8] (the reference's RoutingTrace selected/weights,
  * src/text_endpoint.rs:4342-4380; 16-byte aligned), output [rows x hidden] (out_dtype,
- * bf16-rounded). The schedule is built on the device in the reference's BTreeMap order. rows <= 32.
- * Asynchronous on stream; kernel error bits accumulate in the runtime's error word. */
+ * bf16-rounded). The schedule is built on the device in the reference's BTreeMap order (a
+ * one-token mode A layer at hidden 4096, intermediate 2048 ranks its eight routes inside its
+ * kernels instead: the same order, the same rejections). Invalid routes raise PW_FLAG_SCHEDULE.
+ * rows <= 32. Asynchronous on stream; kernel error bits accumulate in the runtime's error word. */
 int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
                         uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
                         const float *route_weights, void *output, uint32_t out_dtype, void *stream);
