@@ -153,15 +153,6 @@ __device__ __forceinline__ uint32_t encode2_e4m3fn(float a, float b)
     return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
 }
 
-// a / scale for the quantisers, from the correctly rounded reciprocal rcp = 1 / scale (one IEEE
-// division per group instead of one per value): q = a * rcp, then Markstein's correction
-// q + (a - q * scale) * rcp with the remainder exact by fused multiply-add (P. Markstein, IBM J.
-// Res. Dev. 34(1), 1990), and the sign of q, which a zero remainder would otherwise drop from -0.
-// Where the quotient is at least 2^-10 this equals a / scale bit for bit; below that it may differ
-// by an ulp, and every value there encodes to an e4m3 zero of the same sign. Used only where a is
-// a bf16 value and scale = max(m, 1e-10) / 448 for a bf16 group absmax m >= |a|: over that whole
-// domain (every such (a, m) pair, 1,065,402,238 of them) the clamped e4m3 codes equal those of the
-// IEEE quotient.
 // round_bf16 where a non-finite result is only flagged and never stored: the same bits for every
 // finite input and for infinities; a NaN may come out as an infinity of its sign (still
 // non-finite). Two instructions fewer than the select that keeps NaN payloads.
@@ -171,6 +162,15 @@ __device__ __forceinline__ float round_bf16_or_nonfinite(float v)
     return f32_from((b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u);
 }
 
+// a / scale for the quantisers, from the correctly rounded reciprocal rcp = 1 / scale (one IEEE
+// division per group instead of one per value): q = a * rcp, then Markstein's correction
+// q + (a - q * scale) * rcp with the remainder exact by fused multiply-add (P. Markstein, IBM J.
+// Res. Dev. 34(1), 1990), and the sign of q, which a zero remainder would otherwise drop from -0.
+// Where the quotient is at least 2^-10 this equals a / scale bit for bit; below that it may differ
+// by an ulp, and every value there encodes to an e4m3 zero of the same sign. Used only where a is
+// a bf16 value and scale = max(m, 1e-10) / 448 for a bf16 group absmax m >= |a|: over that whole
+// domain (every such (a, m) pair, 1,065,402,238 of them) the clamped e4m3 codes equal those of the
+// IEEE quotient.
 __device__ __forceinline__ float quant_ratio_bf16(float a, float scale, float rcp)
 {
     const float q = a * rcp;
@@ -222,6 +222,74 @@ __device__ __forceinline__ void raise_flag(uint32_t *flags, uint32_t bit)
 {
     if (flags)
         __hip_atomic_fetch_or(flags, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Eight consecutive activations (16 bytes of bf16 or 32 of f32) as f32.
+template <typename T>
+__device__ __forceinline__ void load_act8(const T *p, float (&v)[8]);
+template <>
+__device__ __forceinline__ void load_act8<float>(const float *p, float (&v)[8])
+{
+    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+template <>
+__device__ __forceinline__ void load_act8<uint16_t>(const uint16_t *p, float (&v)[8])
+{
+    const uint4 a = *(const uint4 *)p;
+    const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = f32_from(u[i] << 16);
+        v[2 * i + 1] = f32_from(u[i] & 0xffff0000u);
+    }
+}
+
+// Dynamic FP8 quantisation of one 128-column activation group (dynamic_fp8_quantized_group128,
+// kernels/block_fp8_gemv.metal:84-137; CPU dynamic_fp8_activations, src/text_endpoint.rs:3008-3051)
+// by 16 lanes of one wave (lane16 = 0..15, eight consecutive values each): max |finite x| over
+// the group, scale = max(m, 1e-10) / 448, codes = e4m3fn RNE of x / scale clamped to +-448,
+// non-finite values quantised as 0 and flagged with FLAG_QUANT_NONFINITE.
+template <typename T>
+__device__ __forceinline__ void quant_group128_team(const T *__restrict__ x, uint32_t group, uint32_t lane16,
+                                                    uint8_t *__restrict__ codes, float *__restrict__ scales,
+                                                    uint32_t *flags)
+{
+    const size_t base = (size_t)group * 128 + lane16 * 8;
+    float v[8];
+    load_act8<T>(x + base, v);
+    bool fin[8], all = true;
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        fin[i] = finite_f32(v[i]);
+        all &= fin[i];
+        m = fmaxf(m, fin[i] ? fabsf(v[i]) : 0.f);
+    }
+    if (!all)
+        raise_flag(flags, FLAG_QUANT_NONFINITE);
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
+        m = fmaxf(m, __shfl_xor(m, off, 16));
+    const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
+    if (lane16 == 0)
+        scales[group] = scale;
+    // bf16 inputs: one division per group and quant_ratio_bf16 per value (the same codes as x /
+    // scale over every bf16 input); f32 inputs divide each value
+    const float rcp = 1.0f / scale;
+    float n[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if constexpr (sizeof(T) == 2)
+            n[i] = fin[i] ? quant_ratio_bf16(v[i], scale, rcp) : 0.f;
+        else
+            n[i] = fin[i] ? v[i] / scale : 0.f;
+        n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
+    }
+    const uint32_t lo = encode2_e4m3fn(n[0], n[1]) | (encode2_e4m3fn(n[2], n[3]) << 16);
+    const uint32_t hi = encode2_e4m3fn(n[4], n[5]) | (encode2_e4m3fn(n[6], n[7]) << 16);
+    *(uint2 *)(codes + base) = make_uint2(lo, hi);
 }
 
 // Exclusive prefix sum over the workgroup (blockDim.x <= 1024): wave scans with lane shuffles,

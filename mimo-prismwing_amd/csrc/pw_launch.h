@@ -190,11 +190,21 @@ struct PfTileTable {
 // Bytes of MoeBuffers::sched the schedule of `rows` token rows over E experts needs (0 for the
 // batches scheduled in one workgroup).
 size_t moe_sched_scratch_bytes(uint32_t rows, uint32_t E);
-// With tiles, the schedules of long batches also write the prefill's m-tile table (returns true;
-// false: the caller builds it).
+// Activation rows [rows][K] (f32 or bf16) for the dynamic FP8 quantiser: codes [rows][K] e4m3 and
+// scales [rows][K / 128].
+struct QuantJob {
+    const void *x;
+    uint32_t f32, rows, K;
+    uint8_t *codes;
+    float *scales;
+};
+// Returns true when the batch took the long-batch schedule, which also writes the prefill's
+// m-tile table when given tiles and quantises `quant` when given (in the same launch as its plan);
+// false: the caller launches both itself.
 bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
                          uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
-                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles = nullptr);
+                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles = nullptr,
+                         const QuantJob *quant = nullptr);
 // expert_offsets [E + 1]: expert e's placement slots are [off[e], off[e + 1]) (after a schedule).
 void launch_expert_offsets(const MoeBuffers &mb, uint32_t E, uint32_t *expert_offsets, hipStream_t stream);
 // One token's routes for a mode A layer launched without a schedule (moe_a_one_token_direct).
@@ -229,10 +239,11 @@ void launch_silu_table(uint16_t *table, hipStream_t stream);
 void launch_swiglu_staged(const float *gate, const float *up, uint32_t n, const uint16_t *silu_table, float *out,
                           uint32_t *flags, hipStream_t stream);
 uint32_t prefill_max_tiles(uint32_t rows, uint32_t E);
-// tiles_built: the schedule wrote pb's m-tile table (launch_moe_schedule returned true).
+// scheduled_long: launch_moe_schedule returned true for this batch, given pb's tile table and the
+// QuantJob of x into mb.xq / mb.xs (the m-tile table and the activation codes are in place).
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,
-                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream, bool tiles_built);
+                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream, bool scheduled_long);
 
 void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, const ExpertPtrs &ep, uint32_t expert,
                            const MoeBuffers &mb,

@@ -269,76 +269,16 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_b_kernel(
 // dynamic_fp8_activations (src/text_endpoint.rs:3008-3051): scale = max(absmax, 1e-10) / 448;
 // code = nearest e4m3 of clamp(x/scale). A non-finite input raises FLAG_QUANT_NONFINITE and
 // counts as 0 in the group maximum.
-// Eight consecutive activations (16 bytes of bf16 or 32 of f32) as f32.
-template <typename T>
-__device__ __forceinline__ void load_act8(const T *p, float (&v)[8]);
-template <>
-__device__ __forceinline__ void load_act8<float>(const float *p, float (&v)[8])
-{
-    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
-template <>
-__device__ __forceinline__ void load_act8<uint16_t>(const uint16_t *p, float (&v)[8])
-{
-    const uint4 a = *(const uint4 *)p;
-    const uint32_t u[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        v[2 * i] = f32_from(u[i] << 16);
-        v[2 * i + 1] = f32_from(u[i] & 0xffff0000u);
-    }
-}
-
-// One 128-column group per 16 lanes (eight consecutive values per lane, 16 groups per 256-thread
-// workgroup): max |finite x| over the group, scale = max(m, 1e-10) / 448, codes = e4m3fn RNE of
-// x / scale clamped to +-448, non-finite values quantised as 0 and flagged.
+// One 128-column group per 16 lanes, 16 groups per 256-thread workgroup (quant_group128_team).
 template <typename T>
 __global__ __launch_bounds__(256) void quant_group128_kernel(const T *__restrict__ x, uint32_t rows,
                                                              uint32_t K, uint8_t *__restrict__ codes,
                                                              float *__restrict__ scales,
                                                              uint32_t *flags)
 {
-    const uint32_t lane16 = threadIdx.x & 15;
-    const uint32_t groups_per_row = K >> 7;
     const uint32_t group = blockIdx.x * 16 + (threadIdx.x >> 4);
-    if (group >= rows * groups_per_row)  // whole 16-lane groups leave together
-        return;
-    const size_t base = (size_t)group * 128 + lane16 * 8;
-    float v[8];
-    load_act8<T>(x + base, v);
-    bool fin[8], all = true;
-    float m = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        fin[i] = finite_f32(v[i]);
-        all &= fin[i];
-        m = fmaxf(m, fin[i] ? fabsf(v[i]) : 0.f);
-    }
-    if (!all)
-        raise_flag(flags, FLAG_QUANT_NONFINITE);
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
-        m = fmaxf(m, __shfl_xor(m, off, 16));
-    const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
-    if (lane16 == 0)
-        scales[group] = scale;
-    // bf16 inputs: one division per group and quant_ratio_bf16 per value (the same codes as x /
-    // scale over every bf16 input); f32 inputs divide each value
-    const float rcp = 1.0f / scale;
-    float n[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if constexpr (sizeof(T) == 2)
-            n[i] = fin[i] ? quant_ratio_bf16(v[i], scale, rcp) : 0.f;
-        else
-            n[i] = fin[i] ? v[i] / scale : 0.f;
-        n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
-    }
-    const uint32_t lo = encode2_e4m3fn(n[0], n[1]) | (encode2_e4m3fn(n[2], n[3]) << 16);
-    const uint32_t hi = encode2_e4m3fn(n[4], n[5]) | (encode2_e4m3fn(n[6], n[7]) << 16);
-    *(uint2 *)(codes + base) = make_uint2(lo, hi);
+    if (group < rows * (K >> 7))  // whole 16-lane groups leave together
+        quant_group128_team<T>(x, group, threadIdx.x & 15, codes, scales, flags);
 }
 
 // f32 [n] -> bf16 planes hi [n], mid [n], lo [n] with x == hi + mid + lo.

@@ -223,7 +223,8 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
 //     writes the (expert, 32-row word) bitmap words and their popcounts;
 //   moe_sched_plan_kernel: one workgroup forms each expert's count and per-word prefix counts,
 //     the slot offsets and routed-expert tables (block scans in ascending expert id), the largest
-//     count and the plan;
+//     count and the plan; its other workgroups, when given a QuantJob, quantise the activation
+//     rows (64 groups of 128 columns each) on the CUs the one plan workgroup leaves idle;
 //   moe_sched_place_kernel: one thread per token row writes its eight placements at
 //     offset[e] + prefix[e][word] + (bits below the row in its word) -- ascending rows per
 //     expert, as in moe_schedule_kernel -- and the token row of each of an expert's first 16
@@ -313,8 +314,18 @@ __global__ __launch_bounds__(1024) void moe_sched_plan_kernel(
     const ExpertPtrs *__restrict__ bank, uint32_t rows, uint32_t E, uint32_t max_active, SchedScratch ss,
     MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
     ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
-    uint32_t *__restrict__ row_slots, uint32_t *flags, PfTileTable tt)
+    uint32_t *__restrict__ row_slots, uint32_t *flags, PfTileTable tt, QuantJob qj)
 {
+    if (blockIdx.x > 0) {
+        const uint32_t group = (blockIdx.x - 1) * 64 + (threadIdx.x >> 4);
+        if (group < qj.rows * (qj.K >> 7)) {  // whole 16-lane groups leave together
+            if (qj.f32)
+                quant_group128_team((const float *)qj.x, group, threadIdx.x & 15, qj.codes, qj.scales, flags);
+            else
+                quant_group128_team((const uint16_t *)qj.x, group, threadIdx.x & 15, qj.codes, qj.scales, flags);
+        }
+        return;
+    }
     __shared__ uint32_t s_scan[48], s_bad, s_max;
     const uint32_t tid = threadIdx.x, e = tid;
     const uint32_t W = (rows + 31) >> 5, Wp = (W + 15) & ~15u, nwg = (rows + 63) >> 6;
@@ -1054,9 +1065,9 @@ __global__ __launch_bounds__(256) void round_output_kernel(const float *__restri
 // ------------------------------------------------------------------------------- launchers
 bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
                          uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
-                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles)
+                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles, const QuantJob *quant)
 {
-    bool tiles_built = false;
+    bool long_batch = false;
     const uint32_t words = (rows + 31) >> 5;
     size_t lds = (size_t)(E * words + E) * sizeof(uint32_t);
     const size_t with_prefix_lds = lds + (size_t)E * words * sizeof(uint16_t);
@@ -1087,15 +1098,17 @@ bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
         hipLaunchKernelGGL(moe_sched_mark_kernel, dim3(nwg), dim3(64), (size_t)E * 8, stream, ids, weights, rows, E,
                            ss);
         const PfTileTable tt = tiles ? *tiles : PfTileTable{nullptr, nullptr, 0};
-        hipLaunchKernelGGL(moe_sched_plan_kernel, dim3(1), dim3(1024), 0, stream, bank, rows, E, max_active, ss,
-                           mb.plan, mb.active_expert, mb.active_offset, mb.active, mb.placement_pos,
-                           mb.placement_w, mb.row_slots, flags, tt);
-        tiles_built = tiles != nullptr;
+        const QuantJob qj = quant ? *quant : QuantJob{};
+        const uint32_t quant_wgs = (qj.rows * (qj.K >> 7) + 63) / 64;
+        hipLaunchKernelGGL(moe_sched_plan_kernel, dim3(1 + quant_wgs), dim3(1024), 0, stream, bank, rows, E,
+                           max_active, ss, mb.plan, mb.active_expert, mb.active_offset, mb.active,
+                           mb.placement_pos, mb.placement_w, mb.row_slots, flags, tt, qj);
+        long_batch = true;
         hipLaunchKernelGGL(moe_sched_place_kernel, dim3(nwg), dim3(64), 0, stream, ids, weights, rows, E, max_active,
                            ss, mb.plan, mb.active, mb.placement_pos, mb.placement_w, mb.row_slots);
     }
     timer_end(t, stream);
-    return tiles_built;
+    return long_batch;
 }
 
 // Mode A: gate/up (+SwiGLU) then down, both as split-K expert projections (pw_moe_a.hip).

@@ -49,6 +49,12 @@ static_assert(PF_MT % 16 == 0 && PF_MT > 64 && PF_MT <= 128, "two 64-slot token 
 constexpr uint32_t PF_UNITS = 8;                  // 16-byte units per 128-byte token row of a step
 constexpr int PF_CONS = 8;                        // consumer waves per workgroup, 16 RG weight rows each
 constexpr int PF_WAVES = PF_CONS + 1;             // and one producer wave (the codes ring)
+// Gate/up workgroups start their K loop at column step blockIdx % nsteps (and wrap), so the
+// workgroups in flight, which advance through K at about the same rate, read different offsets of
+// their weight rows instead of all the same 256 bytes of rows 4 KB apart (with every workgroup in
+// step, the gate/up GEMM ran 13% slower for some physical placements of the bank; down, with
+// four n-tiles per workgroup, does not need it).
+constexpr bool PF_ROTATE_GATEUP = true, PF_ROTATE_DOWN = false;
 constexpr uint32_t PF_BLK = PF_MT * PF_UNITS;     // 16-byte code units per 128-column block
 static_assert(PF_BLK % 64 == 0, "a block's codes are whole 64-lane copies");
 
@@ -207,12 +213,20 @@ struct PfTile {
     const uint8_t *mat0, *mat1; // output columns [0, R1): rows of mat0 (gate or down), [R1, R): mat1 (up)
     uint16_t *out;             // the wave's first output: slot0 row, column col0 + wave * 16 RG
     uint32_t K, R, R1, nsteps, n_sub;
+    uint32_t rot;              // K step order: loop step k reads column step (k + rot) % nsteps
     uint32_t wcol;             // the wave's first output column in the first n-tile
     uint32_t loff;             // the lane's weight offset: r16 rows and 16 q columns
     uint32_t cnt;              // placement slots of the m-tile
     const uint8_t *codes;      // activation codes [rows][K] (the producer's)
     uint32_t *lds_tok;         // [PF_MT] token rows of the m-tile's slots, written by the producer
 };
+
+// Column step of loop step k < nsteps (wave-uniform).
+__device__ __forceinline__ uint32_t pf_col_step(const PfTile &tl, uint32_t k)
+{
+    const uint32_t c = k + tl.rot;
+    return c >= tl.nsteps ? c - tl.nsteps : c;
+}
 
 // Wave-uniform address of the wave's first weight row in n-tile sub: column wcol + sub * NROWS is
 // row col - R1 of mat1 when col >= R1, else row col of mat0 (columns past R, of a partial last
@@ -262,7 +276,7 @@ __device__ __forceinline__ void pf_produce(const PfTile &tl, const uint32_t (&to
     const uint32_t total = tl.n_sub * nsteps, tlast = total - 1;
     const auto copy_step = [&](uint32_t s) {
         uint4 *slot = tl.ring + (s % C::D) * C::STEP;
-        const uint32_t k0 = ((s < tlast ? s : tlast) % nsteps) * (128 * C::SB);
+        const uint32_t k0 = pf_col_step(tl, (s < tlast ? s : tlast) % nsteps) * (128 * C::SB);
         for (uint32_t c = 0; c < nc; ++c) {
             const uint32_t t = 8 * c + ((uint32_t)lane >> 3);
             const uint32_t row = __shfl(c < 8 ? tok[0] : tok[1], (int)(t & 63), 64);
@@ -307,7 +321,8 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, int wave, int lane)
     PfW<C> w[C::WS];
 #pragma unroll
     for (int i = 0; i < C::WS; ++i)
-        pf_issue_w<C>(w[i], rows + ((uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB), loff, rstride);
+        pf_issue_w<C>(w[i], rows + pf_col_step(tl, (uint32_t)i < last ? (uint32_t)i : last) * (128 * C::SB), loff,
+                      rstride);
     // the lane's code units of token r16 in a block: units q and q + 4, swizzled by token % 8 (the
     // same for token r16 + 16 j); opaque to the compiler, which would otherwise fold the tile
     // offsets into one address register per tile and half instead of immediate offsets
@@ -334,8 +349,9 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, int wave, int lane)
         // weights of step kk: this n-tile's, or past its last step the next n-tile's first ones
         const auto next_src = [&](uint32_t k) {
             const uint32_t kk = k + C::WS;
-            return kk <= last ? rows + kk * (128 * C::SB)
-                              : (more ? nrows + (kk - nsteps) * (128 * C::SB) : rows + last * (128 * C::SB));
+            return kk <= last ? rows + pf_col_step(tl, kk) * (128 * C::SB)
+                              : (more ? nrows + pf_col_step(tl, kk - nsteps) * (128 * C::SB)
+                                      : rows + pf_col_step(tl, last) * (128 * C::SB));
         };
 
         // Step k: barrier (slot k % C::D published), compute from weight slot k % C::WS, each
@@ -349,8 +365,8 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, int wave, int lane)
             for (int i = 0; i < C::G; ++i) {
                 const uint32_t k = b + i;
                 lds_barrier();
-                pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, wsc, k, r16,
-                                  next_src(k), loff, rstride, cl0, cl1);
+                pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, wsc,
+                                  pf_col_step(tl, k), r16, next_src(k), loff, rstride, cl0, cl1);
             }
         }
 #pragma unroll
@@ -359,8 +375,8 @@ __device__ __forceinline__ void pf_body(const PfTile &tl, int wave, int lane)
             if (k >= nsteps)
                 break;
             lds_barrier();
-            pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, wsc, k, r16,
-                              next_src(k), loff, rstride, cl0, cl1);
+            pf_compute<C, NT>(tot, w[i % C::WS], tl.ring + (i % C::D) * C::STEP, tl.lds_scale, wsc,
+                              pf_col_step(tl, k), r16, next_src(k), loff, rstride, cl0, cl1);
         }
 
         // epilogue: lane holds rows 16 g + 4q + i of the wave's 16 RG for tokens 16j + r16 -> bf16,
@@ -488,6 +504,7 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
     tile.R1 = args.R1;
     tile.nsteps = nsteps;
     tile.n_sub = n_sub;
+    tile.rot = (gather ? PF_ROTATE_GATEUP : PF_ROTATE_DOWN) ? blockIdx.x % nsteps : 0u;
     tile.wcol = col0 + wrow0;
     tile.loff = (uint32_t)r16 * K + (uint32_t)q * 16;
     tile.cnt = cnt_t;
@@ -729,16 +746,17 @@ static void launch_prefill_projection(const PrefillArgs &a, uint32_t nsub, hipSt
 
 void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const PrefillBuffers &pb, const void *x,
                         bool x_f32, uint32_t rows, uint32_t E, uint32_t H, uint32_t I, float *out_f32,
-                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream, bool tiles_built)
+                        uint16_t *out_bf16, bool raw, uint32_t *flags, hipStream_t stream, bool scheduled_long)
 {
     (void)bank;
     const uint32_t P = rows * 8;
     const uint32_t max_active = E < P ? E : P;
     const uint32_t max_tiles = prefill_max_tiles(rows, E);
-    launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
-    if (!tiles_built)
+    if (!scheduled_long) {
+        launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
         hipLaunchKernelGGL(prefill_tiles_kernel, dim3(1), dim3(1024), 0, stream, mb.plan, mb.active, max_active,
                            pb.tiles, max_tiles, pb.n_tiles, flags);
+    }
 
     // gate and up as one stacked projection of 2I output columns per slot
     PrefillArgs ga{};

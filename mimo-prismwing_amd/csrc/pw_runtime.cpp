@@ -1408,12 +1408,13 @@ int pw_moe_prefill_device(pw_runtime *rt, const pw_expert_bank *bank, const void
     pb.silu = (const uint16_t *)rt->pf_silu.p;
     const uint32_t P = rows * 8;
     const pw::PfTileTable tt{pb.tiles, pb.n_tiles, max_tiles};
-    const bool tiles_built = pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E,
-                                                     std::min<uint32_t>(E, P), rt->mb, rt->d_flags, s, &tt);
+    const pw::QuantJob qj{x, x_dtype == PW_DTYPE_F32 ? 1u : 0u, rows, H, rt->mb.xq, rt->mb.xs};
+    const bool scheduled_long = pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E,
+                                                        std::min<uint32_t>(E, P), rt->mb, rt->d_flags, s, &tt, &qj);
     pw::launch_moe_prefill(bank->table, rt->mb, pb, x, x_dtype == PW_DTYPE_F32, rows, E, H, I,
                            out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
                            out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr,
-                           out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s, tiles_built);
+                           out_dtype == PW_DTYPE_F32_RAW, rt->d_flags, s, scheduled_long);
     PW_HIP(hipGetLastError());
     return PW_OK;
 }
