@@ -272,11 +272,12 @@ __device__ __forceinline__ void quant_group128_team(const T *__restrict__ x, uin
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
         m = fmaxf(m, __shfl_xor(m, off, 16));
-    const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
+    // bf16 inputs: a bf16 maximum, so the scale needs no division (scale_of_bf16_max), one
+    // division per group for the reciprocal and quant_ratio_bf16 per value (the same codes as
+    // x / scale over every bf16 input); f32 inputs divide each value
+    const float scale = sizeof(T) == 2 ? scale_of_bf16_max(m) : fmaxf(m, 1.0e-10f) / 448.0f;
     if (lane16 == 0)
         scales[group] = scale;
-    // bf16 inputs: one division per group and quant_ratio_bf16 per value (the same codes as x /
-    // scale over every bf16 input); f32 inputs divide each value
     const float rcp = 1.0f / scale;
     float n[8];
 #pragma unroll

@@ -768,7 +768,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void moe_b_gateup_kernel(
     __shared__ f32x4 red_g[KSPLIT][NT][64];
     __shared__ f32x4 red_u[KSPLIT][NT][64];
     const uint32_t tiles_per_expert = I >> 4;
-    const uint32_t a = blockIdx.x / tiles_per_expert, rt = blockIdx.x % tiles_per_expert;
+    // XCD x (workgroup i runs on XCD i % 8) takes a contiguous eighth of each expert's row tiles
+    const uint32_t a = blockIdx.x / tiles_per_expert, lt = blockIdx.x % tiles_per_expert;
+    const uint32_t rt = tiles_per_expert % 8 == 0 ? (lt % 8) * (tiles_per_expert / 8) + lt / 8 : lt;
     const ExpertTile et = expert_tile(plan, active_expert, active_offset, bank, a);
     if (!et.live)
         return;

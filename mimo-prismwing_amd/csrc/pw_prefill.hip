@@ -565,6 +565,22 @@ void launch_swiglu_staged(const float *gate, const float *up, uint32_t n, const 
 
 constexpr int SWQ_GPT = 2;  // 128-column groups per 16-lane team of prefill_swiglu_quant_kernel
 
+// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r + 15 of a wave): swaps within quads,
+// then the half-row and row mirrors, each a v_max_f32 with a DPP operand (no LDS permute).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float m)
+{
+    m = fmaxf(m, dpp_f32<0xb1>(m));   // quad_perm [1, 0, 3, 2]
+    m = fmaxf(m, dpp_f32<0x4e>(m));   // quad_perm [2, 3, 0, 1]
+    m = fmaxf(m, dpp_f32<0x141>(m));  // row_half_mirror
+    m = fmaxf(m, dpp_f32<0x140>(m));  // row_mirror
+    return m;
+}
+
 // bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343)
 // on the bf16 gate/up outputs, h = round(round(g / (1 + e^-g)) * u), fused with the dynamic
 // per-(slot, 128-column group) re-quantisation of h for the down projection
@@ -618,31 +634,46 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
         if (group0 + j >= n_groups)
             break;
         float h[8];
+        uint32_t ge = 0;  // the largest exponent field of the lane's h values
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const uint32_t ub = uw[j][i >> 1];
             const float uv = f32_from((i & 1) ? (ub & 0xffff0000u) : (ub << 16));
             // a non-finite h is flagged and coded 0, so its NaN payload never matters
             h[i] = round_bf16_or_nonfinite(f32_from(sb[j][i] << 16) * uv);
-            emax = max(emax, f32_bits(h[i]) & 0x7f800000u);
+            ge = max(ge, f32_bits(h[i]) & 0x7f800000u);
         }
+        emax = max(emax, ge);
+        // every h of the wave finite (the usual case, a wave-uniform branch): no per-value selects
+        const bool all_finite = __ballot(ge == 0x7f800000u) == 0;
         float m = 0.f;
+        if (all_finite) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            m = fmaxf(m, finite_f32(h[i]) ? fabsf(h[i]) : 0.f);
+            for (int i = 0; i < 8; ++i)
+                m = fmaxf(m, fabsf(h[i]));
+        } else {
 #pragma unroll
-        for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
-            m = fmaxf(m, __shfl_xor(m, off, 16));
-        const float scale = fmaxf(m, 1.0e-10f) / 448.0f;
+            for (int i = 0; i < 8; ++i)
+                m = fmaxf(m, finite_f32(h[i]) ? fabsf(h[i]) : 0.f);
+        }
+        m = row16_max(m);  // the group's 16 lanes form one DPP row
+        const float scale = scale_of_bf16_max(m);  // m is a bf16 value
         if (lane16 == 0)
             scales[group0 + j] = scale;
         const float rcp = 1.0f / scale;  // h is bf16: one division per group (quant_ratio_bf16)
         float n[8];
+        if (all_finite) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            n[i] = finite_f32(h[i]) ? quant_ratio_bf16(h[i], scale, rcp) : 0.f;
-            n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
+            for (int i = 0; i < 8; ++i)
+                n[i] = quant_ratio_bf16(h[i], scale, rcp);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                n[i] = finite_f32(h[i]) ? quant_ratio_bf16(h[i], scale, rcp) : 0.f;
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            n[i] = fminf(fmaxf(n[i], -448.f), 448.f);  // n is finite: the same as the clamp by comparisons
         uint32_t packed[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
