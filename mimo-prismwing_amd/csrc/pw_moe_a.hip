@@ -232,11 +232,12 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     // Workgroup i runs on XCD i % 8. XCD x takes the contiguous row groups [x G/8, (x + 1) G/8) of
     // each routed expert (1 MB of gate and 1 MB of up at G = 128), not every eighth 16-row group:
     // the strided form gave each XCD's loads a common set of address bits and ran 4% slower, and
-    // up to 7% slower for some physical placements of the bank. Which workgroup computes which
-    // rows does not change any sum.
+    // up to 7% slower for some physical placements of the bank. A lone expert (the one-expert
+    // forward, the dense MLP) keeps the strided order, which measured 1 µs faster there. Which
+    // workgroup computes which rows does not change any sum.
     const uint32_t G = args.R / RM;
     const uint32_t a = blockIdx.x / G, local = blockIdx.x % G;
-    const uint32_t g = G % 8 == 0 ? (local % 8) * (G / 8) + local / 8 : local;
+    const uint32_t g = G % 8 == 0 && !args.single ? (local % 8) * (G / 8) + local / 8 : local;
     const ActiveExpert ae = args.single ? args.one : (args.route_ids ? route_entry(args, a) : args.active[a]);
     if (ae.cnt == 0)
         return;
