@@ -253,15 +253,43 @@ def closed_form_two_step(rt):
 
 @pytest.mark.parametrize("rows", [9, 144])
 def test_closed_form_prefill_two_steps_bit_exact(rt, closed_form_two_step, rows):
-    """Hidden 512, intermediate 512, top-8 of 8 experts: two 256-column K steps per projection, so
-    a prefill workgroup runs two n-tiles of its m-tile in a row (gate/up four n-tiles, down two),
-    the second n-tile's first weights loaded during the first one's last steps; 144 rows give each
-    expert a full 128-slot m-tile and a 16-slot one. Bit for bit the oracle's layer."""
+    """Hidden 512, intermediate 512, top-8 of 8 experts: two 256-column K steps per projection (the
+    gate/up workgroups start at either step and wrap); 144 rows give each expert a full 128-slot
+    m-tile and a 16-slot one. Bit for bit the oracle's layer."""
     experts, x, sel, w, _, bank = closed_form_two_step
     x, sel, w = x[:rows], sel[:rows], w[:rows]
     want, want_raw = O.moe_layer("b", x, experts, 8, sel, w, raw=True)
     _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW, prefill=True), want_raw)
     _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16, prefill=True), want)
+
+
+@pytest.fixture(scope="module")
+def closed_form_wide(rt):
+    experts, x, sel, w = closed_form_mode_b(0x50570400, 40, 8, hidden=4096, inter=512)
+    projs, bank = _bank_from(rt, experts, 8)
+    return experts, x, sel, w, projs, bank
+
+
+@pytest.mark.parametrize("rows", [1, 40])
+def test_closed_form_prefill_production_steps_bit_exact(rt, closed_form_wide, rows):
+    """Hidden 4096 (the production hidden size), intermediate 512, top-8 of 8 experts: the gate/up
+    GEMM's sixteen 256-column K steps, each workgroup starting at its own step and wrapping, and
+    the down GEMM's sixteen 256-row n-tiles of two K steps, four per workgroup with the next
+    n-tile's first weights loaded during the last steps of the one before. Bit for bit the
+    oracle's layer."""
+    experts, x, sel, w, _, bank = closed_form_wide
+    x, sel, w = x[:rows], sel[:rows], w[:rows]
+    want, want_raw = O.moe_layer("b", x, experts, 8, sel, w, raw=True)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW, prefill=True), want_raw)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16, prefill=True), want)
+
+
+def test_closed_form_mode_b_device_layer_wide_hidden_bit_exact(rt, closed_form_wide):
+    """The mode-B decode layer (eight rows) on the hidden-4096 closed form, bit for bit."""
+    experts, x, sel, w, _, bank = closed_form_wide
+    x, sel, w = x[:8], sel[:8], w[:8]
+    want, want_raw = O.moe_layer("b", x, experts, 8, sel, w, raw=True)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW), want_raw)
 
 
 @pytest.fixture(scope="module")

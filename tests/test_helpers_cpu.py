@@ -65,3 +65,11 @@ def test_closed_form_odd_hidden_blocks_meets_its_preconditions():
     experts, x, sel, w = closed_form_mode_b(0x50570200, 96, 12, hidden=384, check=True)
     out = O.moe_layer("b", x[:4], experts, 12, sel[:4], w[:4])
     assert np.all(np.isfinite(out)) and np.any(out)
+
+
+def test_closed_form_wide_hidden_meets_its_preconditions():
+    """The hidden-4096, intermediate-512 closed form (the prefill gate/up's sixteen rotated K steps,
+    the down projection's four n-tiles per workgroup) at the GPU test's seed and size."""
+    experts, x, sel, w = closed_form_mode_b(0x50570400, 40, 8, hidden=4096, inter=512, check=True)
+    out = O.moe_layer("b", x[:2], experts, 8, sel[:2], w[:2])
+    assert np.all(np.isfinite(out)) and np.any(out)
