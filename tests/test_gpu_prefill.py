@@ -142,6 +142,23 @@ def test_prefill_matches_decode_chunks(rt, full_bank, rows, zipf):
     assert normwise(got[pick], ref) <= MODE_B_TOL
 
 
+@pytest.mark.parametrize("zipf", [False, True])
+def test_prefill_is_deterministic(rt, full_bank, zipf):
+    """The same 2048-token batch gives the same raw f32 bits twice, with another batch (300 rows, a
+    different schedule, m-tile table and scratch contents) run on the runtime in between: no result
+    depends on the timing of the plan launch's quantiser workgroups, the rotated K order of the
+    gate/up workgroups or what the scratch held before."""
+    import torch
+    x = WL.activations(2048, WL.SEED_BASE + 4)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
+    sel, w, _ = WL.route_host(x, rw, bias)
+    first = _prefill(rt, torch, full_bank, x, sel, w, out_dtype=P.DTYPE_F32_RAW)
+    _prefill(rt, torch, full_bank, x[:300][::-1].copy(), sel[:300], w[:300], out_dtype=P.DTYPE_F32_RAW)
+    again = _prefill(rt, torch, full_bank, x, sel, w, out_dtype=P.DTYPE_F32_RAW)
+    assert np.array_equal(first.view(np.uint32), again.view(np.uint32))
+    assert np.all(np.isfinite(first)) and np.any(first)
+
+
 def test_prefill_rejects_bad_arguments(rt, small_bank):
     import torch
     x = torch.zeros((8, 256), dtype=torch.int16, device="cuda")
