@@ -235,6 +235,35 @@ def test_decode_layer_256_experts_width8(rt, full_bank, zipf):
             assert normwise(got16, ref) <= 2e-2 and rel_l2(got16, ref) <= 5e-3
 
 
+def test_decode_layer_is_deterministic(rt, full_bank):
+    """The width-8 layer gives the same raw f32 bits for the same batch twice, modes A and B, with a
+    different batch (other routes, so another schedule and other pieces) run in between."""
+    import torch
+    stream = torch.cuda.current_stream().cuda_stream
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    batches = []
+    for seed in (WL.SEED_BASE + 2, WL.SEED_BASE + 40):
+        x = WL.activations(8, seed)
+        _, _, sel, w, _ = O.route(x, rw, bias)
+        batches.append((torch.from_numpy(WL.bf16_bits_np(x).view(np.int16)).cuda(),
+                        torch.from_numpy(sel.astype(np.int32)).cuda(), torch.from_numpy(w).cuda()))
+
+    def layer(b, mode):
+        xt, ids, wts = b
+        raw = torch.empty((8, 4096), dtype=torch.float32, device="cuda")
+        rt.moe_layer_device(full_bank.bank, xt, 8, ids, wts, raw, mode=mode, out_dtype=P.DTYPE_F32_RAW, stream=stream)
+        torch.cuda.synchronize()
+        assert rt.take_flags() == 0
+        return raw.cpu().numpy()
+
+    for mode in (P.MODE_A, P.MODE_B):
+        first = layer(batches[0], mode)
+        layer(batches[1], mode)
+        again = layer(batches[0], mode)
+        assert np.array_equal(first.view(np.uint32), again.view(np.uint32))
+        assert np.all(np.isfinite(first)) and np.any(first)
+
+
 def test_whole_k_gateup_matches_split_k(rt, full_bank):
     """At hidden 4096 a batch of up to 8 bf16 rows takes the whole-K gate/up kernel (SwiGLU fused, no
     split partials in memory); 9 rows take the split-K kernel plus the SwiGLU kernel. Each token's
