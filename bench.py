@@ -77,6 +77,33 @@ def gateup_bytes(sel, rows, hidden=4096, inter=2048):
 SETTLE_S = 0.3
 
 
+def percentile(ordered, fraction):
+    """The reference's wall-time percentile (src/lib.rs:1754-1761): the sorted sample at index
+    round((n - 1) * fraction)."""
+    return ordered[int(round((len(ordered) - 1) * fraction))]
+
+
+def timed_steps(torch, stream, run, steps):
+    """Mean step time (ms) of `steps` back-to-back steps bracketed by one event pair, then the same
+    steps again with an event between consecutive steps: their p10 / median / p90 in µs, the
+    reference's summary of a timing sample. Both passes queue behind the caller's warm-up work."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        run(i)
+    end.record(stream)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    marks[0].record(stream)
+    for i in range(steps):
+        run(i)
+        marks[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(1000.0 * marks[i].elapsed_time(marks[i + 1]) for i in range(steps))
+    spread = {"p10_us": round(percentile(per, 0.10), 2), "median_us": round(percentile(per, 0.50), 2),
+              "p90_us": round(percentile(per, 0.90), 2), "samples": steps}
+    return start.elapsed_time(end) / steps, spread
+
+
 def settle(torch, run, seconds=SETTLE_S):
     """Runs the workload untimed for `seconds` of wall time. The GPU lowers its clocks while it idles
     (host-side set-up between legs): 20 layer steps timed right after such a pause measured 285-287
@@ -107,22 +134,17 @@ def time_layer(torch, rt, bank, P, dev_batches, rows, steps, warmup, mode, settl
         run(i)
     # the start event queues behind the warm-up steps: the timed steps start on a busy GPU, with
     # no drained queue or idle gap in front of them
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(steps):
-        run(i)
-    end.record(stream)
-    torch.cuda.synchronize()
+    ms, spread = timed_steps(torch, stream, run, steps)
     flags = rt.take_flags()
     if flags:
         raise RuntimeError(f"kernels raised error flags {flags}")
-    return start.elapsed_time(end) / steps
+    return ms, spread
 
 
 def kernel_times(torch, rt, bank, P, dev_batches, rows, steps, mode):
     """Per-kernel durations from HIP events recorded on the launch stream inside the library."""
-    time_layer(torch, rt, bank, P, dev_batches, rows, 1, 0, mode)  # settles the clocks
-    rt.enable_timing(steps * 8)
+    time_layer(torch, rt, bank, P, dev_batches, rows, 2, 0, mode)  # settles the clocks
+    rt.enable_timing(steps * 16)  # two passes of up to eight launches per step
     time_layer(torch, rt, bank, P, dev_batches, rows, steps, 0, mode, settle_first=False)
     res = {}
     for k in ("moe_schedule", "quant", "moe_gateup", "moe_swiglu", "moe_down", "moe_combine"):
@@ -156,15 +178,9 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
     settle(torch, run)
     for _ in range(warmup):
         run()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        run()
-    end.record(stream)
-    torch.cuda.synchronize()
+    ms, spread = timed_steps(torch, stream, run, steps)
     if rt.take_flags():
         raise RuntimeError("prefill kernels raised error flags")
-    ms = start.elapsed_time(end) / steps
     rt.enable_timing(steps * 8)
     for _ in range(steps):
         run()
@@ -179,7 +195,7 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
     wbytes = u * (EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES)
     tflops = flops / (ms * 1e-3) / 1e12
     counts = np.bincount(sel.reshape(-1), minlength=256)
-    return {"layer_us": round(ms * 1000, 2), "TFLOP/s": round(tflops, 1),
+    return {"layer_us": round(ms * 1000, 2), "spread_us": spread, "TFLOP/s": round(tflops, 1),
             "fp8_peak_frac": round(tflops / FP8_PEAK_TFLOPS, 4),
             "weight_GB/s": round(wbytes / (ms * 1e-3) / 1e9, 1), "unique_experts": u,
             "max_count": int(counts.max()), "m_tiles_128": int(np.sum((counts + 127) // 128)),
@@ -188,20 +204,15 @@ def prefill_leg(torch, rt, bank, P, WL, zipf, steps=20, warmup=3):
 
 
 def _time_calls(torch, rt, run, n_calls, warmup=3):
-    """µs per call of `run(i)` over n_calls back-to-back calls on the runtime's stream."""
+    """(µs per call, spread) of `run(i)` over n_calls back-to-back calls on the runtime's stream."""
     stream = torch.cuda.ExternalStream(rt.stream)
     settle(torch, lambda i: run(i, stream.cuda_stream), 0.1)
     for i in range(warmup):
         run(i, stream.cuda_stream)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(n_calls):
-        run(i, stream.cuda_stream)
-    end.record(stream)
-    torch.cuda.synchronize()
+    ms, spread = timed_steps(torch, stream, lambda i: run(i, stream.cuda_stream), n_calls)
     if rt.take_flags():
         raise RuntimeError("kernels raised error flags")
-    return 1000.0 * start.elapsed_time(end) / n_calls
+    return 1000.0 * ms, spread
 
 
 def _bf16_x(torch, WL, rows, hidden, seed):
@@ -227,9 +238,10 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
     y = torch.empty((1, n), dtype=torch.int16, device="cuda")
     alg = n * k + (n // 128) * (k // 128) * 4 + k * 2 + n * 2
     for label, pick in (("hbm_cold", lambda i: projs[i % copies]), ("mall_warm", lambda i: projs[0])):
-        us = _time_calls(torch, rt, lambda i, st: rt.fp8_linear_device(pick(i), x, 1, y, mode=P.MODE_A,
-                                                                     out_dtype=P.DTYPE_BF16, stream=st), calls)
-        out.setdefault("config0_w1", {})[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+        us, sp = _time_calls(torch, rt, lambda i, st: rt.fp8_linear_device(pick(i), x, 1, y, mode=P.MODE_A,
+                                                                         out_dtype=P.DTYPE_BF16, stream=st), calls)
+        out.setdefault("config0_w1", {})[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1),
+                                                   "spread_us": sp}
     out["config0_w1"]["algorithmic_bytes"] = alg
     del projs, w, s
     # config 1: one complete expert (gate/up [2 x 2048 x 4096], down [4096 x 2048]) at widths 1..8
@@ -239,9 +251,9 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
         alg = EXPERT_WEIGHT_BYTES + EXPERT_SCALE_BYTES + width * 4096 * 2 * 2
         rec = {"algorithmic_bytes": alg}
         for label, pick in (("hbm_cold", lambda i: i % 256), ("mall_warm", lambda i: 0)):
-            us = _time_calls(torch, rt, lambda i, st: rt.expert_forward_device(
+            us, sp = _time_calls(torch, rt, lambda i, st: rt.expert_forward_device(
                 bank.bank, pick(i), x, width, y, mode=P.MODE_A, out_dtype=P.DTYPE_BF16, stream=st), calls)
-            rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+            rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1), "spread_us": sp}
         out[f"config1_w{width}"] = rec
     # config 3: separate q [12288], k [768 or 1000], v [512] x 4096 with their own scale grids
     for k_rows in ((768,) if small_only else (768, 1000)):
@@ -266,9 +278,9 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
             alg = total * 4096 + sum((r + 127) // 128 for r in seg_rows) * 32 * 4 + width * (4096 + total) * 2
             rec = {"algorithmic_bytes": alg}
             for label, pick in (("hbm_cold", lambda i: projs[i % copies]), ("mall_warm", lambda i: projs[0])):
-                us = _time_calls(torch, rt, lambda i, st: rt.fp8_linear_device(
+                us, sp = _time_calls(torch, rt, lambda i, st: rt.fp8_linear_device(
                     pick(i), x, width, y, mode=P.MODE_A, out_dtype=P.DTYPE_BF16, stream=st), calls)
-                rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+                rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1), "spread_us": sp}
             out[f"config3_k{k_rows}_w{width}"] = rec
         del projs, hosts
     if small_only:
@@ -283,8 +295,9 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
         alg = n * k * 2 + width * k * 4 + width * n * 4
         rec = {"algorithmic_bytes": alg}
         for label, pick in (("hbm_cold", lambda i: bprojs[i % copies]), ("mall_warm", lambda i: bprojs[0])):
-            us = _time_calls(torch, rt, lambda i, st: rt.bf16_linear_device(pick(i), x, width, y, stream=st), calls)
-            rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+            us, sp = _time_calls(torch, rt, lambda i, st: rt.bf16_linear_device(pick(i), x, width, y, stream=st),
+                                 calls)
+            rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1), "spread_us": sp}
         out[f"bf16_o_proj_w{width}"] = rec
     del bprojs, wb
     # dense layer-0 FP8 MLP: gate/up [16384 x 4096], down [4096 x 16384] as one-expert banks, 3 copies
@@ -310,9 +323,9 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
             alg = weight_bytes + width * dh * 2 * 2
             rec = {"algorithmic_bytes": alg}
             for label, pick in (("hbm_cold", lambda i: banks[i % copies]), ("mall_warm", lambda i: banks[0])):
-                us = _time_calls(torch, rt, lambda i, st: rt.expert_forward_device(
+                us, sp = _time_calls(torch, rt, lambda i, st: rt.expert_forward_device(
                     pick(i), 0, x, width, y, mode=mode, out_dtype=P.DTYPE_BF16, stream=st), calls // 2)
-                rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1)}
+                rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1), "spread_us": sp}
             out[f"dense_mlp_mode_{tag}_w{width}"] = rec
     del banks, keep
     return out
@@ -334,7 +347,8 @@ def layer_with_router(torch, rt, bank, P, WL, rows=8, steps=200, warmup=20):
         rt.route_device(x, rows, 4096, wt, 256, bt, ids, wts, stream=st)
         rt.moe_layer_device(bank.bank, x, rows, ids, wts, out, mode=P.MODE_A, out_dtype=P.DTYPE_BF16, stream=st)
 
-    return {"us": round(_time_calls(torch, rt, run, steps, warmup), 2), "rows": rows}
+    us, sp = _time_calls(torch, rt, run, steps, warmup)
+    return {"us": round(us, 2), "spread_us": sp, "rows": rows}
 
 
 def router_leg(torch, rt, P, WL, rows=8, calls=200):
@@ -346,8 +360,9 @@ def router_leg(torch, rt, P, WL, rows=8, calls=200):
     bt = torch.from_numpy(bias).cuda()
     ids = torch.empty((rows, 8), dtype=torch.int32, device="cuda")
     wts = torch.empty((rows, 8), dtype=torch.float32, device="cuda")
-    us = _time_calls(torch, rt, lambda i, st: rt.route_device(x, rows, 4096, wt, 256, bt, ids, wts, stream=st), calls)
-    return {"us": round(us, 2), "rows": rows}
+    us, sp = _time_calls(torch, rt, lambda i, st: rt.route_device(x, rows, 4096, wt, 256, bt, ids, wts, stream=st),
+                         calls)
+    return {"us": round(us, 2), "spread_us": sp, "rows": rows}
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_w8_gateup_hbm_traffic.md")
@@ -427,16 +442,73 @@ def cpu_baseline(WL, bank, batch, scalar_budget_s=12.0, blas_budget_s=3.0):
                 O.moe_layer_blas(x, dequantised, sel, w, pool=pool)
                 reps += 1
             t_blas = (time.perf_counter() - t0) / reps
+            # the reference's mode-B CPU path (routed_mlp_traced with fp8_linear) on the same experts
+            O.moe_layer_blas_mode_b(x, dequantised, sel, w, pool=pool)
+            reps_b, t0 = 0, time.perf_counter()
+            while reps_b < 2 or time.perf_counter() - t0 < blas_budget_s:
+                O.moe_layer_blas_mode_b(x, dequantised, sel, w, pool=pool)
+                reps_b += 1
+            t_blas_b = (time.perf_counter() - t0) / reps_b
     return {"value": round(layer_bytes / t_blas / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "layer_ms": round(t_blas * 1e3, 2),
             "sample": f"the reference's CPU BLAS layer (f32-dequantised weights, f32 SGEMM per expert, "
                       f"oracle.moe_layer_blas) over all {len(used)} routed experts of one width-8 batch, "
                       f"{reps} layers timed on {threads} threads (OpenBLAS, one thread per expert)",
             "hardware_concurrency": os.cpu_count(), "affinity_cpus": affinity,
+            "mode_b": {"value": round(layer_bytes / t_blas_b / 1e9, 3), "unit": "GB/s",
+                       "layer_ms": round(t_blas_b * 1e3, 2), "cores": threads, "kind": "port",
+                       "sample": f"the reference's mode-B CPU layer (routed_mlp_traced: dynamic FP8 activations, "
+                                 f"f32 SGEMM against the dequantised weights, bf16 rounding, staged SwiGLU; "
+                                 f"oracle.moe_layer_blas_mode_b) over the same {len(used)} experts, {reps_b} "
+                                 f"layers on {threads} threads"},
             "scalar_oracle": {"one_thread": {"GB/s": round(expert_bytes(done) / t_one / 1e9, 4),
                                              "experts": len(done), "s": round(t_one, 2)},
                               "all_threads": {"GB/s": round(expert_bytes(used) / t_all / 1e9, 4),
                                               "experts": len(used), "s": round(t_all, 2), "threads": threads}}}
+
+
+def cpu_prefill_baseline(WL, bank, sample_experts=32, budget_s=4.0):
+    """The reference's mode-B CPU path (routed_mlp_traced over fp8_linear, src/text_endpoint.rs:
+    5290-5381, :3053-3108; oracle.expert_blas_mode_b) on a bounded sample of the 2048-token prefill:
+    the `sample_experts` lowest-id routed experts with all of their placements, f32-dequantised
+    before timing, experts dealt over the worker threads (one BLAS thread each). TFLOP/s counts the
+    sample's placements at 2 x 3 x 2048 x 4096 flops each, as the GPU prefill's figure does."""
+    from concurrent.futures import ThreadPoolExecutor
+    from threadpoolctl import threadpool_limits
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    x = WL.activations(PREFILL_ROWS, WL.SEED_BASE + 4)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    sel, _, _ = WL.route_host(x, rw, bias)
+    used = sorted(set(sel.reshape(-1).tolist()))[:sample_experts]
+    rows_of = {e: np.nonzero(np.any(sel == e, axis=1))[0] for e in used}
+    placements = sum(r.size for r in rows_of.values())
+    threads, affinity = _cpu_threads()
+    with ThreadPoolExecutor(threads) as pool:
+        def deq(e):
+            gw, gs, uw, us, dw, ds = bank.expert_host(e)
+            return e, (O.decode_fp8_matrix_f32(gw, gs), O.decode_fp8_matrix_f32(uw, us),
+                       O.decode_fp8_matrix_f32(dw, ds))
+        dequantised = dict(pool.map(deq, used))
+        run = lambda e: O.expert_blas_mode_b(x[rows_of[e]], *dequantised[e])
+        with threadpool_limits(1, "blas"):
+            list(pool.map(run, used))  # untimed first pass
+            reps, t0 = 0, time.perf_counter()
+            while reps < 2 or time.perf_counter() - t0 < budget_s:
+                list(pool.map(run, used))
+                reps += 1
+            t = (time.perf_counter() - t0) / reps
+    flops = 2.0 * placements * EXPERT_MACS
+    all_placements = PREFILL_ROWS * 8
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample_ms": round(t * 1e3, 2), "layer_ms_estimate": round(t * 1e3 * all_placements / placements, 1),
+            "sample": f"the reference's mode-B CPU path (routed_mlp_traced over fp8_linear: dynamic FP8 "
+                      f"activations, f32 SGEMM against f32-dequantised weights, bf16 rounding, staged SwiGLU; "
+                      f"oracle.expert_blas_mode_b) on the {len(used)} lowest-id routed experts of the 2048-token "
+                      f"batch ({placements} of {all_placements} placements), {reps} passes on {threads} threads "
+                      f"(OpenBLAS, one thread per expert); layer_ms_estimate scales the sample time by the "
+                      f"placement count",
+            "hardware_concurrency": os.cpu_count(), "affinity_cpus": affinity}
 
 
 def main():
@@ -492,7 +564,7 @@ def main():
         return
     if args.small_calls_only:
         b1 = build_batches(P, WL, args.batches, 1, zipf=False)
-        ms1 = time_layer(torch, rt, bank, P, upload(torch, WL, b1), 1, args.steps, args.warmup, P.MODE_A)
+        ms1, _ = time_layer(torch, rt, bank, P, upload(torch, WL, b1), 1, args.steps, args.warmup, P.MODE_A)
         res = {"w1_layer_us": round(ms1 * 1000, 2), **projection_legs(torch, rt, bank, P, WL, small_only=True)}
         print(json.dumps({"workload": "small calls: configs 0, 1, 3 and the one-token routed layer, mode A", **res}),
               flush=True)
@@ -506,7 +578,7 @@ def main():
     avg_bytes = float(np.mean([b for _, b in sizes]))
 
     log(f"timing {args.steps} steps after {args.warmup} warm-up (avg {avg_u:.2f} unique experts/step)")
-    ms = time_layer(torch, rt, bank, P, dev_batches, rows, args.steps, args.warmup, P.MODE_A)
+    ms, spread = time_layer(torch, rt, bank, P, dev_batches, rows, args.steps, args.warmup, P.MODE_A)
     value = avg_bytes / (ms * 1e-3) / 1e9
     log(f"mode A width 8: {ms * 1000:.1f} us/layer, {value:.0f} GB/s")
 
@@ -520,28 +592,28 @@ def main():
                 "avg_us": round(gu["avg_us"], 2)}
 
     extras = {"kernels_us": {k: round(v["avg_us"], 2) for k, v in kt.items()},
-              "layer_us": round(ms * 1000, 2), "tokens_per_s": round(rows / (ms * 1e-3), 1),
+              "layer_us": round(ms * 1000, 2), "spread_us": spread, "tokens_per_s": round(rows / (ms * 1e-3), 1),
               "hbm_frac": round(value / HBM_PEAK_GBS, 4), "avg_unique_experts": avg_u,
               "placement_histogram": placement_histogram(np.concatenate([s for _, s, _ in batches]))}
     if not args.no_extras:
         zb = build_batches(P, WL, args.batches, rows, zipf=True)
         zd = upload(torch, WL, zb)
         zs = [step_bytes(sel, rows) for _, sel, _ in zb]
-        zms = time_layer(torch, rt, bank, P, zd, rows, args.steps, args.warmup, P.MODE_A)
-        extras["zipf_w8"] = {"layer_us": round(zms * 1000, 2),
+        zms, zspread = time_layer(torch, rt, bank, P, zd, rows, args.steps, args.warmup, P.MODE_A)
+        extras["zipf_w8"] = {"layer_us": round(zms * 1000, 2), "spread_us": zspread,
                              "avg_unique_experts": float(np.mean([u for u, _ in zs])),
                              "GB/s": round(float(np.mean([b for _, b in zs])) / (zms * 1e-3) / 1e9, 1),
                              "zipf_s": WL.ZIPF_S, "zipf_kappa": WL.ZIPF_KAPPA,
                              "placement_histogram": placement_histogram(np.concatenate([s for _, s, _ in zb]))}
-        bms = time_layer(torch, rt, bank, P, dev_batches, rows, args.steps, args.warmup, P.MODE_B)
-        extras["mode_b_w8"] = {"layer_us": round(bms * 1000, 2),
+        bms, bspread = time_layer(torch, rt, bank, P, dev_batches, rows, args.steps, args.warmup, P.MODE_B)
+        extras["mode_b_w8"] = {"layer_us": round(bms * 1000, 2), "spread_us": bspread,
                                "GB/s": round(avg_bytes / (bms * 1e-3) / 1e9, 1)}
         b1 = build_batches(P, WL, args.batches, 1, zipf=False)
         d1 = upload(torch, WL, b1)
         s1 = [step_bytes(sel, 1) for _, sel, _ in b1]
-        ms1 = time_layer(torch, rt, bank, P, d1, 1, args.steps, args.warmup, P.MODE_A)
+        ms1, spread1 = time_layer(torch, rt, bank, P, d1, 1, args.steps, args.warmup, P.MODE_A)
         kt1 = kernel_times(torch, rt, bank, P, d1, 1, max(20, args.steps // 4), P.MODE_A)
-        extras["w1"] = {"layer_us": round(ms1 * 1000, 2),
+        extras["w1"] = {"layer_us": round(ms1 * 1000, 2), "spread_us": spread1,
                         "GB/s": round(float(np.mean([b for _, b in s1])) / (ms1 * 1e-3) / 1e9, 1),
                         "kernels_us": {k: round(v["avg_us"], 2) for k, v in kt1.items()}}
         for zipf in (False, True):
@@ -559,6 +631,12 @@ def main():
         cpu = cpu_baseline(WL, bank, batches[0])
         log(f"cpu baseline {cpu['value']:.3f} GB/s, {cpu['layer_ms']} ms per layer ({cpu['sample']}); "
             f"scalar oracle {cpu['scalar_oracle']}")
+        if "mode_b_w8" in extras:
+            extras["mode_b_w8"]["cpu_baseline"] = cpu["mode_b"]
+        if "prefill_t2048" in extras:
+            log("timing the mode-B CPU path on a sample of the 2048-token prefill")
+            extras["prefill_t2048"]["cpu_baseline"] = cpu_prefill_baseline(WL, bank)
+            log(f"prefill cpu baseline {extras['prefill_t2048']['cpu_baseline']}")
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,

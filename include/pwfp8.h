@@ -356,7 +356,14 @@ int pw_route_device(pw_runtime *rt, const void *x, uint32_t x_dtype, uint32_t ro
                     uint32_t *route_ids, float *route_weights, float *scores, uint32_t *tie_rows, void *stream);
 
 /* ---- routing on the host (src/text_endpoint.rs:4342-4473, src/pytorch_topk.cpp:8-30) -------- */
-/* pw_pytorch_topk_unsorted_f32 with libc++ std::nth_element order: -1 on bad arguments. */
+/* pw_pytorch_topk_unsorted_f32 (src/pytorch_topk.cpp:7-30, declared by its caller at
+ * src/text_endpoint.rs:2466-2474): the indices of the top_k largest values, in the partition order
+ * of libc++'s std::nth_element(first, first + top_k - 1, last) over (value, index) pairs compared
+ * greater-by-value. Returns 0; -1 when values or selected is NULL, top_k == 0 or top_k >= count;
+ * -2 when the pair buffer cannot be allocated. The reference's own symbol name and signature, so
+ * its extern "C" block links unchanged. */
+int pw_pytorch_topk_unsorted_f32(const float *values, size_t count, size_t top_k, uint32_t *selected);
+/* The same function under this library's pw_ prefix (identical arguments, results and codes). */
 int pw_topk_unsorted_f32(const float *values, size_t count, size_t top_k, uint32_t *selected);
 /* pytorch_noaux_routes: scores [rows x experts] (sigmoid outputs), bias [experts] ->
  * selected / weights [rows x 8]; *tie_rows counts boundary ties. */

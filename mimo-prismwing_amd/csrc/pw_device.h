@@ -116,7 +116,7 @@ struct MoePlan {
     uint32_t n_active;        // U, distinct routed experts
     uint32_t n_placements;    // rows * top_k
     uint32_t max_count;       // largest placement count of any expert
-    uint32_t rejected;        // long-batch schedule: routes rejected, placement tables left zero
+    uint32_t rejected;        // routes rejected: placement tables left zero, the layer writes zeros
 };
 
 // MFMA wrappers (gfx950). 16x16 output tile, lane l holds D[4*(l/16)+i][l%16], i = 0..3.

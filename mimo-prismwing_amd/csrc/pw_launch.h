@@ -176,9 +176,10 @@ void launch_quant_group128(const void *x, bool x_f32, uint32_t rows, uint32_t K,
 constexpr uint32_t PREFILL_MT = 128;
 struct PfTileDesc {
     ExpertPtrs ep;
-    uint32_t slot0;  // first placement slot
-    uint32_t cnt;    // placement slots of the tile
-    uint32_t pad[2];
+    uint32_t slot0;   // first placement slot
+    uint32_t cnt;     // placement slots of the tile
+    uint32_t expert;  // the routed expert's id (sets the tile's K order, so it never depends on the batch)
+    uint32_t pad;
 };
 static_assert(sizeof(PfTileDesc) == 64, "a tile descriptor is one 64-byte scalar load");
 struct PfTileTable {

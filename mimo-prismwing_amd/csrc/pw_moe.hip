@@ -211,6 +211,7 @@ __global__ __launch_bounds__(1024) void moe_schedule_kernel(
         plan->n_active = n_active;
         plan->n_placements = total;
         plan->max_count = s_max;
+        plan->rejected = (s_bad || total != P) ? 1u : 0u;
         if (s_bad || total != P)
             raise_flag(flags, FLAG_SCHEDULE);
     }
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(1024) void moe_sched_plan_kernel(
                 dst[1] = ep1;
                 dst[2] = ep2;
                 dst[3] = u32x4{off + i * PREFILL_MT, live - i * PREFILL_MT < PREFILL_MT ? live - i * PREFILL_MT
-                                                                                       : PREFILL_MT, 0u, 0u};
+                                                                                       : PREFILL_MT, e, 0u};
             }
         if (tid == 0) {
             tt.n_tiles[0] = rejected ? 0u : (n_tiles < tt.max_tiles ? n_tiles : tt.max_tiles);
@@ -701,6 +702,7 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
         plan->n_active = U;
         plan->n_placements = total;
         plan->max_count = mx;
+        plan->rejected = bad ? 1u : 0u;
         if (bad)
             raise_flag(flags, FLAG_SCHEDULE);
     }
@@ -947,9 +949,11 @@ __device__ __forceinline__ float4 split_sum4(const float *p, uint32_t ks, size_t
 template <int KS>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float *__restrict__ y, uint32_t ks_rt, size_t split_stride, const float *__restrict__ placement_w,
-    const uint32_t *__restrict__ row_slots, uint32_t rows, uint32_t H, float *__restrict__ out_f32,
-    uint16_t *__restrict__ out_bf16, uint32_t raw, uint32_t *flags)
+    const uint32_t *__restrict__ row_slots, uint32_t rows, uint32_t H, const MoePlan *__restrict__ plan,
+    float *__restrict__ out_f32, uint16_t *__restrict__ out_bf16, uint32_t raw, uint32_t *flags)
 {
+    // a rejected batch (the schedule raised FLAG_SCHEDULE) writes zeros, whatever its expert outputs hold
+    const bool rejected = plan->rejected != 0;
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;  // one float4 of one token row
     const uint32_t per_row = H >> 2;
     if (idx >= rows * per_row)
@@ -1000,6 +1004,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     const size_t at = (size_t)row * H + c4 * 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        acc[i] = rejected ? 0.f : acc[i];
         const float r = round_bf16(acc[i]);
         bad |= !finite_f32(r);
         if (out_f32)
@@ -1025,6 +1030,7 @@ __global__ void moe_single_plan_kernel(const ExpertPtrs *bank, uint32_t expert, 
         plan->n_active = 1;
         plan->n_placements = rows;
         plan->max_count = rows;
+        plan->rejected = 0u;
         active_expert[0] = expert;
         active_offset[0] = 0;
         active_offset[1] = rows;
@@ -1257,7 +1263,8 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
     const int t = timer_begin(K_MOE_COMBINE, stream);
 #define PW_COMBINE(KS)                                                                                         \
     hipLaunchKernelGGL((moe_combine_kernel<KS>), dim3((n4 + 255) / 256), dim3(256), 0, stream, eo.y, eo.ks, \
-                       eo.stride, mb.placement_w, mb.row_slots, rows, H, out_f32, out_bf16, raw ? 1u : 0u, flags)
+                       eo.stride, mb.placement_w, mb.row_slots, rows, H, mb.plan, out_f32, out_bf16, raw ? 1u : 0u, \
+                       flags)
     switch (eo.ks) {
     case 1: PW_COMBINE(1); break;
     case 2: PW_COMBINE(2); break;

@@ -625,9 +625,11 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
     // waves and the combine take the experts in ascending id like the schedule; duplicates, ids
     // past the bank and non-finite weights are rejected
     uint32_t n_active, slot_of_a = a;
+    bool rejected;  // routes that fail the schedule's checks: the combine writes zeros, as the schedule's does
     if (args.route_ids) {
         const uint32_t li = (uint32_t)lane & 7;
         const uint32_t id = load_g(args.route_ids + li);
+        const float rw = load_g(args.route_w + li);
         uint32_t rank = 0;
         bool dup = false;
 #pragma unroll
@@ -637,15 +639,17 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
             dup |= idj == id && (uint32_t)j != li;
         }
         slot_of_a = __builtin_ctzll(__ballot(lane < 8 && rank == a));
+        const bool bad = dup || id >= args.E || !finite_f32(rw);
+        rejected = __ballot(lane < 8 && bad) != 0;
         if (wave == 0 && lane < 8) {
             rank_slot[rank] = li;
-            const bool bad = dup || id >= args.E || !finite_f32(load_g(args.route_w + li));
             if (bad)
                 raise_flag(args.flags, FLAG_SCHEDULE);
         }
         n_active = 8;
     } else {
         n_active = plan->n_active;
+        rejected = plan->rejected != 0;
     }
     f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
     if (a < n_active) {
@@ -724,6 +728,7 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
         }
         acc = __fadd_rn(acc, __fmul_rn(y, w));
     }
+    acc = rejected ? 0.f : acc;
     const float r = round_bf16(acc);
     const size_t at = row0 + lane;
     if (out_f32)

@@ -49,11 +49,13 @@ static_assert(PF_MT % 16 == 0 && PF_MT > 64 && PF_MT <= 128, "two 64-slot token 
 constexpr uint32_t PF_UNITS = 8;                  // 16-byte units per 128-byte token row of a step
 constexpr int PF_CONS = 8;                        // consumer waves per workgroup, 16 RG weight rows each
 constexpr int PF_WAVES = PF_CONS + 1;             // and one producer wave (the codes ring)
-// Gate/up workgroups start their K loop at column step blockIdx % nsteps (and wrap), so the
-// workgroups in flight, which advance through K at about the same rate, read different offsets of
-// their weight rows instead of all the same 256 bytes of rows 4 KB apart (with every workgroup in
-// step, the gate/up GEMM ran 13% slower for some physical placements of the bank; down, with
-// four n-tiles per workgroup, does not need it).
+// Gate/up workgroups start their K loop at column step (8 n-tile group + expert id % 8) % nsteps
+// (and wrap), so the workgroups in flight, which advance through K at about the same rate, read
+// different offsets of their weight rows instead of all the same 256 bytes of rows 4 KB apart (with
+// every workgroup in step, the gate/up GEMM ran 13% slower for some physical placements of the
+// bank; down, with four n-tiles per workgroup, does not need it). The sixteen n-tile groups of an
+// m-tile share two start steps, so they read two code steps at a time; the start depends on nothing
+// the rest of the batch sets, so a token's results do not either.
 constexpr bool PF_ROTATE_GATEUP = true, PF_ROTATE_DOWN = false;
 constexpr uint32_t PF_BLK = PF_MT * PF_UNITS;     // 16-byte code units per 128-column block
 static_assert(PF_BLK % 64 == 0, "a block's codes are whole 64-lane copies");
@@ -87,6 +89,7 @@ using PfNarrow = PfCfg<1, 4, 4, 1>;
 // (banks hold at most 1024 experts).
 __global__ __launch_bounds__(1024) void prefill_tiles_kernel(const MoePlan *__restrict__ plan,
                                                              const ActiveExpert *__restrict__ active,
+                                                             const uint32_t *__restrict__ active_expert,
                                                              uint32_t max_active, PfTileDesc *__restrict__ tiles,
                                                              uint32_t max_tiles, uint32_t *__restrict__ n_tiles,
                                                              uint32_t *flags)
@@ -107,7 +110,8 @@ __global__ __launch_bounds__(1024) void prefill_tiles_kernel(const MoePlan *__re
                 td.ep = ae.ep;
                 td.slot0 = ae.off + i * PF_MT;
                 td.cnt = cnt - i * PF_MT < PF_MT ? cnt - i * PF_MT : PF_MT;
-                td.pad[0] = td.pad[1] = 0;
+                td.expert = active_expert[a];
+                td.pad = 0;
                 tiles[off + i] = td;
             }
     }
@@ -504,7 +508,9 @@ __global__ __launch_bounds__(64 * PF_WAVES) __attribute__((amdgpu_waves_per_eu(C
     tile.R1 = args.R1;
     tile.nsteps = nsteps;
     tile.n_sub = n_sub;
-    tile.rot = (gather ? PF_ROTATE_GATEUP : PF_ROTATE_DOWN) ? blockIdx.x % nsteps : 0u;
+    // the start step depends on the n-tile group and the expert only, never on where the batch put
+    // the m-tile: a token's sums run in the same order whatever else is routed with it
+    tile.rot = (gather ? PF_ROTATE_GATEUP : PF_ROTATE_DOWN) ? (8 * group + (td.expert & 7)) % nsteps : 0u;
     tile.wcol = col0 + wrow0;
     tile.loff = (uint32_t)r16 * K + (uint32_t)q * 16;
     tile.cnt = cnt_t;
@@ -687,11 +693,13 @@ __global__ __launch_bounds__(256) void prefill_swiglu_quant_kernel(const uint16_
 // route_weighted_scatter_add_f32 + final bf16 round over bf16 expert outputs: each token sums
 // its eight placements in ascending expert id, out += y * w in f32 (no fused multiply-add). One
 // thread per eight consecutive columns of a token row (16-byte loads of each placement's outputs).
+// A rejected batch (the schedule raised FLAG_SCHEDULE) writes zeros.
 __global__ __launch_bounds__(256) void prefill_combine_kernel(
     const uint16_t *__restrict__ y, const float *__restrict__ placement_w, const uint32_t *__restrict__ row_slots,
-    uint32_t rows, uint32_t H, float *__restrict__ out_f32, uint16_t *__restrict__ out_bf16, uint32_t raw,
-    uint32_t *flags)
+    uint32_t rows, uint32_t H, const MoePlan *__restrict__ plan, float *__restrict__ out_f32,
+    uint16_t *__restrict__ out_bf16, uint32_t raw, uint32_t *flags)
 {
+    const bool rejected = plan->rejected != 0;
     const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;  // eight values of one token row
     const uint32_t per_row = H >> 3;
     if (idx >= rows * per_row)
@@ -723,6 +731,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(
     float r[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+        acc[i] = rejected ? 0.f : acc[i];
         r[i] = round_bf16(acc[i]);
         bad |= !finite_f32(r[i]);
     }
@@ -785,8 +794,8 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     const uint32_t max_tiles = prefill_max_tiles(rows, E);
     if (!scheduled_long) {
         launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
-        hipLaunchKernelGGL(prefill_tiles_kernel, dim3(1), dim3(1024), 0, stream, mb.plan, mb.active, max_active,
-                           pb.tiles, max_tiles, pb.n_tiles, flags);
+        hipLaunchKernelGGL(prefill_tiles_kernel, dim3(1), dim3(1024), 0, stream, mb.plan, mb.active,
+                           mb.active_expert, max_active, pb.tiles, max_tiles, pb.n_tiles, flags);
     }
 
     // gate and up as one stacked projection of 2I output columns per slot
@@ -831,7 +840,7 @@ void launch_moe_prefill(const ExpertPtrs *bank, const MoeBuffers &mb, const Pref
     const uint32_t n8 = rows * (H >> 3);
     t = timer_begin(K_MOE_COMBINE, stream);
     hipLaunchKernelGGL(prefill_combine_kernel, dim3((n8 + 255) / 256), dim3(256), 0, stream, pb.y, mb.placement_w,
-                       mb.row_slots, rows, H, out_f32, out_bf16, raw ? 1u : 0u, flags);
+                       mb.row_slots, rows, H, mb.plan, out_f32, out_bf16, raw ? 1u : 0u, flags);
     timer_end(t, stream);
 }
 

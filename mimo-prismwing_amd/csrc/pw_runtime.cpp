@@ -124,13 +124,24 @@ namespace {
 // a stream other than the previous call's waits for the previous call's work; on exit, work
 // enqueued on a caller's stream is marked with the runtime's event. No cost while every call uses
 // the same stream.
+// A call enqueued on a stream under HIP graph capture is left out of this ordering: it neither
+// waits on an event recorded outside the capture (a cross-boundary dependency the capture
+// rejects) nor records the runtime's event into the graph, and the calls after it are ordered
+// against the eager work before it. The caller orders the capture, and every replay of the
+// graph, against the runtime's other calls (they share its scratch).
 struct StreamOrder {
     pw_runtime *rt;
     hipStream_t s;
     hipError_t err = hipSuccess;
+    bool captured = false;
     StreamOrder(pw_runtime *r, hipStream_t stream) : rt(r), s(stream)
     {
-        if (rt->last_stream && rt->last_stream != s) {
+        hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+        err = hipStreamIsCapturing(s, &status);
+        if (err != hipSuccess)
+            return;
+        captured = status != hipStreamCaptureStatusNone;
+        if (!captured && rt->last_stream && rt->last_stream != s) {
             if (rt->last_stream == rt->stream)
                 err = hipEventRecord(rt->order_event, rt->stream);
             if (err == hipSuccess)
@@ -139,6 +150,8 @@ struct StreamOrder {
     }
     ~StreamOrder()
     {
+        if (err != hipSuccess || captured)
+            return;
         if (s != rt->stream)
             (void)hipEventRecord(rt->order_event, s);
         rt->last_stream = s;
@@ -1510,21 +1523,43 @@ int pw_expert_forward_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_
 }
 
 // ----------------------------------------------------------------------------- host routing
-int pw_topk_unsorted_f32(const float *values, size_t count, size_t top_k, uint32_t *selected)
+extern "C++" {
+namespace {
+
+// nth_element over (value, index) pairs with Idx-wide indices; the first top_k indices in
+// partition order, truncated to 32 bits as the reference's static_cast<uint32_t> does.
+template <class Idx>
+void topk_unsorted(const float *values, size_t count, size_t top_k, uint32_t *selected)
 {
-    if (!values || !selected || top_k == 0 || top_k >= count || count > (size_t)INT32_MAX)
+    std::vector<pw::TopkEntryT<Idx>> q(count);
+    for (size_t i = 0; i < count; ++i)
+        q[i] = pw::TopkEntryT<Idx>{values[i], (Idx)i};
+    pw::nth_element_libcxx(q.data(), q.data() + top_k - 1, q.data() + count);
+    for (size_t i = 0; i < top_k; ++i)
+        selected[i] = (uint32_t)q[i].i;
+}
+
+}  // namespace
+}
+
+int pw_pytorch_topk_unsorted_f32(const float *values, size_t count, size_t top_k, uint32_t *selected)
+{
+    if (!values || !selected || top_k == 0 || top_k >= count)
         return -1;
     try {
-        std::vector<pw::TopkEntry> q(count);
-        for (size_t i = 0; i < count; ++i)
-            q[i] = pw::TopkEntry{values[i], (int32_t)i};
-        pw::nth_element_libcxx(q.data(), q.data() + top_k - 1, q.data() + count);
-        for (size_t i = 0; i < top_k; ++i)
-            selected[i] = (uint32_t)q[i].i;
+        if (count <= (size_t)INT32_MAX)
+            topk_unsorted<int32_t>(values, count, top_k, selected);
+        else
+            topk_unsorted<int64_t>(values, count, top_k, selected);
     } catch (...) {
         return -2;
     }
     return 0;
+}
+
+int pw_topk_unsorted_f32(const float *values, size_t count, size_t top_k, uint32_t *selected)
+{
+    return pw_pytorch_topk_unsorted_f32(values, count, top_k, selected);
 }
 
 int pw_noaux_routes(const float *scores, const float *bias, uint32_t rows, uint32_t experts,

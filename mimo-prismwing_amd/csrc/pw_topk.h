@@ -20,21 +20,30 @@
 
 namespace pw {
 
-struct TopkEntry {
+// A (value, index) pair of the partition. The routing paths index at most 2^31 experts and use
+// 32-bit indices; the reference's FFI keeps 64-bit ones (any count), and the algorithm below is
+// the same for both.
+template <class Idx>
+struct TopkEntryT {
     float v;
-    int32_t i;
+    Idx i;
 };
+typedef TopkEntryT<int32_t> TopkEntry;
+typedef TopkEntryT<int64_t> TopkEntry64;
 
-PW_HD bool topk_greater(const TopkEntry &a, const TopkEntry &b) { return a.v > b.v; }
+template <class T>
+PW_HD bool topk_greater(const T &a, const T &b) { return a.v > b.v; }
 
-PW_HD void topk_swap(TopkEntry &a, TopkEntry &b)
+template <class T>
+PW_HD void topk_swap(T &a, T &b)
 {
-    const TopkEntry t = a;
+    const T t = a;
     a = b;
     b = t;
 }
 
-PW_HD unsigned topk_sort3(TopkEntry *x, TopkEntry *y, TopkEntry *z)
+template <class T>
+PW_HD unsigned topk_sort3(T *x, T *y, T *z)
 {
     if (!topk_greater(*y, *x)) {
         if (!topk_greater(*z, *y))
@@ -58,11 +67,12 @@ PW_HD unsigned topk_sort3(TopkEntry *x, TopkEntry *y, TopkEntry *z)
     return 1;
 }
 
-PW_HD void topk_select_sort(TopkEntry *first, TopkEntry *last)
+template <class T>
+PW_HD void topk_select_sort(T *first, T *last)
 {
-    for (TopkEntry *lm1 = last - 1; first != lm1; ++first) {
-        TopkEntry *best = first;
-        for (TopkEntry *it = first + 1; it != last; ++it)
+    for (T *lm1 = last - 1; first != lm1; ++first) {
+        T *best = first;
+        for (T *it = first + 1; it != last; ++it)
             if (topk_greater(*it, *best))
                 best = it;
         if (best != first)
@@ -71,7 +81,8 @@ PW_HD void topk_select_sort(TopkEntry *first, TopkEntry *last)
 }
 
 // The ranges of at most 7 elements nth_element finishes directly; returns false for longer ones.
-PW_HD bool topk_small(TopkEntry *first, TopkEntry *last)
+template <class T>
+PW_HD bool topk_small(T *first, T *last)
 {
     const long len = (long)(last - first);
     if (len <= 1)
@@ -95,9 +106,10 @@ PW_HD bool topk_small(TopkEntry *first, TopkEntry *last)
 // The partition nth_element falls back to when no element of (first, last - 1) is greater than the
 // pivot and *first equals it: partitions around *first. Returns true when nth is placed; otherwise
 // *next is the new start of the range.
-PW_HD bool topk_fallback_partition(TopkEntry *first, TopkEntry *nth, TopkEntry *last, TopkEntry **next)
+template <class T>
+PW_HD bool topk_fallback_partition(T *first, T *nth, T *last, T **next)
 {
-    TopkEntry *i = first + 1, *j = last;
+    T *i = first + 1, *j = last;
     if (!topk_greater(*first, *--j)) {
         for (;; ++i) {
             if (i == j)
@@ -128,7 +140,8 @@ PW_HD bool topk_fallback_partition(TopkEntry *first, TopkEntry *nth, TopkEntry *
     return false;
 }
 
-PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
+template <class T>
+PW_HD void nth_element_libcxx(T *first, T *nth, T *last)
 {
     for (;;) {
         if (nth == last)
@@ -136,9 +149,9 @@ PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
         if (topk_small(first, last))
             return;
         const long len = (long)(last - first);
-        TopkEntry *m = first + len / 2, *lm1 = last - 1;
+        T *m = first + len / 2, *lm1 = last - 1;
         unsigned swaps = topk_sort3(first, m, lm1);
-        TopkEntry *i = first, *j = lm1;
+        T *i = first, *j = lm1;
         if (!topk_greater(*i, *m)) {
             bool guard = false;
             while (!(i == --j)) {
@@ -151,7 +164,7 @@ PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
                 topk_swap(*i, *j);
                 ++swaps;
             } else {
-                TopkEntry *next;
+                T *next;
                 if (topk_fallback_partition(first, nth, last, &next))
                     return;
                 first = next;
@@ -182,7 +195,7 @@ PW_HD void nth_element_libcxx(TopkEntry *first, TopkEntry *nth, TopkEntry *last)
         if (nth == i)
             return;
         if (swaps == 0) {
-            TopkEntry *a = nth < i ? first : i, *end = nth < i ? i : last, *prev = a;
+            T *a = nth < i ? first : i, *end = nth < i ? i : last, *prev = a;
             bool sorted = true;
             while (++a != end) {
                 if (topk_greater(*a, *prev)) {

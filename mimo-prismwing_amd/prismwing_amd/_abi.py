@@ -112,6 +112,7 @@ SIGNATURES = {
     "pw_moe_prefill_device": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
     "pw_moe_schedule_device": (_i, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),
     "pw_route_device": (_i, [_vp, _vp, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pw_pytorch_topk_unsorted_f32": (_i, [_f32p, _sz, _sz, _u32p]),
     "pw_topk_unsorted_f32": (_i, [_f32p, _sz, _sz, _u32p]),
     "pw_noaux_routes": (_i, [_f32p, _f32p, _u32, _u32, _u32p, _f32p, _u64p]),
     "pw_route_from_logits": (_i, [_f32p, _f32p, _u32, _u32, _f32p, _u32p, _f32p, _u64p]),

@@ -400,7 +400,8 @@ def topk_unsorted(values: np.ndarray, top_k: int = 8) -> np.ndarray:
     """pw_pytorch_topk_unsorted_f32 (src/pytorch_topk.cpp:8-30), libc++ nth_element order."""
     v = np.ascontiguousarray(values, np.float32)
     out = np.zeros(top_k, np.uint32)
-    rc = lib().pw_topk_unsorted_f32(v.ctypes.data_as(_abi._f32p), v.size, top_k, out.ctypes.data_as(_abi._u32p))
+    rc = lib().pw_pytorch_topk_unsorted_f32(v.ctypes.data_as(_abi._f32p), v.size, top_k,
+                                            out.ctypes.data_as(_abi._u32p))
     if rc != 0:
         raise _abi.PwError(-1, f"top-k failed ({rc})")
     return out

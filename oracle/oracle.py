@@ -327,3 +327,51 @@ def moe_layer_blas(x: np.ndarray, dequantised: dict, selected: np.ndarray, weigh
         for l, p in enumerate(pos.tolist()):
             block[p] = block[p] + y[l] * wts[l]
     return block
+
+
+def _round_bf16_np(v: np.ndarray) -> np.ndarray:
+    """round_bf16 (src/text_endpoint.rs:2960-2971) on a finite f32 array."""
+    b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
+def fp8_linear_blas(x: np.ndarray, dequantised_w: np.ndarray) -> np.ndarray:
+    """fp8_linear (src/text_endpoint.rs:3053-3108) against an f32-dequantised weight: the dynamic
+    FP8 activations' dequantised values (dynamic_fp8, the C restatement of :3008-3051), one f32
+    SGEMM (the BLAS library's summation order), every output rounded to bf16."""
+    _, _, deq = dynamic_fp8(np.asarray(x, np.float32))
+    return _round_bf16_np(deq @ dequantised_w.T)
+
+
+def expert_blas_mode_b(x: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray) -> np.ndarray:
+    """One expert of routed_mlp_traced (src/text_endpoint.rs:5290-5381) on BLAS: fp8_linear gate and
+    up, the bf16-staged SwiGLU (:5336-5343, the C restatement), fp8_linear down."""
+    g = fp8_linear_blas(x, gate)
+    u = fp8_linear_blas(x, up)
+    return fp8_linear_blas(swiglu_bf16_staged(g, u), down)
+
+
+def moe_layer_blas_mode_b(x: np.ndarray, dequantised: dict, selected: np.ndarray, weights: np.ndarray,
+                          pool=None):
+    """routed_mlp_traced (src/text_endpoint.rs:5290-5381) over f32-dequantised experts: experts in
+    ascending id, each on its token rows in ascending order (expert_blas_mode_b), out[pos] += y * w in
+    f32, bf16 at the end. Returns (bf16-rounded output, the f32 block). With a thread pool the experts
+    run concurrently and are still combined in ascending id."""
+    x = np.asarray(x, np.float32)
+    selected = np.asarray(selected)
+    plan = []
+    for e in sorted(set(selected.reshape(-1).tolist())):
+        pos, slot = np.nonzero(selected == e)
+        order = np.argsort(pos, kind="stable")
+        plan.append((e, pos[order], np.asarray(weights, np.float32)[pos[order], slot[order]]))
+
+    def run(item):
+        e, pos, _ = item
+        return expert_blas_mode_b(x[pos], *dequantised[e])
+
+    outs = list(pool.map(run, plan)) if pool is not None else [run(p) for p in plan]
+    block = np.zeros((x.shape[0], x.shape[1]), np.float32)
+    for (e, pos, wts), y in zip(plan, outs):
+        for l, p in enumerate(pos.tolist()):
+            block[p] = block[p] + y[l] * wts[l]
+    return _round_bf16_np(block), block

@@ -147,17 +147,40 @@ def fp8_blocks_exact(q: np.ndarray, w: np.ndarray) -> bool:
     within 14 bits of the block's largest product (it truncates bits below 2^(e - 13), e the
     exponent of the largest product: measured 448 + 2^-9 -> 448, 64 + 7 * 2^-9 -> 64 + 2^-7).
     q [rows, K] and w [n, K] hold e4m3 values (without block scales): True when every block of every
-    (row, output) sum is inside that window (a product's lowest bit is the product of its operands')."""
+    (row, output) sum is inside that window (a product's lowest bit is the product of its operands').
+
+    Per block, cheap sufficient conditions come first: every output row of w has at most one nonzero
+    (one product per sum), or, over the columns where some output row is nonzero, the smallest
+    lowest bits of q's row and w's row times each other reach the window of the product of their
+    largest magnitudes (an upper bound of the largest product). Pairs that neither settles are
+    checked product by product."""
     lq, lw = _lowbits(q), _lowbits(w)
     for b in range(q.shape[1] // 128):
         blk = slice(128 * b, 128 * b + 128)
-        mx = (np.abs(q[:, None, blk]) * np.abs(w[None, :, blk])).max(axis=-1)
-        lp = lq[:, None, blk] * lw[None, :, blk]
-        low = np.where(lp > 0, lp, np.inf).min(axis=-1)
-        live = mx > 0
-        window = np.ldexp(1.0, np.floor(np.log2(np.where(live, mx, 1.0))).astype(np.int64) - 13)
-        if np.any(live & (low < window)):
-            return False
+        wb = w[:, blk]
+        if np.all(np.count_nonzero(wb, axis=1) <= 1):
+            continue
+        cols = np.any(wb != 0, axis=0)
+        qb, wb = np.abs(q[:, blk][:, cols]), np.abs(wb[:, cols])
+        lqb, lwb = lq[:, blk][:, cols], lw[:, blk][:, cols]
+        qmin = np.where(lqb > 0, lqb, np.inf).min(axis=1)
+        wmin = np.where(lwb > 0, lwb, np.inf).min(axis=1)
+        bound = qb.max(axis=1)[:, None] * wb.max(axis=1)[None, :]
+        live = bound > 0
+        window = np.ldexp(1.0, np.floor(np.log2(np.where(live, bound, 1.0))).astype(np.int64) - 13)
+        unsettled = live & (qmin[:, None] * wmin[None, :] < window)
+        if not np.any(unsettled):
+            continue
+        rs, ns = np.nonzero(unsettled)
+        for r, n in zip(rs, ns):
+            prod = qb[r] * wb[n]
+            mx = prod.max()
+            if mx == 0:
+                continue
+            lp = lqb[r] * lwb[n]
+            low = np.where(lp > 0, lp, np.inf).min()
+            if low < np.ldexp(1.0, int(np.floor(np.log2(mx))) - 13):
+                return False
     return True
 
 
@@ -258,3 +281,79 @@ def moe_condition(x, experts, sel, w):
         for l, p in enumerate(rows_e):
             out[p] += abs(float(np.asarray(w)[p, np.asarray(sel)[p].tolist().index(e)])) * cond[l]
     return out
+
+
+# Known-answer router rows that pin the route-weight denominator of pytorch_noaux_routes
+# (src/text_endpoint.rs:4382-4390, :4450): w_i = s_i / (fold(0, +)(s0 + s4, s1 + s5, s2 + s6, s3 + s7)
+# + 1e-20) over the selected scores in partition order. Each row is 256 logits, logit[e] =
+# base - e / 256 except at `positions`, where logit = num / 256 (all exact in f32). Expected values are
+# the reference's formula in IEEE f32; for each row the alternative orders listed in `differs` give
+# other weight bits, so a slip to any of them fails.
+#   tree      (l0 + l1) + (l2 + l3)
+#   plain     s0 + s1 + ... + s7 left to right
+#   id_order  the reference's fold over the selected scores taken in ascending expert id
+#   no_eps    without the + 1e-20
+ROUTE_WEIGHT_ROWS = [
+    dict(base=-4.0, positions=[1, 3, 53, 76, 126, 169, 223, 236],
+         num=[469, 210, 438, 481, 181, -41, -145, 176],
+         selected=[53, 1, 76, 3, 126, 236, 169, 223],
+         score_bits=[0x3f58d23b, 0x3f5cac43, 0x3f5e1387, 0x3f31bdd2, 0x3f2b7466, 0x3f2a5859, 0x3eeb8b31,
+                     0x3eb960c7],
+         weight_bits=[0x3e1fc77f, 0x3e229e1f, 0x3e23a6df, 0x3e02fb13, 0x3dfcb221, 0x3dfb0f7c, 0x3dad9383,
+                      0x3d889bb7],
+         differs=["tree", "plain", "id_order"]),
+    dict(base=-40.0, positions=[130, 147, 148, 188, 194, 225, 236, 251],
+         num=[-8031, -8362, -8373, -8301, -8229, -8335, -8193, -8184],
+         selected=[251, 236, 188, 194, 130, 225, 147, 148],
+         score_bits=[0x286b6112, 0x28633f77, 0x28150866, 0x28456fb7, 0x28d5f141, 0x28027f5b, 0x27eadebc,
+                     0x27e0fde3],
+         weight_bits=[0x3e16e310, 0x3e11acac, 0x3dbf1243, 0x3dfd20dd, 0x3e89252a, 0x3da74ec2, 0x3d968f83,
+                      0x3d903a6c],
+         differs=["tree", "plain", "id_order", "no_eps"]),
+]
+
+
+def route_weight_row_logits(row) -> np.ndarray:
+    logits = (np.float32(row["base"]) - np.arange(256, dtype=np.float32) / np.float32(256)).astype(np.float32)
+    logits[row["positions"]] = np.array(row["num"], np.float32) / np.float32(256)
+    return logits
+
+
+def route_weight_alternatives(scores_sel: np.ndarray, selected) -> dict:
+    """Route weights of the selected scores (partition order) under the reference's denominator and
+    under each alternative, in IEEE f32."""
+    f = np.float32
+
+    def lanes(s):
+        return [f(s[0] + s[4]), f(s[1] + s[5]), f(s[2] + s[6]), f(s[3] + s[7])]
+
+    def fold(s):
+        acc = f(0.0)
+        for v in lanes(s):
+            acc = f(acc + v)
+        return acc
+
+    def plain(s):
+        acc = f(0.0)
+        for v in s:
+            acc = f(acc + v)
+        return acc
+
+    def tree(s):
+        ln = lanes(s)
+        return f(f(ln[0] + ln[1]) + f(ln[2] + ln[3]))
+
+    def weights(s, den, eps=True):
+        d = f(den + f(1e-20)) if eps else den
+        return np.array([f(v / d) for v in s], np.float32)
+
+    s = np.asarray(scores_sel, np.float32)
+    by_id = np.argsort(np.asarray(selected))
+    s_id = s[by_id]
+    return {
+        "reference": weights(s, fold(s)),
+        "tree": weights(s, tree(s)),
+        "plain": weights(s, plain(s)),
+        "id_order": weights(s, fold(s_id)),
+        "no_eps": weights(s, fold(s), eps=False),
+    }

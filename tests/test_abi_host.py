@@ -66,6 +66,59 @@ def test_product_topk_matches_golden_orders(golden_dir):
         assert P.topk_unsorted(_f32(case["corrected_f32_u32"])).tolist() == case["selected_experts"]
 
 
+def _ref_topk(values, count, top_k, out):
+    """Calls the library through the reference's own FFI name and signature (src/text_endpoint.rs:
+    2466-2474): (*const f32, usize, usize, *mut u32) -> i32."""
+    fn = _abi.lib().pw_pytorch_topk_unsorted_f32
+    return fn(values, ctypes.c_size_t(count), ctypes.c_size_t(top_k), out)
+
+
+def test_reference_topk_symbol_return_codes():
+    """src/pytorch_topk.cpp:7-30: -1 for a null values or selected pointer, top_k == 0 or
+    top_k >= count; -2 when the (value, index) buffer cannot be made; 0 otherwise."""
+    v = np.arange(16, dtype=np.float32)
+    out = np.full(16, 0xDEADBEEF, np.uint32)
+    vp, op = v.ctypes.data_as(_abi._f32p), out.ctypes.data_as(_abi._u32p)
+    assert _ref_topk(None, 16, 4, op) == -1
+    assert _ref_topk(vp, 16, 4, None) == -1
+    assert _ref_topk(vp, 16, 0, op) == -1
+    assert _ref_topk(vp, 16, 16, op) == -1
+    assert _ref_topk(vp, 16, 17, op) == -1
+    assert _ref_topk(vp, 0, 1, op) == -1
+    assert (out == 0xDEADBEEF).all()  # rejected calls write nothing
+    # 2^62 pairs exceed std::vector's max_size: the library throws inside and returns -2 before it
+    # reads a single value (the reference's vector<pair<float, int64_t>>(count) throws the same way)
+    assert _ref_topk(vp, 1 << 62, 8, op) == -2
+    assert (out == 0xDEADBEEF).all()
+    assert _ref_topk(vp, 16, 15, op) == 0
+    assert sorted(out[:15].tolist()) == list(range(1, 16))
+    assert out[15] == 0xDEADBEEF  # only top_k indices are written
+
+
+def test_reference_topk_symbol_golden_orders_and_any_k(golden_dir):
+    """The reference's name gives the libc++ partition orders of pw0063 and pw0157; for other k the
+    selected set is the k largest values (brute force) and the order is the oracle's nth_element."""
+    def call(v, k):
+        v = np.ascontiguousarray(v, np.float32)
+        out = np.zeros(k, np.uint32)
+        assert _ref_topk(v.ctypes.data_as(_abi._f32p), v.size, k, out.ctypes.data_as(_abi._u32p)) == 0
+        return out
+
+    fx = _load(golden_dir, "pw0063-topk-order.json")
+    assert call(_f32(fx["corrected_f32_u32"]), 8).tolist() == fx["selected_experts"]
+    for case in _load(golden_dir, "pw0157-pytorch-topk-ties.json")["cases"]:
+        assert call(_f32(case["corrected_f32_u32"]), 8).tolist() == case["selected_experts"]
+    rng = np.random.default_rng(11)
+    for n in (2, 3, 7, 8, 9, 40, 256):
+        for trial in range(6):
+            v = (rng.integers(0, 5, n) if trial % 2 else rng.standard_normal(n)).astype(np.float32)
+            for k in sorted(k for k in {1, 2, n // 2, n - 1} if 0 < k < n):
+                got = call(v, k)
+                assert len(set(got.tolist())) == k
+                assert np.array_equal(np.sort(v[got])[::-1], np.sort(v)[::-1][:k])
+                assert got.tolist() == O.topk_unsorted(v, k).tolist()
+
+
 def test_product_topk_matches_oracle_on_random_and_tied_rows():
     rng = np.random.default_rng(5)
     for trial in range(400):

@@ -284,6 +284,27 @@ def test_closed_form_prefill_production_steps_bit_exact(rt, closed_form_wide, ro
     _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16, prefill=True), want)
 
 
+@pytest.fixture(scope="module")
+def closed_form_production(rt):
+    experts, x, sel, w = closed_form_mode_b(0x50570500, 24, 8, hidden=4096, inter=2048)
+    projs, bank = _bank_from(rt, experts, 8)
+    return experts, x, sel, w, projs, bank
+
+
+def test_closed_form_prefill_production_shape_bit_exact(rt, closed_form_production):
+    """The production expert shape, hidden 4096 and intermediate 2048, top-8 of 8 experts over 24
+    rows: the gate/up GEMM's sixteen rotated 256-column K steps over 4096 stacked gate and up rows,
+    and the down GEMM at its real K of 2048 (eight 256-column steps, four 256-row n-tiles per
+    workgroup). Bit for bit the oracle's layer, raw f32 and bf16."""
+    experts, x, sel, w, _, bank = closed_form_production
+    want, want_raw = O.moe_layer("b", x, experts, 8, sel, w, raw=True)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW, prefill=True), want_raw)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16, prefill=True), want)
+    # the mode-B decode layer on the first eight rows, the same bits
+    want8, want8_raw = O.moe_layer("b", x[:8], experts, 8, sel[:8], w[:8], raw=True)
+    _same_bits(_device_layer(rt, bank, x[:8], sel[:8], w[:8], P.DTYPE_F32_RAW), want8_raw)
+
+
 def test_closed_form_mode_b_device_layer_wide_hidden_bit_exact(rt, closed_form_wide):
     """The mode-B decode layer (eight rows) on the hidden-4096 closed form, bit for bit."""
     experts, x, sel, w, _, bank = closed_form_wide

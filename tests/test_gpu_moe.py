@@ -373,13 +373,14 @@ def test_device_layer_rejects_misaligned_activations(rt, full_bank):
         rt.moe_layer_device(full_bank.bank, x, 1, ids, w, out)
 
 
+@pytest.mark.parametrize("mode", [0, 1], ids=["mode_a", "mode_b"])
 @pytest.mark.parametrize("rows", [1, 8, 9])
-def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
+def test_device_layer_rejects_bad_routes(rt, full_bank, rows, mode):
     """Route buffers with an expert id outside the bank, one token naming an expert twice, or a NaN
     weight raise the schedule error bit (src/wide_metal_moe.rs:858-938 rejects such schedules) from
-    both schedule kernels (8 rows: one wave; 9 rows: one workgroup) and from the one-token layer's
-    own route checks (1 row, no schedule) without faulting, and the next valid call gives the same
-    bytes as before."""
+    both schedule kernels (8 rows: one wave; 9 rows: one workgroup) and from the one-token mode A
+    layer's own route checks (1 row, no schedule) without faulting; every rejected call writes an
+    all-zero output, whichever path took it, and the next valid call gives the same bytes as before."""
     import torch
     x = WL.activations(rows, WL.SEED_BASE + 90)
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
@@ -390,13 +391,14 @@ def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
     def run(ids, wts):
         out = torch.empty((rows, 4096), dtype=torch.float32, device="cuda")
         rt.moe_layer_device(full_bank.bank, xt, rows, torch.from_numpy(ids.astype(np.int32)).cuda(),
-                            torch.from_numpy(wts).cuda(), out, mode=P.MODE_A, out_dtype=P.DTYPE_F32_RAW,
+                            torch.from_numpy(wts).cuda(), out, mode=mode, out_dtype=P.DTYPE_F32_RAW,
                             stream=stream)
         torch.cuda.synchronize()
         return out.cpu().numpy(), rt.take_flags()
 
     clean, flags = run(sel, w)
     assert flags == 0
+    assert np.any(clean != 0)
     bad_id = sel.copy()
     bad_id[rows - 1, 3] = 256
     twice = sel.copy()
@@ -404,8 +406,9 @@ def test_device_layer_rejects_bad_routes(rt, full_bank, rows):
     nan_w = w.copy()
     nan_w[min(1, rows - 1), 5] = np.nan
     for ids, wts in ((bad_id, w), (twice, w), (sel, nan_w)):
-        _, flags = run(ids, wts)
+        out, flags = run(ids, wts)
         assert flags & P.FLAG_SCHEDULE
+        assert not np.any(out.view(np.uint32)), "a rejected batch writes zeros"
     again, flags = run(sel, w)
     assert flags == 0
     assert np.array_equal(clean.view(np.uint32), again.view(np.uint32))

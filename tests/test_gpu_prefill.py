@@ -122,8 +122,9 @@ def _decode_chunks(rt, torch, bank, x, sel, w, chunk=32):
 def test_prefill_matches_decode_chunks(rt, full_bank, rows, zipf):
     """2048 tokens (and the 4096-row maximum), top-8 of 256 experts (16 384 / 32 768 placements):
     the prefill agrees with the decode layer run on 32-row chunks (the same mode B numerics per
-    placement, summed in another order) within the mode B tolerance and, on eight sampled rows, with
-    the oracle."""
+    placement, summed in another order) within the mode B tolerance, and with the oracle on eight
+    rows spread over the batch plus the token rows of the first and last slot of every 128-slot
+    m-tile of the busiest expert (587 placements in five m-tiles under Zipf routing)."""
     import torch
     x = WL.activations(rows, WL.SEED_BASE + 4)
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
@@ -134,8 +135,15 @@ def test_prefill_matches_decode_chunks(rt, full_bank, rows, zipf):
     dec = _decode_chunks(rt, torch, full_bank, x, sel, w)
     assert normwise(got, dec) <= MODE_B_TOL
     assert rel_l2(got, dec) <= 2e-3
-    # oracle on eight sampled rows spread over the batch (only their experts are fetched)
-    pick = np.linspace(0, rows - 1, 8).astype(np.int64)
+    # oracle rows (only their experts are fetched): eight spread over the batch, and the first and
+    # last slot of each m-tile of the busiest expert (its slots hold its token rows in ascending order)
+    hot = int(np.argmax(counts))
+    hot_rows = np.nonzero(np.any(sel == hot, axis=1))[0]
+    assert hot_rows.size == counts[hot]
+    m_tiles = -(-hot_rows.size // 128)
+    ends = [hot_rows[min(128 * t + k, hot_rows.size - 1)] for t in range(m_tiles) for k in (0, 127)]
+    pick = np.unique(np.concatenate([np.linspace(0, rows - 1, 8).astype(np.int64), ends]))
+    print(f"oracle rows {pick.size}: busiest expert {hot}, {counts[hot]} placements, {m_tiles} m-tiles", flush=True)
     used = sorted(set(sel[pick].reshape(-1).tolist()))
     experts = {e: full_bank.expert_host(e) for e in used}
     ref = O.moe_layer("b", x[pick], experts, 256, sel[pick], w[pick])
@@ -169,3 +177,54 @@ def test_prefill_rejects_bad_arguments(rt, small_bank):
         rt.moe_prefill_device(small_bank.bank, x, 0, ids, w, out)
     with pytest.raises(P.PwError, match="ARGUMENT"):
         rt.moe_prefill_device(small_bank.bank, x, 4097, ids, w, out)
+
+
+def test_prefill_rejected_routes_write_zeros(rt, small_bank):
+    """An expert id outside the bank, an expert named twice by one token, or a NaN weight raise the
+    schedule error bit (src/wide_metal_moe.rs:858-938) for short (one-workgroup schedule) and long
+    (three-launch schedule) batches; the output is all zeros, and the next valid batch gives its
+    bytes again."""
+    import torch
+    for rows in (40, 300):
+        rng = np.random.default_rng(900 + rows)
+        x = WL.activations(rows, WL.SEED_BASE + 95, hidden=256)
+        sel, w = _routes(rng, rows, small_bank.n)
+        clean = _prefill(rt, torch, small_bank, x, sel, w, out_dtype=P.DTYPE_F32_RAW)
+        assert np.any(clean)
+        bad_id = sel.copy()
+        bad_id[rows - 1, 3] = small_bank.n
+        twice = sel.copy()
+        twice[rows // 2, 1] = twice[rows // 2, 0]
+        nan_w = w.copy()
+        nan_w[1, 5] = np.nan
+        for ids, wts in ((bad_id, w), (twice, w), (sel, nan_w)):
+            xt = _bf16_dev(torch, x)
+            out = torch.full((rows, 256), 7.0, dtype=torch.float32, device="cuda")
+            rt.moe_prefill_device(small_bank.bank, xt, rows, _dev(torch, ids.astype(np.int32)),
+                                  _dev(torch, wts.astype(np.float32)), out, out_dtype=P.DTYPE_F32_RAW,
+                                  stream=torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            assert rt.take_flags() & P.FLAG_SCHEDULE
+            assert not np.any(out.cpu().numpy().view(np.uint32)), "a rejected batch writes zeros"
+        again = _prefill(rt, torch, small_bank, x, sel, w, out_dtype=P.DTYPE_F32_RAW)
+        assert np.array_equal(clean.view(np.uint32), again.view(np.uint32))
+
+
+def test_prefill_token_results_do_not_depend_on_the_batch(rt, full_bank):
+    """1024 token rows with their routes give the same raw f32 bits inside two batches: after 1024
+    other tokens under Zipf routing (busy experts take several m-tiles, so every later expert's
+    m-tiles sit elsewhere in the grid, and the shared tokens' slots move), and alone. Each gate/up
+    tile's K order depends only on its expert and n-tile group."""
+    import torch
+    shared = WL.activations(1024, WL.SEED_BASE + 96)
+    rw_u, bias_u = WL.router_inputs(WL.SEED_BASE + 3)
+    sel_s, w_s, _ = WL.route_host(shared, rw_u, bias_u)
+    other = WL.activations(1024, WL.SEED_BASE + 97)
+    rw_z, bias_z = WL.router_inputs(WL.SEED_BASE + 3, zipf=True)
+    sel_o, w_o, _ = WL.route_host(other, rw_z, bias_z)
+    assert np.bincount(sel_o.reshape(-1), minlength=256).max() > 128
+    alone = _prefill(rt, torch, full_bank, shared, sel_s, w_s, out_dtype=P.DTYPE_F32_RAW)
+    mixed = _prefill(rt, torch, full_bank, np.concatenate([other, shared]), np.concatenate([sel_o, sel_s]),
+                     np.concatenate([w_o, w_s]), out_dtype=P.DTYPE_F32_RAW)
+    assert np.array_equal(mixed[1024:].view(np.uint32), alone.view(np.uint32))
+    assert np.all(np.isfinite(alone)) and np.any(alone)

@@ -196,3 +196,26 @@ def test_device_router_flags_nonfinite_bias(rt):
     ids, wts, _, _, flags = _device_route(rt, torch, x, rw, bias)
     assert flags & P.FLAG_ROUTE
     assert (ids == 256).all() and (wts == 0).all()
+
+
+def test_device_route_weights_known_answer(rt):
+    """The device router's route weights on the known-answer rows of tests/helpers.py, which pin the
+    reference's denominator (pytorch_sum_eight folded left to right over the selected scores in
+    partition order, + 1e-20; src/text_endpoint.rs:4382-4390, :4450-4452): a tree or plain sum, a
+    sum in expert-id order or a missing 1e-20 would change these bits. Logits enter exactly through
+    a one-hot activation row and f32 router weights whose column 0 holds them."""
+    import torch
+    from helpers import ROUTE_WEIGHT_ROWS, route_weight_row_logits
+    rows, hidden = len(ROUTE_WEIGHT_ROWS), 64
+    x = np.zeros((rows, hidden), np.float32)
+    rw = np.zeros((256, hidden), np.float32)
+    for r, row in enumerate(ROUTE_WEIGHT_ROWS):
+        x[r, r] = 1.0
+        rw[:, r] = route_weight_row_logits(row)
+    ids, wts, scores, ties, flags = _device_route(rt, torch, x, rw, np.zeros(256, np.float32), x_f32=True,
+                                                  w_f32=True)
+    assert flags == 0 and ties == 0
+    for r, row in enumerate(ROUTE_WEIGHT_ROWS):
+        assert ids[r].tolist() == row["selected"]
+        assert scores[r][ids[r]].view(np.uint32).tolist() == row["score_bits"]
+        assert wts[r].view(np.uint32).tolist() == row["weight_bits"]

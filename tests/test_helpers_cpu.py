@@ -73,3 +73,12 @@ def test_closed_form_wide_hidden_meets_its_preconditions():
     experts, x, sel, w = closed_form_mode_b(0x50570400, 40, 8, hidden=4096, inter=512, check=True)
     out = O.moe_layer("b", x[:2], experts, 8, sel[:2], w[:2])
     assert np.all(np.isfinite(out)) and np.any(out)
+
+
+def test_closed_form_production_shape_meets_its_preconditions():
+    """The hidden-4096, intermediate-2048 closed form (the production expert shape: the prefill
+    gate/up's sixteen rotated K steps over 4096 stacked rows, the down GEMM's eight 256-column K
+    steps) at the GPU test's seed and size."""
+    experts, x, sel, w = closed_form_mode_b(0x50570500, 24, 8, hidden=4096, inter=2048, check=True)
+    out = O.moe_layer("b", x[:1], experts, 8, sel[:1], w[:1])
+    assert np.all(np.isfinite(out)) and np.any(out)

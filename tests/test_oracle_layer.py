@@ -25,7 +25,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from helpers import bf16_normal, bf16_round, dequant, fp8_weight, log_uniform_scales
+from helpers import bf16_normal, bf16_round, closed_form_mode_b, dequant, fp8_weight, log_uniform_scales
 
 
 def _bits(x):
@@ -286,8 +286,8 @@ def test_layer_rejects_non_bijective_routes():
 # ------------------------------------------------------------------ staged SwiGLU known answers
 # (gate bits, up bits) -> output bits of round(round(silu(round(g))) * round(u)). The expected
 # outputs come from the exact silu (every case sits more than 64 f32 ulps from a bf16 rounding
-# boundary, so any faithful f32 evaluation gives these bits). `dropped` is the output without the
-# named rounding; each differs from the expected bits.
+# boundary, so any faithful f32 evaluation gives these bits). `dropped` is the output with the named
+# rounding taken out; each differs from the expected bits.
 STAGED_CASES = [
     # the reference's case: gate 1.03125, up 0.71484375 (src/staged_metal_expert.rs:2826-2831)
     dict(g=0x3F840000, u=0x3F370000, out=0x3F0B0000, dropped={}),
@@ -300,16 +300,37 @@ STAGED_CASES = [
     # product exactly halfway between two bf16 values (0xbd968000): ties to the even code
     dict(g=0xC02E0000, u=0x3EE00000, out=0xBD960000, dropped={"product": 0xBD968000}),
 ]
+STAGES = ("gate", "up", "silu", "product")
+
+
+def _staged_f64_silu(g_bits, u_bits, drop=None):
+    """The staged SwiGLU evaluated independently of the oracle, with the stage `drop` left unrounded:
+    bf16 rounding in numpy, silu in f64 (math.exp) rounded once to f32, the product in f32."""
+    def rnd(v, stage):
+        return v if stage == drop else np.float32(bf16_round(np.array([v], np.float32))[0])
+
+    g = rnd(np.float32(_f32(g_bits)), "gate")
+    u = rnd(np.float32(_f32(u_bits)), "up")
+    silu = rnd(np.float32(float(g) / (1.0 + math.exp(-float(g)))), "silu")
+    return _bits(rnd(np.float32(silu * u), "product"))
 
 
 @pytest.mark.parametrize("case", STAGED_CASES, ids=lambda c: hex(c["g"]))
 def test_staged_swiglu_known_answers(case):
+    """The oracle gives the expected bits; the independent evaluation gives them too with every
+    rounding in place, and taking out the named rounding gives the `dropped` bits instead, so a
+    staged SwiGLU missing that rounding would fail here."""
     g = np.array([_f32(case["g"])], np.float32)
     u = np.array([_f32(case["u"])], np.float32)
     got = _bits(O.swiglu_bf16_staged(g, u)[0])
     assert got == case["out"], hex(got)
-    for stage, alt in case["dropped"].items():
-        assert alt != case["out"], stage
+    assert _staged_f64_silu(case["g"], case["u"]) == case["out"]
+    for stage in STAGES:
+        alt = _staged_f64_silu(case["g"], case["u"], drop=stage)
+        if stage in case["dropped"]:
+            assert alt == case["dropped"][stage] and alt != case["out"], (stage, hex(alt))
+    # together the cases pin all four roundings
+    assert {st for c in STAGED_CASES for st in c["dropped"]} == set(STAGES)
 
 
 def test_staged_swiglu_rounds_every_stage():
@@ -388,3 +409,44 @@ def test_blas_layer_thread_pool_and_one_hot():
         pos = sorted({q for q in range(rows) if e in sel[q].tolist()})
         want = O.expert_blas_f32(x[pos], *deq[e])[pos.index(p)]
         assert np.array_equal(got[p], want), p
+
+
+# ------------------------------------------------------------------ the mode-B CPU BLAS restatement
+# (the prefill's and mode-B decode's CPU-baseline legs time it; routed_mlp_traced and fp8_linear,
+# src/text_endpoint.rs:5290-5381, :3053-3108)
+def _deq_bank(experts):
+    return {e: (O.decode_fp8_matrix_f32(ex[0], ex[1]), O.decode_fp8_matrix_f32(ex[2], ex[3]),
+                O.decode_fp8_matrix_f32(ex[4], ex[5])) for e, ex in experts.items()}
+
+
+def test_blas_mode_b_layer_bit_exact_on_closed_form():
+    """On closed-form mode-B data every projection sum is exact in f32 in any order, so the BLAS
+    restatement (BLAS summation order) must give the scalar oracle's layer bit for bit: a missing
+    activation quantisation, bf16 rounding or staged SwiGLU rounding, a swapped gate/up or a
+    transposed projection changes these bits."""
+    experts, x, sel, w = closed_form_mode_b(0x50570100, 256, 12)
+    x, sel, w = x[:24], sel[:24], w[:24]
+    got, got_raw = O.moe_layer_blas_mode_b(x, _deq_bank(experts), sel, w)
+    want, want_raw = O.moe_layer("b", x, experts, 12, sel, w, raw=True)
+    assert np.array_equal(got_raw.view(np.uint32), want_raw.view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [1, 9])
+def test_blas_mode_b_layer_matches_oracle(rows):
+    """Random FP8 data: BLAS sums in another order than the oracle's sequential loop, so a bf16
+    rounding or an e4m3 re-quantisation may land on the other side; within the mode-B tolerance,
+    and bit-equal through a thread pool (experts combined in ascending id either way)."""
+    from concurrent.futures import ThreadPoolExecutor
+    rng = np.random.default_rng(730 + rows)
+    hidden, inter, n_exp = 512, 256, 12
+    experts = _bank(rng, n_exp, hidden, inter)
+    deq = _deq_bank(experts)
+    x = bf16_normal(rng, (rows, hidden))
+    sel, w = _routes(rng, rows, n_exp)
+    got, _ = O.moe_layer_blas_mode_b(x, deq, sel, w)
+    want = O.moe_layer("b", x, experts, n_exp, sel, w)
+    assert np.max(np.abs(got - want)) <= 2e-2 * np.max(np.abs(want))
+    with ThreadPoolExecutor(4) as pool:
+        pooled, _ = O.moe_layer_blas_mode_b(x, deq, sel, w, pool=pool)
+    assert np.array_equal(pooled.view(np.uint32), got.view(np.uint32))

@@ -62,3 +62,40 @@ def test_noalloc_layer_rejects_requests_beyond_its_scratch(rt, bank):
     out1 = torch.empty((1, 128), dtype=torch.int16, device="cuda")
     with pytest.raises(P.PwError, match="intermediate 2048"):
         rt.moe_layer_device_noalloc(wide, x, 1, ids1, w1, out1)
+
+
+@pytest.mark.parametrize("mode", [P.MODE_A, P.MODE_B])
+def test_noalloc_layer_under_graph_capture(rt, bank, mode):
+    """The entry point is for callers under HIP graph capture: after eager calls on two other streams
+    (so the runtime's last call sits on a stream outside the capture), one call captured on a fresh
+    stream is not ordered against that stream (a wait on an event recorded outside the capture is a
+    cross-boundary dependency the capture rejects), and every replay of the graph gives the eager
+    call's bytes. Between replays the program runs its own eager layer calls (on the same static
+    scratch) and synchronises; those keep their bytes too."""
+    import torch
+    s_eager, s_other, s_cap = torch.cuda.Stream(), torch.cuda.Stream(), torch.cuda.Stream()
+    xt, ids, wts = _inputs(torch, 8, 160)
+    x2, ids2, wts2 = _inputs(torch, 8, 161)
+    want = torch.empty((8, 4096), dtype=torch.int16, device="cuda")
+    other = torch.empty((8, 4096), dtype=torch.int16, device="cuda")
+    rt.moe_layer_device_noalloc(bank.bank, xt, 8, ids, wts, want, mode=mode, stream=s_eager.cuda_stream)
+    rt.moe_layer_device_noalloc(bank.bank, x2, 8, ids2, wts2, other, mode=mode, stream=s_other.cuda_stream)
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    got = torch.full((8, 4096), 7, dtype=torch.int16, device="cuda")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s_cap, capture_error_mode="thread_local"):
+        rt.moe_layer_device_noalloc(bank.bank, xt, 8, ids, wts, got, mode=mode, stream=s_cap.cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.all(got == 7), "capturing enqueues nothing"
+    for replay in range(3):
+        got.fill_(7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {replay}"
+        again = torch.empty_like(other)
+        rt.moe_layer_device_noalloc(bank.bank, x2, 8, ids2, wts2, again, mode=mode, stream=s_other.cuda_stream)
+        torch.cuda.synchronize()
+        assert torch.equal(again, other), f"eager call after replay {replay}"
+    assert rt.take_flags() == 0
