@@ -331,9 +331,11 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
     return out
 
 
-def layer_with_router(torch, rt, bank, P, WL, rows=8, steps=200, warmup=20):
-    """One decode step including its routing: the device router (logits, sigmoid + bias, top-8,
-    weights) on the batch's activations, then the width-8 layer on those routes, per step."""
+def layer_with_router(torch, rt, bank, P, WL, rows=8, steps=200, warmup=20, two_calls=False):
+    """One decode step including its routing, per step: the device router (logits, sigmoid + bias,
+    top-8, weights) on the batch's activations, then the width-8 layer on those routes -- as one
+    pw_moe_layer_routed_device call (the route selection and the layer's schedule in one launch), or
+    with two_calls as pw_route_device then pw_moe_layer_device."""
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
     wt = torch.from_numpy(WL.bf16_bits_np(rw).view(np.int16)).cuda()
     bt = torch.from_numpy(bias).cuda()
@@ -344,11 +346,17 @@ def layer_with_router(torch, rt, bank, P, WL, rows=8, steps=200, warmup=20):
 
     def run(i, st):
         x = xs[i % len(xs)]
-        rt.route_device(x, rows, 4096, wt, 256, bt, ids, wts, stream=st)
-        rt.moe_layer_device(bank.bank, x, rows, ids, wts, out, mode=P.MODE_A, out_dtype=P.DTYPE_BF16, stream=st)
+        if two_calls:
+            rt.route_device(x, rows, 4096, wt, 256, bt, ids, wts, stream=st)
+            rt.moe_layer_device(bank.bank, x, rows, ids, wts, out, mode=P.MODE_A, out_dtype=P.DTYPE_BF16,
+                                stream=st)
+        else:
+            rt.moe_layer_routed_device(bank.bank, x, rows, wt, bt, ids, wts, out, mode=P.MODE_A,
+                                       out_dtype=P.DTYPE_BF16, stream=st)
 
     us, sp = _time_calls(torch, rt, run, steps, warmup)
-    return {"us": round(us, 2), "spread_us": sp, "rows": rows}
+    return {"us": round(us, 2), "spread_us": sp, "rows": rows,
+            "calls": "pw_route_device + pw_moe_layer_device" if two_calls else "pw_moe_layer_routed_device"}
 
 
 def router_leg(torch, rt, P, WL, rows=8, calls=200):
@@ -523,6 +531,8 @@ def main():
                     help="run only the 2048-token prefill leg and print its line (for profiling)")
     ap.add_argument("--router-only", action="store_true",
                     help="run only the on-device router leg and print its line (for profiling)")
+    ap.add_argument("--router-layer-only", action="store_true",
+                    help="run only the decode steps with their routing (widths 8 and 1) and print their line")
     ap.add_argument("--routing", choices=("uniform", "zipf"), default="uniform",
                     help="routing of the headline decode leg and of --prefill-only (zipf: for profiling)")
     ap.add_argument("--small-calls-only", action="store_true",
@@ -556,6 +566,16 @@ def main():
         return
     log("synthesising the 256-expert bank (6.4 GB) on the device")
     bank = WL.synth_bank(rt, 256, seed=WL.SEED_BASE + 2)
+    if args.router_layer_only:
+        res = {"router_w8": router_leg(torch, rt, P, WL, calls=args.steps),
+               "layer_plus_router_w8": layer_with_router(torch, rt, bank, P, WL, steps=args.steps),
+               "layer_plus_router_w8_two_calls": layer_with_router(torch, rt, bank, P, WL, steps=args.steps,
+                                                                   two_calls=True),
+               "layer_plus_router_w1": layer_with_router(torch, rt, bank, P, WL, rows=1, steps=args.steps)}
+        print(json.dumps({"workload": "decode steps with their routing, 256 experts, hidden 4096, mode A", **res}),
+              flush=True)
+        rt.close()
+        return
     if args.prefill_only:
         res = prefill_leg(torch, rt, bank, P, WL, zipf=args.routing == "zipf")
         print(json.dumps({"workload": "routed-MoE prefill, 2048 tokens, top-8 of 256 experts, mode B, "
@@ -620,6 +640,8 @@ def main():
             extras["prefill_t2048" + ("_zipf" if zipf else "")] = prefill_leg(torch, rt, bank, P, WL, zipf)
         extras["router_w8"] = router_leg(torch, rt, P, WL)
         extras["layer_plus_router_w8"] = layer_with_router(torch, rt, bank, P, WL)
+        extras["layer_plus_router_w8_two_calls"] = layer_with_router(torch, rt, bank, P, WL, two_calls=True)
+        extras["layer_plus_router_w1"] = layer_with_router(torch, rt, bank, P, WL, rows=1)
         extras.update(projection_legs(torch, rt, bank, P, WL))
         for k, v in extras.items():
             if isinstance(v, dict) and k != "kernels_us":

@@ -150,7 +150,8 @@ int pw_runtime_take_flags(pw_runtime *rt, uint32_t *flags);
  * command buffer, src/staged_metal_expert.rs:1763-1771): when enabled, every timed launch records
  * a start and a stop event on the stream it runs on, up to max_launches (0 disables). Kernel
  * names: linear_a, linear_b, quant, moe_schedule, moe_gateup, moe_swiglu, moe_down, moe_combine,
- * prefill_gateup, prefill_down, router, bf16_linear. */
+ * prefill_gateup, prefill_down, router, bf16_linear, route_schedule (the route selection and schedule
+ * launch of pw_moe_layer_routed_device). */
 int pw_runtime_enable_timing(pw_runtime *rt, uint32_t max_launches);
 /* Synchronise the device; report the recorded launches of `kernel` and their summed duration. */
 int pw_runtime_timing_summary(pw_runtime *rt, const char *kernel, uint32_t *launches,
@@ -288,6 +289,21 @@ int pw_expert_bank_shape(const pw_expert_bank *bank, uint32_t *n_experts, uint32
 int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
                         uint32_t x_dtype, uint32_t rows, const uint32_t *route_ids,
                         const float *route_weights, void *output, uint32_t out_dtype, void *stream);
+
+/* A decode step's routing and its routed layer in one call on device buffers: route_mlp
+ * (src/text_endpoint.rs:4342-4380, as pw_route_device runs it over the bank's experts: router_weight
+ * [n_experts x hidden] f32 or bf16, bias [n_experts]) followed by the routed layer on those routes
+ * (as pw_moe_layer_device), the composition routed_mlp_traced (src/text_endpoint.rs:5290-5381) makes.
+ * The routes are also written to route_ids / route_weights [rows x 8] (16-byte aligned), the
+ * reference's RoutingTrace. For decode batches of up to 8 rows over banks of up to 256 experts the
+ * route selection and the layer's schedule run in one launch. The same routes and the same output
+ * bytes as pw_route_device then pw_moe_layer_device. A row whose routing fails raises
+ * PW_FLAG_ROUTE, and the batch is rejected like invalid routes (PW_FLAG_SCHEDULE, zero output).
+ * rows 1..32; hidden a multiple of 8; x and router_weight 16-byte aligned. Asynchronous on stream. */
+int pw_moe_layer_routed_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
+                               uint32_t x_dtype, uint32_t rows, const void *router_weight, uint32_t w_dtype,
+                               const float *bias, uint32_t *route_ids, float *route_weights, void *output,
+                               uint32_t out_dtype, void *stream);
 
 /* No counterpart in the reference: pw_moe_layer_device for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

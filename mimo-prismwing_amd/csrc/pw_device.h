@@ -218,6 +218,49 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
+// One wave's primitives for code written against a wave policy (pw_select_wave.h): lane id,
+// ballot, a lane's value (the lane index wave-uniform), the value of the lane below, the wave
+// maximum, and LDS ordering between the wave's own lanes (its LDS operations complete in order).
+struct DeviceWave {
+    __device__ __forceinline__ uint32_t lane() const { return __lane_id(); }
+    __device__ __forceinline__ uint64_t ballot(bool b) const { return __ballot(b); }
+    __device__ __forceinline__ uint32_t readlane(uint32_t v, uint32_t l) const
+    {
+        return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+    }
+    __device__ __forceinline__ int32_t readlane(int32_t v, uint32_t l) const
+    {
+        return __builtin_amdgcn_readlane(v, (int)l);
+    }
+    __device__ __forceinline__ float readlane(float v, uint32_t l) const
+    {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), (int)l));
+    }
+    __device__ __forceinline__ uint32_t below(uint64_t m) const
+    {
+        return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    }
+    // v (wave-uniform) into lane l of a register
+    __device__ __forceinline__ float writelane(float old, float v, uint32_t l) const { return lane() == l ? v : old; }
+    __device__ __forceinline__ int32_t writelane(int32_t old, int32_t v, uint32_t l) const
+    {
+        return lane() == l ? v : old;
+    }
+    __device__ __forceinline__ float shift_up1(float v) const { return __shfl_up(v, 1, 64); }
+    __device__ __forceinline__ float max_all(float v) const
+    {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(v, off, 64);
+            v = o > v ? o : v;
+        }
+        return v;
+    }
+    __device__ __forceinline__ float shfl(float v, uint32_t src) const { return __shfl(v, (int)src, 64); }
+    __device__ __forceinline__ void lds_sync() const { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+    __device__ __forceinline__ void mark() const {}
+};
+
 __device__ __forceinline__ void raise_flag(uint32_t *flags, uint32_t bit)
 {
     if (flags)

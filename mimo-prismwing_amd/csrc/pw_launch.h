@@ -23,6 +23,7 @@ enum KernelId : uint32_t {
     K_PREFILL_DOWN,
     K_ROUTER,
     K_BF16_LINEAR,
+    K_ROUTE_SCHEDULE,
     K_COUNT
 };
 
@@ -226,6 +227,18 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
 void launch_router(const void *x, bool x_f32, const void *w, bool w_f32, const float *bias, uint32_t rows,
                    uint32_t E, uint32_t K, float *scores, uint32_t *selected, float *weights, uint32_t *tie_rows,
                    uint32_t *flags, hipStream_t stream);
+// Its scores kernel alone (scores [rows][E]) and its selection alone (from scores).
+void launch_router_scores(const void *x, bool x_f32, const void *w, bool w_f32, uint32_t rows, uint32_t E,
+                          uint32_t K, float *scores, hipStream_t stream);
+void launch_router_select(const float *scores, const float *bias, uint32_t rows, uint32_t E, uint32_t *selected,
+                          float *weights, uint32_t *tie_rows, uint32_t *flags, hipStream_t stream);
+// A decode batch's routes and its schedule in one launch (pw_moe.hip): each row's top-8 and weights
+// from its router scores (the router's selection, written to selected / weights) and the one-wave
+// schedule built from them, as launch_moe_schedule would build it. False (nothing launched) when
+// the batch does not fit it (rows <= 8, 9 <= E <= 256).
+bool launch_route_schedule(const float *scores, const float *bias, const ExpertPtrs *bank, uint32_t rows, uint32_t E,
+                           uint32_t max_active, uint32_t *selected, float *weights, uint32_t *tie_rows,
+                           const MoeBuffers &mb, uint32_t *flags, hipStream_t stream);
 
 // Routed-MoE prefill (mode B grouped block-FP8 GEMM, pw_prefill.hip) after launch_moe_schedule.
 struct PrefillBuffers {

@@ -31,7 +31,12 @@ struct Acc {
 // ------------------------------------------------------------------------------------ mode A
 // Activations arrive as NS bf16 planes [NS][W][K] (NS = 1: bf16 input; NS = 3: an f32 input split
 // exactly into hi + mid + lo), so the inner loop does no conversion work on them.
-template <int NS, int KSPLIT, int NT, int BPW>
+// STAGE: each wave first copies its round's activation columns of the W rows into its own LDS region
+// with direct-to-LDS loads (no registers), then issues its weight loads; those copies are the oldest
+// loads in the in-order memory counter, so block j's MFMAs start when block j's weights arrive. The
+// unstaged form reads the activations from global memory inside the MFMA loop, after every weight
+// load of the round, so each round's first MFMA also waits for those reads.
+template <int NS, int KSPLIT, int NT, int BPW, bool STAGE>
 __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
     const ProjTile *__restrict__ tiles, uint32_t n_tiles, const uint16_t *__restrict__ x, uint32_t W,
     uint32_t K, float *__restrict__ y_f32, uint16_t *__restrict__ y_bf16, uint32_t N,
@@ -42,6 +47,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane >> 4, r16 = lane & 15;
     __shared__ f32x4 red[KSPLIT > 1 ? KSPLIT : 1][NT][64];
+    extern __shared__ uint4 lds_xa[];  // STAGE: per wave [NS][W][ROW] 16-byte units
+    constexpr uint32_t UNITS = BPW * 16, ROW = UNITS + 1;  // a row's units per round (+1: bank spread)
+    uint4 *xs = lds_xa + (size_t)wave * NS * W * ROW;
     const uint32_t blocks = K >> 7;
 
     for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
@@ -57,6 +65,20 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
         // block scale of them before its first MFMA
         for (uint32_t round = 0; round < blocks; round += KSPLIT * BPW) {
             const uint32_t b0 = round + (uint32_t)wave * BPW;
+            // whole rounds: this wave issues exactly 2 BPW weight loads after its copies
+            const bool whole = b0 + BPW <= blocks;
+            if constexpr (STAGE) {
+                // the wave's columns [128 b0, 128 (b0 + BPW)) of every activation row (whole blocks
+                // only; a partial round copies the blocks it has)
+                const uint32_t units = (b0 < blocks ? (blocks - b0 < (uint32_t)BPW ? blocks - b0 : BPW) : 0) * 16;
+                for (uint32_t s = 0; s < (uint32_t)NS; ++s)
+                    for (uint32_t t = 0; t < W; ++t)
+                        for (uint32_t u0 = 0; u0 < units; u0 += 64)
+                            if (u0 + (uint32_t)lane < units)
+                                lds_load16(x + s * plane + (size_t)t * K + ((size_t)b0 << 7) + (u0 + lane) * 8,
+                                           xs + (s * W + t) * ROW + u0);
+                asm volatile("" ::: "memory");  // the copies stay the oldest memory operations
+            }
             uint4 wv[BPW][2];
             float sc[BPW];
 #pragma unroll
@@ -72,6 +94,13 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
                     }
                     sc[j] = tile.s[b];
                 }
+            }
+            if constexpr (STAGE) {
+                // every load but this wave's youngest 2 BPW weight loads: its copies have landed
+                if (whole)
+                    wait_vmcnt<2 * BPW>();
+                else
+                    wait_vmcnt<0>();
             }
 #pragma unroll
             for (int j = 0; j < BPW; ++j) {
@@ -94,9 +123,15 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
                         for (int s = 0; s < NS; ++s) {
                             uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
                             if (token < W) {
-                                const uint4 *xp = (const uint4 *)(x + s * plane + (size_t)token * K + col);
-                                x0 = xp[0];
-                                x1 = xp[1];
+                                if constexpr (STAGE) {
+                                    const uint4 *xp = xs + (s * W + token) * ROW + j * 16 + half * 8 + q * 2;
+                                    x0 = xp[0];
+                                    x1 = xp[1];
+                                } else {
+                                    const uint4 *xp = (const uint4 *)(x + s * plane + (size_t)token * K + col);
+                                    x0 = xp[0];
+                                    x1 = xp[1];
+                                }
                             }
                             acc[nt] = mfma_bf16_16x16x32(a0, bf16x8_from_u4(x0), acc[nt]);
                             acc[nt] = mfma_bf16_16x16x32(a1, bf16x8_from_u4(x1), acc[nt]);
@@ -109,6 +144,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
                     for (int i = 0; i < 4; ++i)
                         total[nt][i] = __builtin_fmaf(sc[j], acc[nt][i], total[nt][i]);
             }
+            if constexpr (STAGE)
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next copies
         }
 
         if constexpr (KSPLIT > 1) {
@@ -329,20 +366,35 @@ static LinearSplit pick_split(uint32_t blocks, uint32_t W, uint32_t n_tiles)
     return LinearSplit{(int)ks, (int)bpw};
 }
 
+// LDS of the staged form: KSPLIT waves x NS planes x W rows x (16 BPW + 1) 16-byte units.
+static size_t staged_lds(int ns, int ksplit, int bpw, uint32_t W)
+{
+    return (size_t)ksplit * ns * W * (16 * bpw + 1) * 16;
+}
+
+// The staged form takes batches of up to 8 rows whose activations fit 80 KB of LDS per workgroup
+// (eight rows of a 4096-column projection at four waves: 66 KB, two workgroups per CU).
+constexpr size_t LINEAR_STAGE_LDS = 80 * 1024;
+
 template <int NS, int KSPLIT, int BPW>
 static void launch_a_split(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, uint32_t W, uint32_t K,
                            float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32, hipStream_t stream)
 {
     const int grid = grid_for(n_tiles, 65535);
-    if constexpr (KSPLIT == 16)
-        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
-                           n_tiles, x, W, K, y32, y16, N, round_f32);
-    else if (W <= 16)
-        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
-                           n_tiles, x, W, K, y32, y16, N, round_f32);
-    else
-        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 2, BPW>), dim3(grid), dim3(64 * KSPLIT), 0, stream, tiles,
-                           n_tiles, x, W, K, y32, y16, N, round_f32);
+    const size_t lds = staged_lds(NS, KSPLIT, BPW, W);
+    if (W <= 8 && lds + sizeof(f32x4) * KSPLIT * 64 <= LINEAR_STAGE_LDS) {
+        if (lds > 48 * 1024)
+            (void)hipFuncSetAttribute((const void *)linear_a_kernel<NS, KSPLIT, 1, BPW, true>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW, true>), dim3(grid), dim3(64 * KSPLIT), lds, stream,
+                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+    }
+    else if (KSPLIT == 16 || W <= 16)
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW, false>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
+                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+    else if constexpr (KSPLIT < 16)
+        hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 2, BPW, false>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
+                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
 }
 
 template <int NS>

@@ -17,6 +17,7 @@
 // token's eight placements in ascending expert id (the reference's order) before the bf16 round.
 #include "pw_device.h"
 #include "pw_launch.h"
+#include "pw_select_wave.h"
 
 namespace pw {
 
@@ -541,31 +542,32 @@ __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, int lane)
     return v;
 }
 
-__global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
-    const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids, const float *__restrict__ weights,
-    uint32_t rows, uint32_t E, uint32_t max_active, MoePlan *plan, uint32_t *__restrict__ active_expert,
-    uint32_t *__restrict__ active_offset, ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos,
-    float *__restrict__ placement_w, uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces,
-    uint32_t max_pieces, uint32_t *flags)
+// LDS of the one-wave schedule besides the bank's pointer table.
+struct SchedWaveLds {
+    uint32_t bitmap[32];      // routed expert ids (E <= 1024)
+    uint32_t expert_of[64];   // by rank
+    uint32_t count_of[64];
+    uint16_t tok_of[64 * 16]; // token rows of each expert's first 16 placements
+};
+
+// Orders the LDS accesses of one wave's lanes (its LDS operations complete in order; this waits for
+// them and keeps the compiler from moving memory accesses across).
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// The one-wave schedule on lane a's route (id, w) (lanes a < rows * 8; the rest pass zeros), with
+// the bank's pointer table already in lds_bank (E x 48 bytes) and visible to this wave. Only this
+// wave touches `lds`, so it needs no workgroup barrier (the routed-layer entry that selects the
+// routes runs it after its other waves have left).
+__device__ __forceinline__ void schedule_wave_body(
+    uint32_t id, float w, uint32_t rows, uint32_t E, uint32_t max_active, const u32x4 *lds_bank, SchedWaveLds &lds,
+    MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
+    ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
+    uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces, uint32_t max_pieces, uint32_t *flags)
 {
-    extern __shared__ u32x4 lds_bank[];  // the bank's ExpertPtrs table, E x 48 bytes
-    __shared__ uint32_t bitmap[32];      // routed expert ids (E <= 1024)
-    __shared__ uint32_t expert_of[64];   // by rank
-    __shared__ uint32_t count_of[64];
-    __shared__ uint16_t tok_of[64 * 16]; // token rows of each expert's first 16 placements
-    const int lane = threadIdx.x;
+    uint32_t *bitmap = lds.bitmap, *expert_of = lds.expert_of, *count_of = lds.count_of;
+    uint16_t *tok_of = lds.tok_of;
+    const int lane = threadIdx.x & 63;
     const uint32_t P = rows * 8;
-    // the routes and the whole pointer table go out together (one memory round trip in all)
-    uint32_t id = 0;
-    float w = 0.f;
-    if ((uint32_t)lane < P) {
-        id = ids[lane];
-        w = weights[lane];
-    }
-    const uint32_t units = E * 3;  // 16-byte units of the table
-    for (uint32_t u0 = 0; u0 < units; u0 += 64)
-        if (u0 + (uint32_t)lane < units)
-            lds_load16((const u32x4 *)bank + u0 + lane, lds_bank + u0);
     const uint32_t nw = (E + 31) >> 5;
     if ((uint32_t)lane < nw)
         bitmap[lane] = 0u;
@@ -586,10 +588,10 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
     ok &= !dup;
     const bool bad = __ballot((uint32_t)lane < P && !ok) != 0;
     const uint64_t valid = __ballot(ok);
-    __syncthreads();
+    wave_lds_sync();
     if (ok)
         atomicOr(&bitmap[id >> 5], 1u << (id & 31));
-    __syncthreads();
+    wave_lds_sync();
     // rank of this lane's expert: routed ids below it
     const uint32_t word = (uint32_t)lane < nw ? bitmap[lane] : 0u;
     const uint32_t wc = __popc(word);
@@ -616,7 +618,7 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
         const uint32_t o = __shfl(id, base + m, 64);
         before += (((valid >> (base + m)) & 1u) && o < id) ? 1u : 0u;
     }
-    __syncthreads();
+    wave_lds_sync();
     // lane a: the a-th routed expert
     const uint32_t a = (uint32_t)lane;
     const uint32_t e_a = a < U ? expert_of[a] : 0u;
@@ -629,8 +631,7 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
         if (t < 16)
             tok_of[rank * 16 + t] = (uint16_t)(lane >> 3);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // the table copy has landed in LDS
-    __syncthreads();
+    wave_lds_sync();
     u32x4 ep0 = {0u, 0u, 0u, 0u}, ep1 = ep0, ep2 = ep0;
     if (a < U && a < max_active) {
         ep0 = lds_bank[e_a * 3];
@@ -706,6 +707,112 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
         if (bad)
             raise_flag(flags, FLAG_SCHEDULE);
     }
+}
+
+
+__global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
+    const ExpertPtrs *__restrict__ bank, const uint32_t *__restrict__ ids, const float *__restrict__ weights,
+    uint32_t rows, uint32_t E, uint32_t max_active, MoePlan *plan, uint32_t *__restrict__ active_expert,
+    uint32_t *__restrict__ active_offset, ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos,
+    float *__restrict__ placement_w, uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces,
+    uint32_t max_pieces, uint32_t *flags)
+{
+    extern __shared__ u32x4 lds_bank[];  // the bank's ExpertPtrs table, E x 48 bytes
+    __shared__ SchedWaveLds sl;
+    const int lane = threadIdx.x;
+    const uint32_t P = rows * 8;
+    // the routes and the whole pointer table go out together (one memory round trip in all)
+    uint32_t id = 0;
+    float w = 0.f;
+    if ((uint32_t)lane < P) {
+        id = ids[lane];
+        w = weights[lane];
+    }
+    const uint32_t units = E * 3;  // 16-byte units of the table
+    for (uint32_t u0 = 0; u0 < units; u0 += 64)
+        if (u0 + (uint32_t)lane < units)
+            lds_load16((const u32x4 *)bank + u0 + lane, lds_bank + u0);
+    __builtin_amdgcn_s_waitcnt(0);  // the table copy has landed in LDS (and the routes are in)
+    schedule_wave_body(id, w, rows, E, max_active, lds_bank, sl, plan, active_expert, active_offset, active,
+                       placement_pos, placement_w, row_slots, pieces, max_pieces, flags);
+}
+
+// A decode batch's routes and its schedule in one launch. Wave r < rows selects row r's routes
+// from its router scores (select_route_row: pytorch_noaux_routes, src/text_endpoint.rs:4394-4473,
+// as the router's own selection kernel runs it) and writes them out; meanwhile all waves copy the
+// bank's pointer table into LDS; wave 0 then builds the schedule from the routes in LDS
+// (schedule_wave_body), the schedule moe_schedule_wave_kernel builds from the same routes. A row
+// whose routing fails raises FLAG_ROUTE and gets ids E, which the schedule rejects.
+template <int NC>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void route_schedule_kernel(
+    const float *__restrict__ scores, const float *__restrict__ bias, const ExpertPtrs *__restrict__ bank,
+    uint32_t rows, uint32_t E, uint32_t max_active, uint32_t *__restrict__ route_ids, float *__restrict__ route_w,
+    uint32_t *tie_rows, MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
+    ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
+    uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces, uint32_t max_pieces, uint32_t *flags)
+{
+    extern __shared__ u32x4 lds_bank[];  // the bank's ExpertPtrs table, E x 48 bytes
+    __shared__ TopkEntry pairs[8][64 * NC];
+    __shared__ uint32_t r_id[64];
+    __shared__ float r_w[64];
+    __shared__ SchedWaveLds sl;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const uint32_t units = E * 3;  // 16-byte units of the table
+    for (uint32_t u0 = wave * 64; u0 < units; u0 += 512)
+        if (u0 + lane < units)
+            lds_load16((const u32x4 *)bank + u0 + lane, lds_bank + u0);
+    if (wave < rows) {
+        DeviceWave w;
+        uint32_t sel_k;
+        float w_k;
+        bool tie = false;
+        const int st = select_route_row<NC>(w, scores + (size_t)wave * E, bias, E, pairs[wave], sel_k, w_k, &tie);
+        if (st != ROUTE_OK) {
+            sel_k = E;
+            w_k = 0.0f;
+            tie = false;
+            if (lane == 0)
+                raise_flag(flags, FLAG_ROUTE);
+        }
+        if (lane < 8) {
+            route_ids[(size_t)wave * 8 + lane] = sel_k;
+            route_w[(size_t)wave * 8 + lane] = w_k;
+            r_id[wave * 8 + lane] = sel_k;
+            r_w[wave * 8 + lane] = w_k;
+        }
+        if (lane == 0 && tie && tie_rows)
+            atomicAdd(tie_rows, 1u);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the table copy has landed in LDS
+    __syncthreads();
+    if (wave != 0)
+        return;
+    const uint32_t P = rows * 8;
+    const uint32_t id = lane < P ? r_id[lane] : 0u;
+    const float wgt = lane < P ? r_w[lane] : 0.f;
+    schedule_wave_body(id, wgt, rows, E, max_active, lds_bank, sl, plan, active_expert, active_offset, active,
+                       placement_pos, placement_w, row_slots, pieces, max_pieces, flags);
+}
+
+bool launch_route_schedule(const float *scores, const float *bias, const ExpertPtrs *bank, uint32_t rows, uint32_t E,
+                           uint32_t max_active, uint32_t *selected, float *weights, uint32_t *tie_rows,
+                           const MoeBuffers &mb, uint32_t *flags, hipStream_t stream)
+{
+    if (rows < 1 || rows > 8 || E < 9 || E > 256 || max_active > 64)
+        return false;
+    const size_t table = (size_t)E * sizeof(ExpertPtrs);  // <= 12 KB
+    const int t = timer_begin(K_ROUTE_SCHEDULE, stream);
+#define PW_RS(NC)                                                                                                  \
+    hipLaunchKernelGGL(route_schedule_kernel<NC>, dim3(1), dim3(512), table, stream, scores, bias, bank, rows, E,  \
+                       max_active, selected, weights, tie_rows, mb.plan, mb.active_expert, mb.active_offset,       \
+                       mb.active, mb.placement_pos, mb.placement_w, mb.row_slots, mb.pieces, rows * 8, flags)
+    if (E <= 64) PW_RS(1);
+    else if (E <= 128) PW_RS(2);
+    else PW_RS(4);
+#undef PW_RS
+    timer_end(t, stream);
+    return true;
 }
 
 // --------------------------------------------------------------- shared tile preamble

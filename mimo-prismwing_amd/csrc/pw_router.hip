@@ -9,11 +9,12 @@
 // is (w0 + w1) + (w2 + w3). The reference's order belongs to Apple Accelerate's SGEMM, which is
 // closed; any fixed order is within the routes' tolerance of it, and this one is restated by the
 // oracle so the device routes can be checked bit for bit. Scores are the PyTorch sigmoid on the
-// SLEEF expf_u10 restatement; the selection and weights are pytorch_noaux_routes (pw_topk.h),
-// with nth_element's partitions split across a wave (same result, same partition order).
+// SLEEF expf_u10 restatement; the selection and weights are pytorch_noaux_routes (pw_topk.h), with
+// nth_element run on the row held in one wave's registers (pw_select_wave.h: the same result, the
+// same partition order).
 #include "pw_device.h"
 #include "pw_launch.h"
-#include "pw_topk.h"
+#include "pw_select_wave.h"
 
 namespace pw {
 
@@ -88,194 +89,40 @@ __global__ __launch_bounds__(256) void router_scores_kernel(const TX *__restrict
     }
 }
 
-__device__ __forceinline__ uint32_t lanes_below(uint64_t mask)
-{
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
-__device__ __forceinline__ uint64_t wave_ballot(bool b) { return __ballot(b); }
-
-// libc++ nth_element(a, a + nth, a + n) run by one whole wave on LDS. The steps that touch a few
-// elements (median of three, small ranges, the rare all-not-greater fallback, the pivot fix-up) are
-// run by every lane alike on the same LDS words; the Hoare partition is split across the lanes:
-// with A the ascending positions in [first + 1, j0] not greater than the pivot and B the descending
-// positions in [first, j0 - 1] greater than it, the serial loop swaps A[t] with B[t] exactly while
-// A[t] < B[t], stops i at min(A[T], B[T - 1]) (A[0] if T = 0) and moves the pivot from A[r] to B[r]
-// when r < T. `apos` and `bpos` hold n positions each.
-__device__ void nth_element_wave(TopkEntry *a, uint32_t nth, uint32_t n, uint32_t *apos, uint32_t *bpos,
-                                 uint32_t lane)
-{
-    uint32_t first = 0, last = n;
-    for (;;) {
-        if (nth == last)
-            return;
-        if (topk_small(a + first, a + last))
-            return;
-        const uint32_t len = last - first;
-        uint32_t m = first + len / 2;
-        const uint32_t lm1 = last - 1;
-        unsigned swaps = topk_sort3(a + first, a + m, a + lm1);
-        __syncthreads();
-        const float pv = a[m].v;
-        uint32_t j0 = lm1;
-        if (!(a[first].v > pv)) {
-            // guard: the highest position in (first, lm1) greater than the pivot
-            int32_t q = -1;
-            for (int32_t c = (int32_t)lm1 - 1; c > (int32_t)first && q < 0; c -= 64) {
-                const int32_t p = c - (int32_t)lane;
-                const uint64_t mask = wave_ballot(p > (int32_t)first && a[p].v > pv);
-                if (mask)
-                    q = c - (int32_t)__builtin_ctzll(mask);
-            }
-            if (q >= 0) {
-                topk_swap(a[first], a[q]);
-                ++swaps;
-                j0 = (uint32_t)q;
-                __syncthreads();
-            } else {
-                TopkEntry *next;
-                const bool done = topk_fallback_partition(a + first, a + nth, a + last, &next);
-                __syncthreads();
-                if (done)
-                    return;
-                first = (uint32_t)(next - a);
-                continue;
-            }
-        }
-        uint32_t i = first + 1;
-        if (i < j0) {
-            const uint32_t i0 = i;
-            uint32_t na = 0, mrank = 0;
-            for (uint32_t c = i0; c <= j0; c += 64) {
-                const uint32_t p = c + lane;
-                const bool ng = p <= j0 && !(a[p].v > pv);
-                const uint64_t mask = wave_ballot(ng);
-                if (ng)
-                    apos[na + lanes_below(mask)] = p;
-                if (m > c) {
-                    const uint64_t below_m = m - c >= 64 ? ~0ull : ((1ull << (m - c)) - 1);
-                    mrank += (uint32_t)__builtin_popcountll(mask & below_m);
-                }
-                na += (uint32_t)__builtin_popcountll(mask);
-            }
-            uint32_t nb = 0;
-            for (int32_t c = (int32_t)j0 - 1; c >= (int32_t)first; c -= 64) {
-                const int32_t p = c - (int32_t)lane;
-                const bool gt = p >= (int32_t)first && a[p].v > pv;
-                const uint64_t mask = wave_ballot(gt);
-                if (gt)
-                    bpos[nb + lanes_below(mask)] = (uint32_t)p;
-                nb += (uint32_t)__builtin_popcountll(mask);
-            }
-            __syncthreads();
-            const uint32_t pairs = na < nb ? na : nb;
-            uint32_t T = 0;
-            for (uint32_t c = 0; c < pairs; c += 64) {
-                const uint32_t t = c + lane;
-                const uint64_t mask = wave_ballot(t < pairs && apos[t] < bpos[t]);
-                T += (uint32_t)__builtin_popcountll(mask);
-                if (~mask)
-                    break;
-            }
-            i = T > 0 ? (apos[T] < bpos[T - 1] ? apos[T] : bpos[T - 1]) : apos[0];
-            if (m >= i0 && m <= j0 && mrank < T)
-                m = bpos[mrank];
-            for (uint32_t c = 0; c < T; c += 64) {
-                const uint32_t t = c + lane;
-                if (t < T) {
-                    const uint32_t pa = apos[t], pb = bpos[t];
-                    const TopkEntry ea = a[pa], eb = a[pb];
-                    a[pa] = eb;
-                    a[pb] = ea;
-                }
-            }
-            swaps += T;
-            __syncthreads();
-        }
-        if (i != m && a[m].v > a[i].v) {
-            topk_swap(a[i], a[m]);
-            ++swaps;
-        }
-        __syncthreads();
-        if (nth == i)
-            return;
-        if (swaps == 0) {
-            // already partitioned: is the side holding nth non-increasing?
-            const uint32_t lo = nth < i ? first : i, end = nth < i ? i : last;
-            bool sorted = true;
-            for (uint32_t c = lo + 1; c < end && sorted; c += 64) {
-                const uint32_t k = c + lane;
-                sorted = wave_ballot(k < end && a[k].v > a[k - 1].v) == 0;
-            }
-            if (sorted)
-                return;
-        }
-        if (nth < i)
-            last = i;
-        else
-            first = i + 1;
-    }
-}
-
-// One wave per row: the lanes stage the row's corrected scores in LDS with coalesced loads, the
-// wave runs the top-8 partition, the rejected maximum is a wave reduction, and lane 0 finishes the
-// row. A row that fails (non-finite score or bias, a broken top-k, invalid weights) raises
-// FLAG_ROUTE and gets expert ids E (which the layer schedule rejects) with zero weights.
+// One wave per row: the row's corrected scores stay in the wave's registers (position p = 64 c +
+// lane in register c), select_route_row runs the top-8 partition on them (pw_select_wave.h), and
+// lane 0 writes the row. A row that fails (non-finite score or bias, a broken top-k, invalid
+// weights) raises FLAG_ROUTE and gets expert ids E (which the layer schedule rejects) with zero
+// weights.
+template <int NC>
 __global__ __launch_bounds__(64) void router_select_kernel(const float *__restrict__ scores,
                                                            const float *__restrict__ bias, uint32_t rows,
                                                            uint32_t E, uint32_t *__restrict__ selected,
                                                            float *__restrict__ weights, uint32_t *tie_rows,
                                                            uint32_t *flags)
 {
-    extern __shared__ uint4 lds_sel[];  // E TopkEntry, E scores, E + E positions
-    const uint32_t p = blockIdx.x, lane = threadIdx.x;
+    __shared__ TopkEntry lds_pairs[64 * NC];
+    const uint32_t p = blockIdx.x;
     if (p >= rows)
         return;
-    TopkEntry *ent = (TopkEntry *)lds_sel;
-    float *s_row = (float *)(ent + E);
-    uint32_t *apos = (uint32_t *)(s_row + E), *bpos = apos + E;
-    bool bad = false;
-    for (uint32_t e = lane; e < E; e += 64) {
-        const float s = scores[(size_t)p * E + e], b = bias[e];
-        bad |= !finite_f32_bits(s) || !finite_f32_bits(b);
-        s_row[e] = s;
-        ent[e].v = s + b;
-        ent[e].i = (int32_t)e;
-    }
-    const bool any_bad = wave_ballot(bad) != 0;
-    __syncthreads();
-    uint32_t sel[8];
-    float wt[8];
+    DeviceWave w;
+    uint32_t sel_k;
+    float w_k;
     bool tie = false;
-    int st = ROUTE_NONFINITE;
-    if (!any_bad) {
-        nth_element_wave(ent, 7, E, apos, bpos, lane);
-        float rejected = -__builtin_inff();
-        for (uint32_t k = 8 + lane; k < E; k += 64)
-            rejected = ent[k].v > rejected ? ent[k].v : rejected;
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float o = __shfl_xor(rejected, off, 64);
-            rejected = o > rejected ? o : rejected;
-        }
-        st = noaux_finish_row(s_row, ent, rejected, sel, wt, &tie);
-    }
-    if (lane != 0)
-        return;
+    const int st = select_route_row<NC>(w, scores + (size_t)p * E, bias, E, lds_pairs, sel_k, w_k, &tie);
+    const uint32_t lane = w.lane();
     if (st != ROUTE_OK) {
-        raise_flag(flags, FLAG_ROUTE);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            sel[k] = E;
-            wt[k] = 0.0f;
-        }
+        sel_k = E;
+        w_k = 0.0f;
         tie = false;
+        if (lane == 0)
+            raise_flag(flags, FLAG_ROUTE);
     }
-    *(uint4 *)(selected + (size_t)p * 8) = make_uint4(sel[0], sel[1], sel[2], sel[3]);
-    *(uint4 *)(selected + (size_t)p * 8 + 4) = make_uint4(sel[4], sel[5], sel[6], sel[7]);
-    *(float4 *)(weights + (size_t)p * 8) = make_float4(wt[0], wt[1], wt[2], wt[3]);
-    *(float4 *)(weights + (size_t)p * 8 + 4) = make_float4(wt[4], wt[5], wt[6], wt[7]);
-    if (tie && tie_rows)
+    if (lane < 8) {
+        selected[(size_t)p * 8 + lane] = sel_k;
+        weights[(size_t)p * 8 + lane] = w_k;
+    }
+    if (lane == 0 && tie && tie_rows)
         atomicAdd(tie_rows, 1u);
 }
 
@@ -292,17 +139,36 @@ static void launch_scores_x(const TX *x, const void *w, bool w_f32, uint32_t row
                            rows, E, K, scores);
 }
 
+void launch_router_scores(const void *x, bool x_f32, const void *w, bool w_f32, uint32_t rows, uint32_t E,
+                          uint32_t K, float *scores, hipStream_t stream)
+{
+    if (x_f32)
+        launch_scores_x<float>((const float *)x, w, w_f32, rows, E, K, scores, stream);
+    else
+        launch_scores_x<uint16_t>((const uint16_t *)x, w, w_f32, rows, E, K, scores, stream);
+}
+
+void launch_router_select(const float *scores, const float *bias, uint32_t rows, uint32_t E, uint32_t *selected,
+                          float *weights, uint32_t *tie_rows, uint32_t *flags, hipStream_t stream)
+{
+#define PW_SELECT(NC)                                                                                         \
+    hipLaunchKernelGGL(router_select_kernel<NC>, dim3(rows), dim3(64), 0, stream, scores, bias, rows, E, selected, \
+                       weights, tie_rows, flags)
+    if (E <= 64) PW_SELECT(1);
+    else if (E <= 128) PW_SELECT(2);
+    else if (E <= 256) PW_SELECT(4);
+    else if (E <= 512) PW_SELECT(8);
+    else PW_SELECT(16);
+#undef PW_SELECT
+}
+
 void launch_router(const void *x, bool x_f32, const void *w, bool w_f32, const float *bias, uint32_t rows,
                    uint32_t E, uint32_t K, float *scores, uint32_t *selected, float *weights, uint32_t *tie_rows,
                    uint32_t *flags, hipStream_t stream)
 {
     const int t = timer_begin(K_ROUTER, stream);
-    if (x_f32)
-        launch_scores_x<float>((const float *)x, w, w_f32, rows, E, K, scores, stream);
-    else
-        launch_scores_x<uint16_t>((const uint16_t *)x, w, w_f32, rows, E, K, scores, stream);
-    hipLaunchKernelGGL(router_select_kernel, dim3(rows), dim3(64), (size_t)E * (sizeof(TopkEntry) + 3 * sizeof(float)),
-                       stream, scores, bias, rows, E, selected, weights, tie_rows, flags);
+    launch_router_scores(x, x_f32, w, w_f32, rows, E, K, scores, stream);
+    launch_router_select(scores, bias, rows, E, selected, weights, tie_rows, flags, stream);
     timer_end(t, stream);
 }
 

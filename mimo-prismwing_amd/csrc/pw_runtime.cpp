@@ -35,7 +35,7 @@ namespace {
 
 const char *const kKernelNames[pw::K_COUNT] = {
     "linear_a", "linear_b", "quant", "moe_schedule", "moe_gateup", "moe_swiglu", "moe_down",
-    "moe_combine", "prefill_gateup", "prefill_down", "router", "bf16_linear"};
+    "moe_combine", "prefill_gateup", "prefill_down", "router", "bf16_linear", "route_schedule"};
 
 thread_local std::string g_error;
 
@@ -1344,6 +1344,52 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
     PW_TRY(ensure_moe(rt, rows, bank->n_experts, bank->hidden, bank->intermediate));
     launch_routed_layer(rt->mb, bank, mode, x, x_dtype == PW_DTYPE_F32, rows, route_ids, route_weights,
                         std::min<uint32_t>(bank->n_experts, rows * 8), output, out_dtype, rt->d_flags, s);
+    PW_HIP(hipGetLastError());
+    return PW_OK;
+}
+
+int pw_moe_layer_routed_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,
+                               uint32_t x_dtype, uint32_t rows, const void *router_weight, uint32_t w_dtype,
+                               const float *bias, uint32_t *route_ids, float *route_weights, void *output,
+                               uint32_t out_dtype, void *stream)
+{
+    if (!rt || !bank || !x || !router_weight || !bias || !route_ids || !route_weights || !output)
+        return fail(PW_ERR_ARGUMENT, "null argument");
+    if (mode > PW_MODE_B || x_dtype > PW_DTYPE_BF16 || w_dtype > PW_DTYPE_BF16 || out_dtype > PW_DTYPE_F32_RAW)
+        return fail(PW_ERR_ARGUMENT, "unknown mode or dtype");
+    if (rows < 1 || rows > 32)
+        return fail(PW_ERR_ARGUMENT, "device MoE row count must be between one and 32");
+    const uint32_t E = bank->n_experts, H = bank->hidden, I = bank->intermediate;
+    if (E <= 8 || E > 1024 || H % 8 || H > 65536)
+        return fail(PW_ERR_ARGUMENT, "the router needs 9..1024 experts and a hidden size that is a multiple of 8 "
+                                     "(at most 65536)");
+    if (((uintptr_t)x | (uintptr_t)router_weight | (uintptr_t)route_ids | (uintptr_t)route_weights) & 15)
+        return fail(PW_ERR_ARGUMENT, "activations, router weights and route buffers must be 16-byte aligned");
+    PW_HIP(set_device(rt));
+    TimerScope timer_scope(rt);
+    hipStream_t s = stream ? (hipStream_t)stream : rt->stream;
+    StreamOrder order(rt, s);
+    PW_HIP(order.err);
+    PW_TRY(ensure_moe(rt, rows, E, H, I));
+    PW_HIP(rt->router_scores.ensure((size_t)rows * E * 4));
+    float *scores = (float *)rt->router_scores.p;
+    const bool x_f32 = x_dtype == PW_DTYPE_F32;
+    const uint32_t max_active = std::min<uint32_t>(E, rows * 8);
+    const int t = pw::timer_begin(pw::K_ROUTER, s);
+    pw::launch_router_scores(x, x_f32, router_weight, w_dtype == PW_DTYPE_F32, rows, E, H, scores, s);
+    pw::timer_end(t, s);
+    const bool direct = mode == PW_MODE_A && rows == 1 && pw::moe_a_one_token_direct(H, I);
+    if (!direct && pw::launch_route_schedule(scores, bias, bank->table, rows, E, max_active, route_ids, route_weights,
+                                             nullptr, rt->mb, rt->d_flags, s)) {
+        pw::launch_moe_layer(mode, bank->table, rt->mb, x, x_f32, rows, max_active, rows, H, I,
+                             out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
+                             out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr, out_dtype == PW_DTYPE_F32_RAW,
+                             rt->d_flags, s);
+    } else {
+        pw::launch_router_select(scores, bias, rows, E, route_ids, route_weights, nullptr, rt->d_flags, s);
+        launch_routed_layer(rt->mb, bank, mode, x, x_f32, rows, route_ids, route_weights, max_active, output,
+                            out_dtype, rt->d_flags, s);
+    }
     PW_HIP(hipGetLastError());
     return PW_OK;
 }

@@ -217,37 +217,41 @@ PW_HD void nth_element_libcxx(T *first, T *nth, T *last)
 // Outcome of one routed row.
 enum RouteStatus : int { ROUTE_OK = 0, ROUTE_NONFINITE = 1, ROUTE_TOPK = 2, ROUTE_WEIGHTS = 3 };
 
-// The end of one row after the top-k partition: scratch[0..8) holds the selected (corrected, id)
-// entries in partition order and `rejected` is the largest corrected value of the rest. Checks the
-// boundary (equality counts as a tie) and writes selected[8], weights[8].
-PW_HD int noaux_finish_row(const float *scores, const TopkEntry *scratch, float rejected, uint32_t *selected,
-                           float *weights, bool *tie)
+// The end of one row after the top-k partition: sel8[0..8) holds the selected (corrected, id)
+// entries in partition order, chosen[k] the uncorrected score of sel8[k]'s expert, and `rejected`
+// is the largest corrected value of the rest. Checks the boundary (equality counts as a tie) and
+// writes selected[8], weights[8].
+PW_HD int noaux_finish_row8(const TopkEntry *sel8, const float *chosen, float rejected, uint32_t *selected,
+                            float *weights, bool *tie)
 {
     constexpr uint32_t K = 8;
     uint32_t sel[K];
+#pragma unroll
     for (uint32_t k = 0; k < K; ++k) {
-        sel[k] = (uint32_t)scratch[k].i;
+        sel[k] = (uint32_t)sel8[k].i;
+#pragma unroll
         for (uint32_t j = 0; j < k; ++j)
             if (sel[j] == sel[k])
                 return ROUTE_TOPK;
     }
-    float boundary = scratch[0].v;
+    float boundary = sel8[0].v;
+#pragma unroll
     for (uint32_t k = 1; k < K; ++k)
-        boundary = scratch[k].v < boundary ? scratch[k].v : boundary;
+        boundary = sel8[k].v < boundary ? sel8[k].v : boundary;
     if (!finite_f32_bits(boundary) || boundary < rejected)
         return ROUTE_TOPK;
     *tie = boundary == rejected;
-    float c[K];
-    for (uint32_t k = 0; k < K; ++k)
-        c[k] = scores[sel[k]];
-    const float lanes[4] = {c[0] + c[4], c[1] + c[5], c[2] + c[6], c[3] + c[7]};
+    const float lanes[4] = {chosen[0] + chosen[4], chosen[1] + chosen[5], chosen[2] + chosen[6],
+                            chosen[3] + chosen[7]};
     float sum = 0.0f;
+#pragma unroll
     for (uint32_t l = 0; l < 4; ++l)
         sum = sum + lanes[l];
     const float denominator = sum + 1.0e-20f;
     float wsum = 0.0f;
+#pragma unroll
     for (uint32_t k = 0; k < K; ++k) {
-        const float w = scores[sel[k]] / denominator;
+        const float w = chosen[k] / denominator;
         if (!finite_f32_bits(w) || w < 0.0f)
             return ROUTE_WEIGHTS;
         weights[k] = w;
@@ -258,6 +262,16 @@ PW_HD int noaux_finish_row(const float *scores, const TopkEntry *scratch, float 
     if ((dev < 0.0f ? -dev : dev) > 1.0e-6f)
         return ROUTE_WEIGHTS;
     return ROUTE_OK;
+}
+
+// The same from the full scores row and the partitioned entries.
+PW_HD int noaux_finish_row(const float *scores, const TopkEntry *scratch, float rejected, uint32_t *selected,
+                           float *weights, bool *tie)
+{
+    float chosen[8];
+    for (uint32_t k = 0; k < 8; ++k)
+        chosen[k] = scores[scratch[k].i];
+    return noaux_finish_row8(scratch, chosen, rejected, selected, weights, tie);
 }
 
 // One row of pytorch_noaux_routes: scores [experts] (sigmoid outputs), bias [experts] ->

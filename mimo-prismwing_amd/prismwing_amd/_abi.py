@@ -108,6 +108,7 @@ SIGNATURES = {
     "pw_expert_bank_shape": (_i, [_vp, _u32p, _u32p, _u32p]),
     "pw_moe_layer_device": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
     "pw_moe_layer_device_noalloc": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
+    "pw_moe_layer_routed_device": (_i, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp]),
     "pw_expert_forward_device": (_i, [_vp, _vp, _u32, _u32, _vp, _u32, _u32, _vp, _u32, _vp]),
     "pw_moe_prefill_device": (_i, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp, _u32, _vp]),
     "pw_moe_schedule_device": (_i, [_vp, _vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _vp]),

@@ -348,6 +348,15 @@ class WideMoeRuntime:
                                         _ptr(route_ids), _ptr(route_weights), _ptr(out), out_dtype,
                                         stream or 0))
 
+    def moe_layer_routed_device(self, bank: ExpertBank, x, rows: int, router_weight, bias, route_ids, route_weights,
+                                out, mode: int = MODE_A, x_dtype: int = DTYPE_BF16, w_dtype: int = DTYPE_BF16,
+                                out_dtype: int = DTYPE_BF16, stream: Optional[int] = None):
+        """route_mlp over the bank's experts, then the routed layer on those routes (one call); the
+        routes are also written to route_ids / route_weights [rows x 8]."""
+        check(lib().pw_moe_layer_routed_device(self.handle, bank.handle, mode, _ptr(x), x_dtype, rows,
+                                               _ptr(router_weight), w_dtype, _ptr(bias), _ptr(route_ids),
+                                               _ptr(route_weights), _ptr(out), out_dtype, stream or 0))
+
     def moe_layer_device_noalloc(self, bank: ExpertBank, x, rows: int, route_ids, route_weights, out,
                                  mode: int = MODE_A, x_dtype: int = DTYPE_BF16, out_dtype: int = DTYPE_BF16,
                                  stream: Optional[int] = None):

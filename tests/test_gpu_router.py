@@ -219,3 +219,89 @@ def test_device_route_weights_known_answer(rt):
         assert ids[r].tolist() == row["selected"]
         assert scores[r][ids[r]].view(np.uint32).tolist() == row["score_bits"]
         assert wts[r].view(np.uint32).tolist() == row["weight_bits"]
+
+
+@pytest.fixture(scope="module")
+def router_full_bank(rt):
+    return WL.synth_bank(rt, n_experts=256, seed=WL.SEED_BASE + 2)
+
+
+def _routed_vs_two_calls(rt, torch, bank, x, rw, bias, mode, out_dtype=P.DTYPE_F32_RAW, w_f32=False):
+    """(routes and output of pw_moe_layer_routed_device, the same of pw_route_device then
+    pw_moe_layer_device, the device flags)."""
+    rows, hidden = x.shape
+    experts = rw.shape[0]
+    xt = _bf16_dev(torch, x)
+    wt = torch.from_numpy(rw.astype(np.float32)).cuda() if w_f32 else _bf16_dev(torch, rw)
+    bt = torch.from_numpy(bias.astype(np.float32)).cuda()
+    odt = torch.float32 if out_dtype != P.DTYPE_BF16 else torch.int16
+    stream = torch.cuda.current_stream().cuda_stream
+    res = []
+    for fused in (True, False):
+        ids = torch.full((rows, 8), -1, dtype=torch.int32, device="cuda")
+        wts = torch.full((rows, 8), 7.0, dtype=torch.float32, device="cuda")
+        out = torch.full((rows, hidden), 7, dtype=odt, device="cuda")
+        wd = P.DTYPE_F32 if w_f32 else P.DTYPE_BF16
+        if fused:
+            rt.moe_layer_routed_device(bank.bank, xt, rows, wt, bt, ids, wts, out, mode=mode, w_dtype=wd,
+                                       out_dtype=out_dtype, stream=stream)
+        else:
+            rt.route_device(xt, rows, hidden, wt, experts, bt, ids, wts, w_dtype=wd, stream=stream)
+            rt.moe_layer_device(bank.bank, xt, rows, ids, wts, out, mode=mode, out_dtype=out_dtype, stream=stream)
+        torch.cuda.synchronize()
+        res.append((ids.cpu().numpy().astype(np.uint32), wts.cpu().numpy(), out.cpu().numpy()))
+    return res[0], res[1], rt.take_flags()
+
+
+@pytest.mark.parametrize("rows,mode", [(1, 0), (1, 1), (5, 0), (8, 0), (8, 1), (9, 0), (32, 1)])
+def test_routed_layer_equals_router_then_layer(rt, router_full_bank, rows, mode):
+    """pw_moe_layer_routed_device on the 256-expert bank at hidden 4096: the routes it writes equal
+    the oracle's and pw_route_device's bit for bit, and its output equals pw_route_device followed by
+    pw_moe_layer_device byte for byte -- the one-token mode A path (selection, then the schedule-free
+    layer), the one-launch selection and schedule (2..8 rows), and the separate selection (9, 32)."""
+    import torch
+    x = WL.activations(rows, WL.SEED_BASE + 80 + rows)
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=rows == 5)
+    (fi, fw, fo), (ti, tw, to), flags = _routed_vs_two_calls(rt, torch, router_full_bank, x, rw, bias, mode)
+    assert flags == 0
+    _, _, ref_sel, ref_w, _ = O.route(x, rw, bias)
+    assert np.array_equal(fi, ref_sel) and np.array_equal(fi, ti)
+    assert np.array_equal(fw.view(np.uint32), ref_w.view(np.uint32)) and np.array_equal(fw.view(np.uint32),
+                                                                                          tw.view(np.uint32))
+    assert np.array_equal(fo.view(np.uint32), to.view(np.uint32))
+    assert np.all(np.isfinite(fo)) and np.any(fo)
+
+
+@pytest.mark.parametrize("experts", [16, 100, 300])
+def test_routed_layer_expert_counts(rt, experts):
+    """Banks of 16, 100 (the one-launch selection with one and two 64-expert registers per lane) and
+    300 experts (above the one-launch bound: the separate selection kernel), hidden 256: the same
+    routes and bytes as the two calls, f32 router weights, modes A and B, bf16 output."""
+    import torch
+    bank = WL.synth_bank(rt, n_experts=experts, hidden=256, inter=128, seed=WL.SEED_BASE + 85 + experts)
+    rng = np.random.default_rng(experts)
+    for rows, mode in ((3, 0), (8, 1), (1, 1)):
+        x = WL.activations(rows, WL.SEED_BASE + 86 + rows, hidden=256)
+        rw = (rng.standard_normal((experts, 256)) * 0.05).astype(np.float32)
+        bias = rng.uniform(-0.01, 0.01, experts).astype(np.float32)
+        (fi, fw, fo), (ti, tw, to), flags = _routed_vs_two_calls(rt, torch, bank, x, rw, bias, mode,
+                                                                 out_dtype=P.DTYPE_BF16, w_f32=True)
+        assert flags == 0
+        assert np.array_equal(fi, ti) and np.array_equal(fw.view(np.uint32), tw.view(np.uint32))
+        assert np.array_equal(fo, to)
+        _, _, ref_sel, ref_w, _ = O.route(x, rw, bias)
+        assert np.array_equal(fi, ref_sel)
+
+
+def test_routed_layer_rejects_a_failed_row(rt, router_full_bank):
+    """A NaN bias fails every row's routing: FLAG_ROUTE, ids E, zero weights, and the layer rejects the
+    batch (FLAG_SCHEDULE) and writes zeros, on the one-launch path and the one-token path."""
+    import torch
+    rw, bias = WL.router_inputs(WL.SEED_BASE + 3)
+    bias = bias.copy()
+    bias[3] = np.nan
+    for rows, mode in ((8, 0), (1, 0), (12, 1)):
+        x = WL.activations(rows, WL.SEED_BASE + 90 + rows)
+        (fi, fw, fo), _, flags = _routed_vs_two_calls(rt, torch, router_full_bank, x, rw, bias, mode)
+        assert flags & P.FLAG_ROUTE and flags & P.FLAG_SCHEDULE
+        assert (fi == 256).all() and not np.any(fw) and not np.any(fo.view(np.uint32))
