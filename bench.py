@@ -300,7 +300,14 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
             rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1), "spread_us": sp}
         out[f"bf16_o_proj_w{width}"] = rec
     del bprojs, wb
-    # dense layer-0 FP8 MLP: gate/up [16384 x 4096], down [4096 x 16384] as one-expert banks, 3 copies
+    out.update(dense_mlp_legs(torch, rt, P, WL, (P.MODE_A, P.MODE_B), calls))
+    return out
+
+
+def dense_mlp_legs(torch, rt, P, WL, modes, calls=200, widths=(1, 8)):
+    """The dense layer-0 FP8 MLP (gate/up [16384 x 4096], down [4096 x 16384]) as one-expert banks,
+    three copies, through pw_expert_forward_device in each of `modes`, bf16 in and out."""
+    out = {}
     dh, di, copies = 4096, 16384, 3
     keep, banks = [], []
     for c in range(copies):
@@ -316,8 +323,9 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
         banks.append(rt.expert_bank([projs[0]], [projs[1]], [projs[2]]))
         keep.append(projs)
     weight_bytes = 3 * dh * di + 3 * (dh // 128) * (di // 128) * 4
-    for mode, tag in ((P.MODE_A, "a"), (P.MODE_B, "b")):
-        for width in (1, 8):
+    for mode in modes:
+        tag = "a" if mode == P.MODE_A else "b"
+        for width in widths:
             x = _bf16_x(torch, WL, width, dh, WL.SEED_BASE + 720 + width)
             y = torch.empty((width, dh), dtype=torch.int16, device="cuda")
             alg = weight_bytes + width * dh * 2 * 2
@@ -537,6 +545,9 @@ def main():
                     help="routing of the headline decode leg and of --prefill-only (zipf: for profiling)")
     ap.add_argument("--small-calls-only", action="store_true",
                     help="run only configs 0, 1 and 3 and the one-token layer and print their line (for profiling)")
+    ap.add_argument("--mode-b-only", action="store_true",
+                    help="run only the mode-B decode layer (width 8, with per-kernel times) and the dense MLP "
+                         "in mode B, and print their line (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a plain 1 GiB device copy (reference kernel for HBM byte counters)")
     args = ap.parse_args()
@@ -588,6 +599,21 @@ def main():
         res = {"w1_layer_us": round(ms1 * 1000, 2), **projection_legs(torch, rt, bank, P, WL, small_only=True)}
         print(json.dumps({"workload": "small calls: configs 0, 1, 3 and the one-token routed layer, mode A", **res}),
               flush=True)
+        rt.close()
+        return
+    if args.mode_b_only:
+        bb = build_batches(P, WL, args.batches, 8, zipf=False)
+        bd = upload(torch, WL, bb)
+        bms, bspread = time_layer(torch, rt, bank, P, bd, 8, args.steps, args.warmup, P.MODE_B)
+        kt = kernel_times(torch, rt, bank, P, bd, 8, max(20, args.steps // 4), P.MODE_B)
+        b1 = upload(torch, WL, build_batches(P, WL, args.batches, 1, zipf=False))
+        ms1, spread1 = time_layer(torch, rt, bank, P, b1, 1, args.steps, args.warmup, P.MODE_B)
+        res = {"mode_b_w8": {"layer_us": round(bms * 1000, 2), "spread_us": bspread,
+                             "kernels_us": {k: round(v["avg_us"], 2) for k, v in kt.items()}},
+               "mode_b_w1": {"layer_us": round(ms1 * 1000, 2), "spread_us": spread1},
+               **dense_mlp_legs(torch, rt, P, WL, (P.MODE_B,), calls=args.steps)}
+        print(json.dumps({"workload": "mode-B decode layer (widths 8 and 1) and dense MLP, 256 experts, "
+                                      "hidden 4096", **res}), flush=True)
         rt.close()
         return
     rows = 8

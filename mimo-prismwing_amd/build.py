@@ -17,7 +17,7 @@ LIB = os.path.join(OUT_DIR, "libpwfp8.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["pw_linear.hip", "pw_bf16.hip", "pw_moe.hip", "pw_moe_a.hip", "pw_prefill.hip", "pw_router.hip",
+SOURCES = ["pw_linear.hip", "pw_bf16.hip", "pw_moe.hip", "pw_moe_a.hip", "pw_moe_b.hip", "pw_prefill.hip", "pw_router.hip",
            "pw_synth.hip", "pw_checkpoint.cpp",
            "pw_runtime.cpp"]
 

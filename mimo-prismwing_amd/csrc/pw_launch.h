@@ -150,6 +150,33 @@ bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_activ
 void launch_moe_a_swiglu(const float *partial, uint32_t ks, uint32_t P, uint32_t I, uint16_t *hidden_planes,
                          uint32_t *flags, hipStream_t stream);
 
+// Mode B whole-K projections of routed experts (pw_moe_b.hip): e4m3 activation codes with per
+// (row, 128-column) scales against the block-FP8 weights. Gate/up reads token rows ae.tok[t] of
+// the codes and writes the bf16-staged SwiGLU to hidden [slots][R]; down reads slot rows
+// ae.off + t and writes each expert output rounded to bf16 at its slot row.
+struct MoeBArgs {
+    const ActiveExpert *active;  // schedule entries (unused when single)
+    const uint8_t *codes;        // activation codes [rows][K]
+    const float *scales;         // activation scales [rows][K/128]
+    uint32_t K, R, rows, cap;    // columns, weight rows, activation rows, routed rows per expert at most
+    uint32_t single;             // 1: one expert, entry `one` (no schedule)
+    ActiveExpert one;
+    float *out;                  // gate/up: hidden; down: expert outputs (single: the output rows)
+    uint16_t *out_bf16;          // down, single: bf16 output rows (or null)
+    uint32_t KS;                 // down: K shares (set by the launcher)
+    float *partial;              // down with KS > 1: share sums [KS][rows][R]
+    uint32_t *flags;
+};
+// Whether both launches below take hidden H, intermediate I and `cap` rows per expert: K a
+// multiple of 1024 with K/1024 a power of two (gate/up: up to 4; down: up to 16, more than 4
+// only for a lone expert), R a multiple of 16, at most 16 rows per expert whose codes fit LDS.
+bool moe_b_fused_shapes(uint32_t H, uint32_t I, uint32_t cap, bool single);
+bool launch_moe_b_gateup_fused(const MoeBArgs &args, uint32_t max_active, hipStream_t stream);
+// Returns the K shares it launched with (0: nothing launched). One share: the rounded expert outputs
+// are in args.out / args.out_bf16. KS > 1 (a lone expert): the share sums are in args.partial,
+// args.rows * R floats apart, for the output rounding to add in share order.
+uint32_t launch_moe_b_down_fused(const MoeBArgs &args, uint32_t max_active, hipStream_t stream);
+
 // The runtime points this at its timer for the duration of one ABI call (calls on a runtime are
 // serialised by the caller, and each thread has its own pointer).
 extern thread_local KernelTimer *tl_timer;
@@ -202,11 +229,13 @@ struct QuantJob {
 };
 // Returns true when the batch took the long-batch schedule, which also writes the prefill's
 // m-tile table when given tiles and quantises `quant` when given (in the same launch as its plan);
-// false: the caller launches both itself.
+// false: the caller launches both itself. With `quantised` non-null, a decode batch's one-wave
+// schedule also quantises `quant` (in other workgroups of its launch); *quantised tells whether
+// `quant` was done by either path.
 bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
                          uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
                          uint32_t *flags, hipStream_t stream, const PfTileTable *tiles = nullptr,
-                         const QuantJob *quant = nullptr);
+                         const QuantJob *quant = nullptr, bool *quantised = nullptr);
 // expert_offsets [E + 1]: expert e's placement slots are [off[e], off[e + 1]) (after a schedule).
 void launch_expert_offsets(const MoeBuffers &mb, uint32_t E, uint32_t *expert_offsets, hipStream_t stream);
 // One token's routes for a mode A layer launched without a schedule (moe_a_one_token_direct).
@@ -220,7 +249,7 @@ struct OneTokenRoutes {
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                       bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
-                      hipStream_t stream, const OneTokenRoutes *routes = nullptr);
+                      hipStream_t stream, const OneTokenRoutes *routes = nullptr, bool x_quantised = false);
 
 // Device router (pw_router.hip): x [rows][K] (f32 or bf16) and router weights [E][K] (f32 or bf16)
 // -> scores [rows][E], selected / weights [rows][8]; tie_rows (optional) counts boundary ties.

@@ -715,11 +715,23 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
     uint32_t rows, uint32_t E, uint32_t max_active, MoePlan *plan, uint32_t *__restrict__ active_expert,
     uint32_t *__restrict__ active_offset, ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos,
     float *__restrict__ placement_w, uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces,
-    uint32_t max_pieces, uint32_t *flags)
+    uint32_t max_pieces, uint32_t *flags, const QuantJob qj)
 {
     extern __shared__ u32x4 lds_bank[];  // the bank's ExpertPtrs table, E x 48 bytes
     __shared__ SchedWaveLds sl;
     const int lane = threadIdx.x;
+    if (blockIdx.x > 0) {
+        // workgroups 1.. quantise the activation rows of qj (four 128-column groups each) while
+        // workgroup 0 schedules
+        const uint32_t group = (blockIdx.x - 1) * 4 + ((uint32_t)lane >> 4);
+        if (group < qj.rows * (qj.K >> 7)) {
+            if (qj.f32)
+                quant_group128_team<float>((const float *)qj.x, group, lane & 15, qj.codes, qj.scales, flags);
+            else
+                quant_group128_team<uint16_t>((const uint16_t *)qj.x, group, lane & 15, qj.codes, qj.scales, flags);
+        }
+        return;
+    }
     const uint32_t P = rows * 8;
     // the routes and the whole pointer table go out together (one memory round trip in all)
     uint32_t id = 0;
@@ -1180,9 +1192,12 @@ __global__ __launch_bounds__(256) void round_output_kernel(const float *__restri
 // ------------------------------------------------------------------------------- launchers
 bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const float *weights,
                          uint32_t rows, uint32_t E, uint32_t max_active, const MoeBuffers &mb,
-                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles, const QuantJob *quant)
+                         uint32_t *flags, hipStream_t stream, const PfTileTable *tiles, const QuantJob *quant,
+                         bool *quantised)
 {
     bool long_batch = false;
+    if (quantised)
+        *quantised = false;
     const uint32_t words = (rows + 31) >> 5;
     size_t lds = (size_t)(E * words + E) * sizeof(uint32_t);
     const size_t with_prefix_lds = lds + (size_t)E * words * sizeof(uint16_t);
@@ -1198,9 +1213,14 @@ bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
         if (table > 32768)
             (void)hipFuncSetAttribute((const void *)moe_schedule_wave_kernel,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)table);
-        hipLaunchKernelGGL(moe_schedule_wave_kernel, dim3(1), dim3(64), table, stream, bank, ids, weights, rows, E,
-                           max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active, mb.placement_pos,
-                           mb.placement_w, mb.row_slots, mb.pieces, rows * 8, flags);
+        // with `quant` and somewhere to report it, the activation rows are quantised in the same launch
+        const QuantJob qj = quant && quantised ? *quant : QuantJob{};
+        const uint32_t quant_wgs = (qj.rows * (qj.K >> 7) + 3) / 4;
+        hipLaunchKernelGGL(moe_schedule_wave_kernel, dim3(1 + quant_wgs), dim3(64), table, stream, bank, ids, weights,
+                           rows, E, max_active, mb.plan, mb.active_expert, mb.active_offset, mb.active,
+                           mb.placement_pos, mb.placement_w, mb.row_slots, mb.pieces, rows * 8, flags, qj);
+        if (quant_wgs)
+            *quantised = true;
     }
     else if (rows <= SCHED_WG_MAX_ROWS)
         hipLaunchKernelGGL(moe_schedule_kernel, dim3(1), dim3(1024), lds, stream, bank, ids, weights, rows,
@@ -1219,6 +1239,8 @@ bool launch_moe_schedule(const ExpertPtrs *bank, const uint32_t *ids, const floa
                            max_active, ss, mb.plan, mb.active_expert, mb.active_offset, mb.active,
                            mb.placement_pos, mb.placement_w, mb.row_slots, flags, tt, qj);
         long_batch = true;
+        if (quantised && quant)
+            *quantised = true;
         hipLaunchKernelGGL(moe_sched_place_kernel, dim3(nwg), dim3(64), 0, stream, ids, weights, rows, E, max_active,
                            ss, mb.plan, mb.active, mb.placement_pos, mb.placement_w, mb.row_slots);
     }
@@ -1322,6 +1344,66 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     return ExpertOut{mb.partial, dp.ks, (size_t)placements * H};
 }
 
+// Mode B gate/up, hidden re-quantisation and down as whole-K workgroups (pw_moe_b.hip), after the
+// activations were quantised into mb.xq / mb.xs: from the schedule's entries, or for the one expert
+// `one` on token rows 0..rows-1. The down writes each expert output rounded to bf16 into y (a lone
+// expert: the output rows, y_bf16 too). False, with nothing launched, when the shapes do not fit.
+static bool launch_b_fused(const ExpertPtrs *bank, const MoeBuffers &mb, const ActiveExpert *one, uint32_t rows,
+                           uint32_t placements,
+                           uint32_t max_active, uint32_t max_count, uint32_t H, uint32_t I, float *y,
+                           uint16_t *y_bf16, uint32_t *flags, hipStream_t stream)
+{
+    if (!moe_b_fused_shapes(H, I, max_count, one != nullptr))  // both launches take the shapes, or neither runs
+        return false;
+    MoeBArgs ga{};
+    ga.active = mb.active;
+    ga.codes = mb.xq;
+    ga.scales = mb.xs;
+    ga.K = H;
+    ga.R = I;
+    ga.rows = rows;
+    ga.cap = max_count;
+    if (one) {
+        ga.single = 1;
+        ga.one = *one;
+    }
+    ga.out = mb.hidden;
+    ga.flags = flags;
+    MoeBArgs da = ga;
+    da.codes = mb.hq;
+    da.scales = mb.hs;
+    da.K = I;
+    da.R = H;
+    da.rows = placements;
+    da.out = y;
+    da.out_bf16 = y_bf16;
+    da.partial = mb.y;  // a lone expert's share sums: [KS][rows][H] within y's [8 rows][H]
+    int t = timer_begin(K_MOE_GATEUP, stream);
+    (void)launch_moe_b_gateup_fused(ga, max_active, stream);
+    timer_end(t, stream);
+    // re-quantise the bf16-staged hidden activations per (placement, 128 group)
+    launch_quant_group128(mb.hidden, true, placements, I, mb.hq, mb.hs, flags, stream);
+    t = timer_begin(K_MOE_DOWN, stream);
+    // a lone expert: whole-K down workgroups that write the output rows; routed experts: the
+    // split-K down (16 rows per workgroup, four waves of four blocks each), which measured faster
+    // there than whole-K workgroups of 16 rows (81 against 98 us at width 8)
+    uint32_t ks = 1;
+    if (one)
+        ks = launch_moe_b_down_fused(da, max_active, stream);
+    else
+        hipLaunchKernelGGL((moe_b_down_kernel<4, 1>), dim3(max_active * (H >> 4)), dim3(256), 0, stream, bank, mb.plan,
+                           mb.active_expert, mb.active_offset, mb.hq, mb.hs, H, I, mb.y, flags);
+    timer_end(t, stream);
+    if (ks > 1) {
+        // the share sums added in share order and rounded (mode B's output is the rounded expert
+        // output, also as F32_RAW)
+        const uint32_t n = rows * H;
+        hipLaunchKernelGGL(round_output_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, mb.y, ks, (size_t)n, n,
+                           y, y_bf16, 0u, flags);
+    }
+    return true;
+}
+
 template <int KS, int NT>
 static void launch_b_moe(const ExpertPtrs *bank, const MoeBuffers &mb, uint32_t rows, uint32_t placements,
                          uint32_t max_active, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream)
@@ -1343,13 +1425,18 @@ static void launch_b_moe(const ExpertPtrs *bank, const MoeBuffers &mb, uint32_t 
 static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                                 bool x_f32, uint32_t rows, uint32_t placements, uint32_t max_active,
                                 uint32_t max_count, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream,
-                                const DirectOut *direct = nullptr, const OneTokenRoutes *routes = nullptr)
+                                const DirectOut *direct = nullptr, const OneTokenRoutes *routes = nullptr,
+                                bool x_quantised = false)
 {
     const bool wide = max_count > 16;
     if (mode == 0)
         return launch_a_moe(mb, x, x_f32, rows, placements, max_active, max_count, H, I, flags, stream, nullptr,
                             direct, bank, routes);
-    launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
+    if (!x_quantised)
+        launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
+    if (!wide && launch_b_fused(bank, mb, nullptr, rows, placements, max_active, max_count, H, I, mb.y, nullptr, flags,
+                                stream))
+        return ExpertOut{mb.y, 1, 0};
     if (wide) launch_b_moe<4, 2>(bank, mb, rows, placements, max_active, H, I, flags, stream);
     else launch_b_moe<4, 1>(bank, mb, rows, placements, max_active, H, I, flags, stream);
     return ExpertOut{mb.y, 1, 0};
@@ -1358,12 +1445,12 @@ static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const Moe
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                       bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
-                      hipStream_t stream, const OneTokenRoutes *routes)
+                      hipStream_t stream, const OneTokenRoutes *routes, bool x_quantised)
 {
     const DirectOut direct{out_f32, out_bf16, raw};
     const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, routes ? 8 : max_active,
                                         routes ? 1 : max_count, H, I, flags, stream, rows == 1 ? &direct : nullptr,
-                                        routes);
+                                        routes, x_quantised);
     if (!eo.y)
         return;  // the one-token down wrote the combined output
     const uint32_t n4 = rows * (H >> 2);
@@ -1400,6 +1487,19 @@ void launch_expert_forward(uint32_t mode, const ExpertPtrs *bank, const ExpertPt
         if (!eo.y)
             return;  // the down projection wrote the output
     } else {
+        // mode B: the whole-K kernels take the expert's entry by value and the down writes the
+        // output rows (the expert output rounded to bf16, which is also the F32_RAW result)
+        if (rows <= 16) {
+            ActiveExpert one{};
+            one.ep = ep;
+            one.off = 0;
+            one.cnt = rows;
+            for (uint32_t k = 0; k < 16; ++k)
+                one.tok[k] = (uint16_t)k;
+            launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
+            if (launch_b_fused(bank, mb, &one, rows, rows, 1, rows, H, I, out_f32, out_bf16, flags, stream))
+                return;
+        }
         hipLaunchKernelGGL(moe_single_plan_kernel, dim3(1), dim3(256), 0, stream, bank, expert, rows, mb.plan,
                            mb.active_expert, mb.active_offset, mb.active, mb.placement_pos, mb.placement_w);
         eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows, 1, rows, H, I, flags, stream);

@@ -1180,12 +1180,15 @@ int pw_moe_execute(pw_runtime *rt, uint32_t mode, uint32_t fused_gate_up, const 
                           hipMemcpyHostToDevice, rt->stream));
     PW_TRY(ensure_moe(rt, rows, n_experts, H, I));
     PW_HIP(rt->out.ensure(n_in * 4));
+    const pw::QuantJob qj{rt->in.p, x_f32 ? 1u : 0u, rows, H, rt->mb.xq, rt->mb.xs};
+    bool quantised = false;
     pw::launch_moe_schedule((const ExpertPtrs *)rt->bank_table.p, (const uint32_t *)rt->route_ids.p,
                             (const float *)rt->route_w.p, rows, n_experts,
-                            std::min<uint32_t>(n_experts, rows * 8), rt->mb, rt->d_flags, rt->stream);
+                            std::min<uint32_t>(n_experts, rows * 8), rt->mb, rt->d_flags, rt->stream, nullptr,
+                            mode == PW_MODE_B ? &qj : nullptr, mode == PW_MODE_B ? &quantised : nullptr);
     pw::launch_moe_layer(mode, (const ExpertPtrs *)rt->bank_table.p, rt->mb, rt->in.p, x_f32, rows,
                          std::min<uint32_t>(n_experts, rows * 8), max_count, H, I,
-                         (float *)rt->out.p, nullptr, false, rt->d_flags, rt->stream);
+                         (float *)rt->out.p, nullptr, false, rt->d_flags, rt->stream, nullptr, quantised);
     PW_HIP(hipGetLastError());
     PW_HIP(hipMemcpyAsync(output, rt->out.p, n_in * 4, hipMemcpyDeviceToHost, rt->stream));
     uint32_t flags = 0;
@@ -1317,9 +1320,13 @@ static void launch_routed_layer(const MoeBuffers &mb, const pw_expert_bank *bank
                              flags, s, &routes);
         return;
     }
-    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, max_active, mb, flags, s);
+    // mode B: a decode batch's schedule launch also quantises the activations
+    const pw::QuantJob qj{x, x_f32 ? 1u : 0u, rows, H, mb.xq, mb.xs};
+    bool quantised = false;
+    pw::launch_moe_schedule(bank->table, route_ids, route_weights, rows, E, max_active, mb, flags, s, nullptr,
+                            mode == PW_MODE_B ? &qj : nullptr, mode == PW_MODE_B ? &quantised : nullptr);
     pw::launch_moe_layer(mode, bank->table, mb, x, x_f32, rows, max_active, rows, H, I, out_f32, out_bf16, raw, flags,
-                         s);
+                         s, nullptr, quantised);
 }
 
 int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,

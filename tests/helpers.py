@@ -125,12 +125,29 @@ def _unit_codes(rng, shape, p_zero):
     return c
 
 
+def _lowbits_chunk(t: np.ndarray) -> np.ndarray:
+    b = np.abs(t).view(np.uint64)
+    e = (b >> np.uint64(52)).astype(np.int64)                    # biased exponent (0: subnormal or zero)
+    mant = b & np.uint64((1 << 52) - 1)
+    mant = np.where(e > 0, mant | np.uint64(1 << 52), mant)      # with the implicit bit of normal values
+    lb = (mant & (~mant + np.uint64(1))).astype(np.float64)      # its lowest set bit, a power of two < 2^53
+    k = (lb.view(np.uint64) >> np.uint64(52)).astype(np.int64) - 1023 + np.maximum(e, 1) - 1075
+    normal = ((np.clip(k, -1022, 1023) + 1023).astype(np.uint64) << np.uint64(52)).view(np.float64)
+    out = np.where(k >= -1022, normal, np.ldexp(1.0, np.maximum(k, -1074)))
+    return np.where(b == 0, 0.0, out)
+
+
 def _lowbits(t: np.ndarray) -> np.ndarray:
-    """The lowest set bit (a power of two) of each dyadic value of t, exact in f64; 0 where t == 0."""
-    t = np.abs(np.asarray(t, np.float64))
-    m, e = np.frexp(t)
-    mant = (m * 2.0 ** 53).astype(np.int64)
-    return np.where(t == 0, 0.0, np.ldexp((mant & -mant).astype(np.float64), e - 53))
+    """The lowest set bit (a power of two) of each dyadic value of t, exact in f64; 0 where t == 0.
+    From the f64 bit fields (lowest set bit of the significand, shifted by the exponent), in chunks
+    of 2^20 values so the temporaries stay small."""
+    t = np.asarray(t, np.float64)
+    flat = np.ascontiguousarray(t).reshape(-1)
+    out = np.empty_like(flat)
+    step = 1 << 20
+    for i in range(0, flat.size, step):
+        out[i:i + step] = _lowbits_chunk(flat[i:i + step])
+    return out.reshape(t.shape)
 
 
 def exact_in_f32(x: np.ndarray, w: np.ndarray) -> bool:
@@ -189,7 +206,7 @@ def peak_offset(e, j):
     return (41 * e + 67 * j + 5) % 128
 
 
-def closed_form_mode_b(seed, rows, n_experts, hidden=256, inter=256, top_k=8, check=False):
+def closed_form_mode_b(seed, rows, n_experts, hidden=256, inter=256, top_k=8, check=False, down_block_step=1):
     """A routed layer whose mode-B result is fixed bit for bit, whatever the summation order.
 
     Every activation group holds +-448 (so its dynamic scale is exactly 1 and the codes are the
@@ -205,13 +222,15 @@ def closed_form_mode_b(seed, rows, n_experts, hidden=256, inter=256, top_k=8, ch
     differently could round them the other way). Returns experts {id: (gw, gs, uw, us, dw, ds)},
     x [rows, hidden] f32, selected [rows, top_k], weights [rows, top_k]. With check, asserts that
     every projection sum of the routed placements is exact in f32 and inside the FP8 MFMA's window
-    (a CPU test runs the checks for the seeds and sizes the GPU tests use)."""
+    (a CPU test runs the checks for the seeds and sizes the GPU tests use). down_block_step: the
+    down weights hold their one code per block only in every down_block_step-th 128-column block
+    (zeros elsewhere), so that a wide intermediate keeps its down sums exact in f32."""
     rng = np.random.default_rng(seed)
     experts = {}
     for e in range(n_experts):
         gw, uw = _unit_codes(rng, (inter, hidden), 0.3), _unit_codes(rng, (inter, hidden), 0.3)
         dw = np.zeros((hidden, inter), np.uint8)
-        for b in range(inter // 128):
+        for b in range(0, inter // 128, down_block_step):
             c = 128 * b + rng.integers(1, 128, hidden)
             dw[np.arange(hidden), c] = _unit_codes(rng, hidden, 0.0)
         for w in (gw, uw):

@@ -347,6 +347,66 @@ def test_closed_form_mode_b_expert_forward_bit_exact(rt, closed_form, rows):
     _same_bits(out.cpu().numpy(), want)
 
 
+def _expert_forward(rt, bank, e, x, out_dtype):
+    torch = _torch()
+    rows = x.shape[0]
+    xt = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    out = torch.empty((rows, x.shape[1]), dtype=torch.int16 if out_dtype == P.DTYPE_BF16 else torch.float32,
+                      device="cuda")
+    rt.expert_forward_device(bank, e, xt, rows, out, mode=P.MODE_B, x_dtype=P.DTYPE_F32, out_dtype=out_dtype,
+                             stream=_stream())
+    torch.cuda.synchronize()
+    assert rt.take_flags() == 0
+    o = out.cpu().numpy()
+    return (o.view(np.uint16).astype(np.uint32) << 16).view(np.float32) if out_dtype == P.DTYPE_BF16 else o
+
+
+@pytest.mark.parametrize("rows", [1, 8, 16, 17])
+def test_closed_form_mode_b_expert_forward_production_bit_exact(rt, closed_form_production, rows):
+    """The one-expert forward in mode B at the production expert shape (hidden 4096, intermediate
+    2048): up to 16 rows run as whole-K workgroups (gate/up of 8 + 8 stacked rows, the down writing
+    the output rows), 17 rows take the split kernels. Bit for bit the oracle's layer, f32 (also as
+    F32_RAW, which in mode B is the rounded expert output) and bf16."""
+    experts, x, _, _, _, bank = closed_form_production
+    e = 5
+    xr = x[:rows]
+    want = O.moe_layer("b", xr, experts, 8, np.full((rows, 1), e, np.uint32), np.ones((rows, 1), np.float32))
+    for dt in (P.DTYPE_F32, P.DTYPE_F32_RAW, P.DTYPE_BF16):
+        _same_bits(_expert_forward(rt, bank, e, xr, dt), want)
+
+
+@pytest.mark.parametrize("rows", [1, 16, 17])
+def test_closed_form_mode_b_device_layer_production_rows_bit_exact(rt, closed_form_production, rows):
+    """The mode-B decode layer at the production expert shape with one row (one-row experts: 8 + 8
+    stacked gate/up rows per workgroup), sixteen rows (sixteen rows per expert in LDS) and seventeen
+    (the split kernels), top-8 of 8 experts; bit for bit the oracle's layer."""
+    experts, x, sel, w, _, bank = closed_form_production
+    x, sel, w = x[:rows], sel[:rows], w[:rows]
+    want, want_raw = O.moe_layer("b", x, experts, 8, sel, w, raw=True)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_F32_RAW), want_raw)
+    _same_bits(_device_layer(rt, bank, x, sel, w, P.DTYPE_BF16), want)
+
+
+@pytest.fixture(scope="module")
+def closed_form_dense(rt):
+    experts, x, sel, w = closed_form_mode_b(0x50570600, 8, 1, hidden=1024, inter=16384, top_k=1, down_block_step=8)
+    projs, bank = _bank_from(rt, experts, 1)
+    return experts, x, projs, bank
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_closed_form_mode_b_dense_mlp_bit_exact(rt, closed_form_dense, rows):
+    """The dense layer-0 MLP's intermediate 16384 as a one-expert bank in mode B (hidden 1024 keeps
+    the fixture small): the down's K of 16384 runs as four K shares whose sums are added in share
+    order by the output rounding (the down weights hold codes in every eighth 128-column block, four
+    blocks per share, which keeps every sum exact). Bit for bit the oracle's layer, f32 and bf16."""
+    experts, x, _, bank = closed_form_dense
+    xr = x[:rows]
+    want = O.moe_layer("b", xr, experts, 1, np.zeros((rows, 1), np.uint32), np.ones((rows, 1), np.float32))
+    for dt in (P.DTYPE_F32, P.DTYPE_BF16):
+        _same_bits(_expert_forward(rt, bank, 0, xr, dt), want)
+
+
 # ------------------------------------------------------------------ layer vs separate calls
 @pytest.mark.parametrize("rows", [1, 5, 8])
 def test_mode_b_layer_equals_unfused_calls(rt, rows):

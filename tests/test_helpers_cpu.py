@@ -82,3 +82,12 @@ def test_closed_form_production_shape_meets_its_preconditions():
     experts, x, sel, w = closed_form_mode_b(0x50570500, 24, 8, hidden=4096, inter=2048, check=True)
     out = O.moe_layer("b", x[:1], experts, 8, sel[:1], w[:1])
     assert np.all(np.isfinite(out)) and np.any(out)
+
+
+def test_closed_form_dense_intermediate_meets_its_preconditions():
+    """The intermediate-16384 closed form of the dense-MLP test (hidden 1024, one expert, down codes
+    in every eighth 128-column block) at the GPU test's seed and size."""
+    experts, x, sel, w = closed_form_mode_b(0x50570600, 8, 1, hidden=1024, inter=16384, top_k=1, check=True,
+                                            down_block_step=8)
+    out = O.moe_layer("b", x[:1], experts, 1, sel[:1], np.ones((1, 1), np.float32))
+    assert np.all(np.isfinite(out)) and np.any(out)
