@@ -150,7 +150,7 @@ int pw_runtime_take_flags(pw_runtime *rt, uint32_t *flags);
  * command buffer, src/staged_metal_expert.rs:1763-1771): when enabled, every timed launch records
  * a start and a stop event on the stream it runs on, up to max_launches (0 disables). Kernel
  * names: linear_a, linear_b, quant, moe_schedule, moe_gateup, moe_swiglu, moe_down, moe_combine,
- * prefill_gateup, prefill_down, router, bf16_linear, route_schedule (the route selection and schedule
+ * prefill_gateup, prefill_down, router, bf16_linear, route_schedule (the expert-set and schedule
  * launch of pw_moe_layer_routed_device). */
 int pw_runtime_enable_timing(pw_runtime *rt, uint32_t max_launches);
 /* Synchronise the device; report the recorded launches of `kernel` and their summed duration. */
@@ -296,8 +296,10 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
  * (as pw_moe_layer_device), the composition routed_mlp_traced (src/text_endpoint.rs:5290-5381) makes.
  * The routes are also written to route_ids / route_weights [rows x 8] (16-byte aligned), the
  * reference's RoutingTrace. For decode batches of up to 8 rows over banks of up to 256 experts the
- * route selection and the layer's schedule run in one launch. The same routes and the same output
- * bytes as pw_route_device then pw_moe_layer_device. A row whose routing fails raises
+ * layer's schedule is built from each row's expert set (found without the top-k partition where the
+ * row's top-8 boundary is not tied), and the routes' order and weights (the partition) run in extra
+ * workgroups of the gate/up launch, beside the expert weight stream. The same routes and the same
+ * output bytes as pw_route_device then pw_moe_layer_device. A row whose routing fails raises
  * PW_FLAG_ROUTE, and the batch is rejected like invalid routes (PW_FLAG_SCHEDULE, zero output).
  * rows 1..32; hidden a multiple of 8; x and router_weight 16-byte aligned. Asynchronous on stream. */
 int pw_moe_layer_routed_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,

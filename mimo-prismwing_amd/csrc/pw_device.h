@@ -247,14 +247,23 @@ struct DeviceWave {
         return lane() == l ? v : old;
     }
     __device__ __forceinline__ float shift_up1(float v) const { return __shfl_up(v, 1, 64); }
+    // the maximum of v over the wave (finite or infinite values; every lane active): within each
+    // 16-lane row by DPP swaps (quads, half-row and row mirrors), then the four rows' maxima read
+    // out as scalars
+    template <int CTRL>
+    __device__ __forceinline__ static float dpp(float v)
+    {
+        return __builtin_bit_cast(float,
+                                  __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+    }
+    __device__ __forceinline__ static float fmax2(float a, float b) { return b > a ? b : a; }
     __device__ __forceinline__ float max_all(float v) const
     {
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float o = __shfl_xor(v, off, 64);
-            v = o > v ? o : v;
-        }
-        return v;
+        v = fmax2(v, dpp<0xb1>(v));   // quad_perm [1, 0, 3, 2]
+        v = fmax2(v, dpp<0x4e>(v));   // quad_perm [2, 3, 0, 1]
+        v = fmax2(v, dpp<0x141>(v));  // row_half_mirror
+        v = fmax2(v, dpp<0x140>(v));  // row_mirror
+        return fmax2(fmax2(readlane(v, 0u), readlane(v, 16u)), fmax2(readlane(v, 32u), readlane(v, 48u)));
     }
     __device__ __forceinline__ float shfl(float v, uint32_t src) const { return __shfl(v, (int)src, 64); }
     __device__ __forceinline__ void lds_sync() const { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }

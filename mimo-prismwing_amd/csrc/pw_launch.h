@@ -75,6 +75,25 @@ struct MoeBuffers {
     uint32_t experts;
 };
 
+// The route weights of a batch scheduled from its expert sets alone (launch_route_set_schedule):
+// per row, select_route_row gives the routes in the reference's order and their weights, which go
+// to the route outputs and to the placements (route_weights_row, pw_route_job.h). The decode
+// layer's gate/up launch runs it in eight extra workgroups while its other workgroups stream the
+// experts' weights; rows = 0: no job.
+struct RouteJob {
+    const float *scores, *bias;  // router scores [rows][E], bias [E]
+    uint32_t rows, E;
+    const uint32_t *set_ids;     // [rows][8] the schedule's expert sets
+    uint32_t *route_ids;         // [rows][8] out
+    float *route_w;              // [rows][8] out
+    uint32_t *tie_rows;          // optional tie count
+    MoePlan *plan;
+    const uint32_t *row_slots;   // null: no schedule (a one-token direct layer)
+    float *placement_w;          // the schedule's placement weights, or [rows][8] in set order
+    uint32_t *flags;
+};
+constexpr uint32_t ROUTE_JOB_WGS = 8;  // workgroups a gate/up launch adds for a job (one per row)
+
 // Arguments of the split-K mode A expert projection (pw_moe_a.hip).
 struct SplitArgs {
     const ActiveExpert *active;
@@ -93,6 +112,7 @@ struct SplitArgs {
     const uint32_t *route_ids;
     const float *route_w;
     uint32_t E;
+    RouteJob job;  // fused gate/up only: run in ROUTE_JOB_WGS extra workgroups
 };
 
 // Where a launch left the per-placement expert outputs: `ks` split-K partial sums of [P][H] f32,
@@ -166,6 +186,7 @@ struct MoeBArgs {
     uint32_t KS;                 // down: K shares (set by the launcher)
     float *partial;              // down with KS > 1: share sums [KS][rows][R]
     uint32_t *flags;
+    RouteJob job;                // gate/up only: run in ROUTE_JOB_WGS extra workgroups
 };
 // Whether both launches below take hidden H, intermediate I and `cap` rows per expert: K a
 // multiple of 1024 with K/1024 a power of two (gate/up: up to 4; down: up to 16, more than 4
@@ -249,7 +270,8 @@ struct OneTokenRoutes {
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                       bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
-                      hipStream_t stream, const OneTokenRoutes *routes = nullptr, bool x_quantised = false);
+                      hipStream_t stream, const OneTokenRoutes *routes = nullptr, bool x_quantised = false,
+                      const RouteJob *job = nullptr);
 
 // Device router (pw_router.hip): x [rows][K] (f32 or bf16) and router weights [E][K] (f32 or bf16)
 // -> scores [rows][E], selected / weights [rows][8]; tie_rows (optional) counts boundary ties.
@@ -261,13 +283,19 @@ void launch_router_scores(const void *x, bool x_f32, const void *w, bool w_f32, 
                           uint32_t K, float *scores, hipStream_t stream);
 void launch_router_select(const float *scores, const float *bias, uint32_t rows, uint32_t E, uint32_t *selected,
                           float *weights, uint32_t *tie_rows, uint32_t *flags, hipStream_t stream);
-// A decode batch's routes and its schedule in one launch (pw_moe.hip): each row's top-8 and weights
-// from its router scores (the router's selection, written to selected / weights) and the one-wave
-// schedule built from them, as launch_moe_schedule would build it. False (nothing launched) when
-// the batch does not fit it (rows <= 8, 9 <= E <= 256).
-bool launch_route_schedule(const float *scores, const float *bias, const ExpertPtrs *bank, uint32_t rows, uint32_t E,
-                           uint32_t max_active, uint32_t *selected, float *weights, uint32_t *tie_rows,
-                           const MoeBuffers &mb, uint32_t *flags, hipStream_t stream);
+// A decode batch's expert sets (fast_top8_set, select_route_row where a boundary is tied) and its
+// schedule in one launch, with zero placement weights and the sets in set_ids [rows][8]; with
+// `quant`, the launch also quantises those activation rows. False (nothing launched) outside
+// rows 1..8, 9..256 experts, 64 routed experts. A RouteJob then writes the routes, their weights
+// and the placement weights before the combine: inside the gate/up launch (launch_moe_layer's job)
+// or as launch_route_weights.
+bool launch_route_set_schedule(const float *scores, const float *bias, const ExpertPtrs *bank, uint32_t rows,
+                               uint32_t E, uint32_t max_active, uint32_t *set_ids, const MoeBuffers &mb,
+                               uint32_t *flags, hipStream_t stream, const QuantJob *quant = nullptr);
+void launch_route_weights(const RouteJob &job, hipStream_t stream);
+// The expert sets alone (row_expert_set: one wave per row) into set_ids [rows][8], rows <= 8.
+void launch_route_set(const float *scores, const float *bias, uint32_t rows, uint32_t E, uint32_t *set_ids,
+                      hipStream_t stream);
 
 // Routed-MoE prefill (mode B grouped block-FP8 GEMM, pw_prefill.hip) after launch_moe_schedule.
 struct PrefillBuffers {

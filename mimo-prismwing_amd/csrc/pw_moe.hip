@@ -17,6 +17,7 @@
 // token's eight placements in ascending expert id (the reference's order) before the bf16 round.
 #include "pw_device.h"
 #include "pw_launch.h"
+#include "pw_route_job.h"
 #include "pw_select_wave.h"
 
 namespace pw {
@@ -749,82 +750,131 @@ __global__ __launch_bounds__(64) void moe_schedule_wave_kernel(
                        placement_pos, placement_w, row_slots, pieces, max_pieces, flags);
 }
 
-// A decode batch's routes and its schedule in one launch. Wave r < rows selects row r's routes
-// from its router scores (select_route_row: pytorch_noaux_routes, src/text_endpoint.rs:4394-4473,
-// as the router's own selection kernel runs it) and writes them out; meanwhile all waves copy the
-// bank's pointer table into LDS; wave 0 then builds the schedule from the routes in LDS
-// (schedule_wave_body), the schedule moe_schedule_wave_kernel builds from the same routes. A row
-// whose routing fails raises FLAG_ROUTE and gets ids E, which the schedule rejects.
+// Row p's eight experts into ids[0..7] by one wave: fast_top8_set (ascending ids), or where that
+// cannot decide, select_route_row (its order; ids E when the row's routing fails).
 template <int NC>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void route_schedule_kernel(
+__device__ __forceinline__ void row_expert_set(const float *scores_row, const float *bias, uint32_t E, TopkEntry *pairs,
+                                               uint32_t *ids)
+{
+    DeviceWave w;
+    if (fast_top8_set<NC>(w, scores_row, bias, E, ids))
+        return;
+    uint32_t sel_k;
+    float w_k;
+    bool tie = false;
+    const int st = select_route_row<NC>(w, scores_row, bias, E, pairs, sel_k, w_k, &tie);
+    if (w.lane() < 8)
+        ids[w.lane()] = st == ROUTE_OK ? sel_k : E;
+}
+
+// The expert sets alone (a one-token batch's direct layer reads them as its routes): one wave per
+// row, row_expert_set into set_ids [rows][8].
+template <int NC>
+__global__ __launch_bounds__(64) void route_set_kernel(const float *__restrict__ scores, const float *__restrict__ bias,
+                                                       uint32_t rows, uint32_t E, uint32_t *__restrict__ set_ids)
+{
+    __shared__ TopkEntry pairs[64 * NC];
+    if (blockIdx.x < rows)
+        row_expert_set<NC>(scores + (size_t)blockIdx.x * E, bias, E, pairs, set_ids + (size_t)blockIdx.x * 8);
+}
+
+void launch_route_set(const float *scores, const float *bias, uint32_t rows, uint32_t E, uint32_t *set_ids,
+                      hipStream_t stream)
+{
+    if (E <= 64) hipLaunchKernelGGL(route_set_kernel<1>, dim3(rows), dim3(64), 0, stream, scores, bias, rows, E, set_ids);
+    else if (E <= 128) hipLaunchKernelGGL(route_set_kernel<2>, dim3(rows), dim3(64), 0, stream, scores, bias, rows, E, set_ids);
+    else if (E <= 256) hipLaunchKernelGGL(route_set_kernel<4>, dim3(rows), dim3(64), 0, stream, scores, bias, rows, E, set_ids);
+    else if (E <= 512) hipLaunchKernelGGL(route_set_kernel<8>, dim3(rows), dim3(64), 0, stream, scores, bias, rows, E, set_ids);
+    else hipLaunchKernelGGL(route_set_kernel<16>, dim3(rows), dim3(64), 0, stream, scores, bias, rows, E, set_ids);
+}
+
+// A decode batch's expert sets and its schedule in one launch, the route weights left to
+// route_weights_kernel. Wave r < rows finds row r's eight experts with fast_top8_set (the set
+// select_route_row selects, found without the partition when the row's boundary is not tied);
+// a row with a tied boundary or a non-finite value runs select_route_row itself (failing rows get
+// ids E, which the schedule rejects). Wave 0 then builds the schedule from the sets with weights
+// 0 in place of the route weights, and writes the sets to set_ids for the weights kernel's
+// check. With a QuantJob, workgroups 1.. quantise its activation rows (mode B) meanwhile.
+template <int NC>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(1, 2))) void route_set_schedule_kernel(
     const float *__restrict__ scores, const float *__restrict__ bias, const ExpertPtrs *__restrict__ bank,
-    uint32_t rows, uint32_t E, uint32_t max_active, uint32_t *__restrict__ route_ids, float *__restrict__ route_w,
-    uint32_t *tie_rows, MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
-    ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
-    uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces, uint32_t max_pieces, uint32_t *flags)
+    uint32_t rows, uint32_t E, uint32_t max_active, uint32_t *__restrict__ set_ids, MoePlan *plan,
+    uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset, ActiveExpert *__restrict__ active,
+    uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w, uint32_t *__restrict__ row_slots,
+    ActiveExpert *__restrict__ pieces, uint32_t max_pieces, uint32_t *flags, const QuantJob qj)
 {
     extern __shared__ u32x4 lds_bank[];  // the bank's ExpertPtrs table, E x 48 bytes
     __shared__ TopkEntry pairs[8][64 * NC];
     __shared__ uint32_t r_id[64];
-    __shared__ float r_w[64];
     __shared__ SchedWaveLds sl;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (blockIdx.x > 0) {
+        // 32 128-column groups per workgroup (16 lanes each)
+        const uint32_t group = (blockIdx.x - 1) * 32 + (threadIdx.x >> 4);
+        if (group < qj.rows * (qj.K >> 7)) {
+            if (qj.f32)
+                quant_group128_team<float>((const float *)qj.x, group, lane & 15, qj.codes, qj.scales, flags);
+            else
+                quant_group128_team<uint16_t>((const uint16_t *)qj.x, group, lane & 15, qj.codes, qj.scales, flags);
+        }
+        return;
+    }
     const uint32_t units = E * 3;  // 16-byte units of the table
     for (uint32_t u0 = wave * 64; u0 < units; u0 += 512)
         if (u0 + lane < units)
             lds_load16((const u32x4 *)bank + u0 + lane, lds_bank + u0);
-    if (wave < rows) {
-        DeviceWave w;
-        uint32_t sel_k;
-        float w_k;
-        bool tie = false;
-        const int st = select_route_row<NC>(w, scores + (size_t)wave * E, bias, E, pairs[wave], sel_k, w_k, &tie);
-        if (st != ROUTE_OK) {
-            sel_k = E;
-            w_k = 0.0f;
-            tie = false;
-            if (lane == 0)
-                raise_flag(flags, FLAG_ROUTE);
-        }
-        if (lane < 8) {
-            route_ids[(size_t)wave * 8 + lane] = sel_k;
-            route_w[(size_t)wave * 8 + lane] = w_k;
-            r_id[wave * 8 + lane] = sel_k;
-            r_w[wave * 8 + lane] = w_k;
-        }
-        if (lane == 0 && tie && tie_rows)
-            atomicAdd(tie_rows, 1u);
-    }
+    if (wave < rows)
+        row_expert_set<NC>(scores + (size_t)wave * E, bias, E, pairs[wave], r_id + wave * 8);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the table copy has landed in LDS
     __syncthreads();
     if (wave != 0)
         return;
     const uint32_t P = rows * 8;
     const uint32_t id = lane < P ? r_id[lane] : 0u;
-    const float wgt = lane < P ? r_w[lane] : 0.f;
-    schedule_wave_body(id, wgt, rows, E, max_active, lds_bank, sl, plan, active_expert, active_offset, active,
+    if (lane < P)
+        set_ids[lane] = id;
+    schedule_wave_body(id, 0.0f, rows, E, max_active, lds_bank, sl, plan, active_expert, active_offset, active,
                        placement_pos, placement_w, row_slots, pieces, max_pieces, flags);
 }
 
-bool launch_route_schedule(const float *scores, const float *bias, const ExpertPtrs *bank, uint32_t rows, uint32_t E,
-                           uint32_t max_active, uint32_t *selected, float *weights, uint32_t *tie_rows,
-                           const MoeBuffers &mb, uint32_t *flags, hipStream_t stream)
+bool launch_route_set_schedule(const float *scores, const float *bias, const ExpertPtrs *bank, uint32_t rows,
+                               uint32_t E, uint32_t max_active, uint32_t *set_ids, const MoeBuffers &mb,
+                               uint32_t *flags, hipStream_t stream, const QuantJob *quant)
 {
     if (rows < 1 || rows > 8 || E < 9 || E > 256 || max_active > 64)
         return false;
     const size_t table = (size_t)E * sizeof(ExpertPtrs);  // <= 12 KB
+    const QuantJob qj = quant ? *quant : QuantJob{};
+    const uint32_t quant_wgs = (qj.rows * (qj.K >> 7) + 31) / 32;
     const int t = timer_begin(K_ROUTE_SCHEDULE, stream);
-#define PW_RS(NC)                                                                                                  \
-    hipLaunchKernelGGL(route_schedule_kernel<NC>, dim3(1), dim3(512), table, stream, scores, bias, bank, rows, E,  \
-                       max_active, selected, weights, tie_rows, mb.plan, mb.active_expert, mb.active_offset,       \
-                       mb.active, mb.placement_pos, mb.placement_w, mb.row_slots, mb.pieces, rows * 8, flags)
-    if (E <= 64) PW_RS(1);
-    else if (E <= 128) PW_RS(2);
-    else PW_RS(4);
-#undef PW_RS
+#define PW_RSS(NC)                                                                                                 \
+    hipLaunchKernelGGL(route_set_schedule_kernel<NC>, dim3(1 + quant_wgs), dim3(512), table, stream, scores, bias,  \
+                       bank, rows, E, max_active, set_ids, mb.plan, mb.active_expert, mb.active_offset, mb.active,  \
+                       mb.placement_pos, mb.placement_w, mb.row_slots, mb.pieces, rows * 8, flags, qj)
+    if (E <= 64) PW_RSS(1);
+    else if (E <= 128) PW_RSS(2);
+    else PW_RSS(4);
+#undef PW_RSS
     timer_end(t, stream);
     return true;
+}
+
+// The route weights of a batch scheduled by route_set_schedule_kernel as a launch of its own (when
+// the gate/up launch cannot carry them): one wave per row (route_weights_row).
+template <int NC>
+__global__ __launch_bounds__(64) void route_weights_kernel(const RouteJob job)
+{
+    __shared__ TopkEntry lds_pairs[64 * NC];
+    if (blockIdx.x < job.rows)
+        route_weights_row<NC>(job, blockIdx.x, lds_pairs);
+}
+
+void launch_route_weights(const RouteJob &job, hipStream_t stream)
+{
+    if (job.E <= 64) hipLaunchKernelGGL(route_weights_kernel<1>, dim3(job.rows), dim3(64), 0, stream, job);
+    else if (job.E <= 128) hipLaunchKernelGGL(route_weights_kernel<2>, dim3(job.rows), dim3(64), 0, stream, job);
+    else hipLaunchKernelGGL(route_weights_kernel<4>, dim3(job.rows), dim3(64), 0, stream, job);
 }
 
 // --------------------------------------------------------------- shared tile preamble
@@ -1260,7 +1310,8 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
                               uint32_t placements, uint32_t max_active, uint32_t max_count, uint32_t H,
                               uint32_t I, uint32_t *flags, hipStream_t stream, const ActiveExpert *one = nullptr,
                               const DirectOut *direct = nullptr, const ExpertPtrs *bank = nullptr,
-                              const OneTokenRoutes *routes = nullptr)
+                              const OneTokenRoutes *routes = nullptr, const RouteJob *job = nullptr,
+                              bool *job_done = nullptr)
 {
     const int nt = max_count > 16 ? 2 : 1;
     const uint32_t cnt = max_count < 16u * nt ? max_count : 16u * nt;
@@ -1304,6 +1355,8 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
         gp_args.active = mb.pieces;
         gp_args.cap = PIECE_ROWS;
     }
+    if (job)  // the fused gate/up carries the route weights (in extra workgroups)
+        gp_args.job = *job;
     const bool fused = nt == 1 && launch_moe_a_gateup_fused(x_f32 ? 3 : 1, gp_args, pieces && !x_f32 ? placements
                                                             : max_active, mb.hidden_planes, stream);
     if (!fused)
@@ -1313,6 +1366,11 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
         t = timer_begin(K_MOE_SWIGLU, stream);
         launch_moe_a_swiglu(mb.partial, gp.ks, placements, I, mb.hidden_planes, flags, stream);
         timer_end(t, stream);
+    }
+    if (job) {
+        if (!fused)  // the split gate/up cannot carry the route weights: before the down, on their own
+            launch_route_weights(*job, stream);
+        *job_done = true;
     }
 
     SplitArgs da = ga;
@@ -1351,7 +1409,8 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
 static bool launch_b_fused(const ExpertPtrs *bank, const MoeBuffers &mb, const ActiveExpert *one, uint32_t rows,
                            uint32_t placements,
                            uint32_t max_active, uint32_t max_count, uint32_t H, uint32_t I, float *y,
-                           uint16_t *y_bf16, uint32_t *flags, hipStream_t stream)
+                           uint16_t *y_bf16, uint32_t *flags, hipStream_t stream, const RouteJob *job = nullptr,
+                           bool *job_done = nullptr)
 {
     if (!moe_b_fused_shapes(H, I, max_count, one != nullptr))  // both launches take the shapes, or neither runs
         return false;
@@ -1370,6 +1429,10 @@ static bool launch_b_fused(const ExpertPtrs *bank, const MoeBuffers &mb, const A
     ga.out = mb.hidden;
     ga.flags = flags;
     MoeBArgs da = ga;
+    if (job) {  // the gate/up launch carries the route weights (in extra workgroups)
+        ga.job = *job;
+        *job_done = true;
+    }
     da.codes = mb.hq;
     da.scales = mb.hs;
     da.K = I;
@@ -1426,16 +1489,16 @@ static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const Moe
                                 bool x_f32, uint32_t rows, uint32_t placements, uint32_t max_active,
                                 uint32_t max_count, uint32_t H, uint32_t I, uint32_t *flags, hipStream_t stream,
                                 const DirectOut *direct = nullptr, const OneTokenRoutes *routes = nullptr,
-                                bool x_quantised = false)
+                                bool x_quantised = false, const RouteJob *job = nullptr, bool *job_done = nullptr)
 {
     const bool wide = max_count > 16;
     if (mode == 0)
         return launch_a_moe(mb, x, x_f32, rows, placements, max_active, max_count, H, I, flags, stream, nullptr,
-                            direct, bank, routes);
+                            direct, bank, routes, job, job_done);
     if (!x_quantised)
         launch_quant_group128(x, x_f32, rows, H, mb.xq, mb.xs, flags, stream);
     if (!wide && launch_b_fused(bank, mb, nullptr, rows, placements, max_active, max_count, H, I, mb.y, nullptr, flags,
-                                stream))
+                                stream, job, job_done))
         return ExpertOut{mb.y, 1, 0};
     if (wide) launch_b_moe<4, 2>(bank, mb, rows, placements, max_active, H, I, flags, stream);
     else launch_b_moe<4, 1>(bank, mb, rows, placements, max_active, H, I, flags, stream);
@@ -1445,12 +1508,18 @@ static ExpertOut launch_experts(uint32_t mode, const ExpertPtrs *bank, const Moe
 void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &mb, const void *x,
                       bool x_f32, uint32_t rows, uint32_t max_active, uint32_t max_count, uint32_t H,
                       uint32_t I, float *out_f32, uint16_t *out_bf16, bool raw, uint32_t *flags,
-                      hipStream_t stream, const OneTokenRoutes *routes, bool x_quantised)
+                      hipStream_t stream, const OneTokenRoutes *routes, bool x_quantised, const RouteJob *job)
 {
     const DirectOut direct{out_f32, out_bf16, raw};
+    // the route weights (job) must be in place before a kernel reads them: the mode A experts carry
+    // them in their gate/up launch or launch them right after it (before the down, which may combine
+    // as well), the mode B ones in their whole-K gate/up launch, else they run before the combine
+    bool job_done = false;
     const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, routes ? 8 : max_active,
                                         routes ? 1 : max_count, H, I, flags, stream, rows == 1 ? &direct : nullptr,
-                                        routes, x_quantised);
+                                        routes, x_quantised, job, &job_done);
+    if (job && !job_done)  // the gate/up launch did not carry the route weights
+        launch_route_weights(*job, stream);
     if (!eo.y)
         return;  // the one-token down wrote the combined output
     const uint32_t n4 = rows * (H >> 2);

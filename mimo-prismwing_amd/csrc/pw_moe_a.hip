@@ -20,6 +20,7 @@
 // the down projection), the combine (or the single-expert output rounding) for down.
 #include "pw_device.h"
 #include "pw_launch.h"
+#include "pw_route_job.h"
 
 namespace pw {
 
@@ -235,8 +236,11 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     // up to 7% slower for some physical placements of the bank. A lone expert (the one-expert
     // forward, the dense MLP) keeps the strided order, which measured 1 µs faster there. Which
     // workgroup computes which rows does not change any sum.
+    uint32_t bid;
+    if (route_job_prologue(args.job, lds_x, &bid))
+        return;  // one of the route-weights workgroups
     const uint32_t G = args.R / RM;
-    const uint32_t a = blockIdx.x / G, local = blockIdx.x % G;
+    const uint32_t a = bid / G, local = bid % G;
     const uint32_t g = G % 8 == 0 && !args.single ? (local % 8) * (G / 8) + local / 8 : local;
     const ActiveExpert ae = args.single ? args.one : (args.route_ids ? route_entry(args, a) : args.active[a]);
     if (ae.cnt == 0)
@@ -431,7 +435,7 @@ bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_activ
     // a lone expert (the one-expert forward) and one-row experts (a one-token batch) take 8 + 8-row
     // work items: twice the workgroups
     const bool half = args.R % 8 == 0 && (args.single || args.cap == 1);
-    const dim3 grid(max_active * (args.R / (half ? 8 : 16))), block(512);
+    const dim3 grid(max_active * (args.R / (half ? 8 : 16)) + (args.job.rows ? ROUTE_JOB_WGS : 0)), block(512);
 #define PW_FUSED(NS, RM)                                                                                     \
     do {                                                                                                      \
         if (lds > 65536)                                                                                      \

@@ -19,6 +19,7 @@
 //            expert, the output rows themselves.
 #include "pw_device.h"
 #include "pw_launch.h"
+#include "pw_route_job.h"
 
 namespace pw {
 
@@ -96,9 +97,12 @@ __global__ __launch_bounds__(512) void moe_b_gateup_fused_kernel(const MoeBArgs 
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // split index, wave-uniform
     const int q = lane >> 4, r16 = lane & 15;
+    uint32_t bid;
+    if (route_job_prologue(args.job, lds_x, &bid))
+        return;  // one of the route-weights workgroups
     const uint32_t G = args.R / RM;
-    const uint32_t a = blockIdx.x / G;
-    const uint32_t g = xcd_group(blockIdx.x % G, G, args.single);
+    const uint32_t a = bid / G;
+    const uint32_t g = xcd_group(bid % G, G, args.single);
     const ActiveExpert ae = args.single ? args.one : args.active[a];
     if (ae.cnt == 0)
         return;
@@ -388,7 +392,7 @@ bool launch_moe_b_gateup_fused(const MoeBArgs &args, uint32_t max_active, hipStr
     const int bpw = b_bpw(args.K);
     const bool half = args.single || args.cap == 1;
     const size_t lds = b_lds(args.cap, args.K, half ? 1 : 2);
-    const uint32_t grid = max_active * (args.R / (half ? 8 : 16));
+    const uint32_t grid = max_active * (args.R / (half ? 8 : 16)) + (args.job.rows ? ROUTE_JOB_WGS : 0);
 #define PW_GU(B)                                                                                     \
     do {                                                                                             \
         if (half) launch_b(moe_b_gateup_fused_kernel<B, 8>, grid, lds, args, stream);                \

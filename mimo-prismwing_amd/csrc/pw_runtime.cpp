@@ -116,6 +116,7 @@ struct pw_runtime {
     // runtime's own stream (the runtime never touches a caller's stream after the call returns).
     hipStream_t last_stream = nullptr;
     hipEvent_t order_event = nullptr;
+    DevBuf set_ids, set_w;  // the routed layer's expert sets [rows][8] (and their weights, one-token layer)
 };
 
 namespace {
@@ -1386,12 +1387,54 @@ int pw_moe_layer_routed_device(pw_runtime *rt, const pw_expert_bank *bank, uint3
     pw::launch_router_scores(x, x_f32, router_weight, w_dtype == PW_DTYPE_F32, rows, E, H, scores, s);
     pw::timer_end(t, s);
     const bool direct = mode == PW_MODE_A && rows == 1 && pw::moe_a_one_token_direct(H, I);
-    if (!direct && pw::launch_route_schedule(scores, bias, bank->table, rows, E, max_active, route_ids, route_weights,
-                                             nullptr, rt->mb, rt->d_flags, s)) {
+    PW_HIP(rt->set_ids.ensure((size_t)rows * 8 * 4));
+    // mode B: the schedule launch also quantises the activations
+    const pw::QuantJob qj{x, x_f32 ? 1u : 0u, rows, H, rt->mb.xq, rt->mb.xs};
+    if (!direct && pw::launch_route_set_schedule(scores, bias, bank->table, rows, E, max_active,
+                                                 (uint32_t *)rt->set_ids.p, rt->mb, rt->d_flags, s,
+                                                 mode == PW_MODE_B ? &qj : nullptr)) {
+        // the expert sets are scheduled; the routes' order and weights (a serial partition per row)
+        // run in extra workgroups of the gate/up launch while its others stream the experts'
+        // weights (or in a launch of their own before the combine)
+        pw::RouteJob job{};
+        job.scores = scores;
+        job.bias = bias;
+        job.rows = rows;
+        job.E = E;
+        job.set_ids = (const uint32_t *)rt->set_ids.p;
+        job.route_ids = route_ids;
+        job.route_w = route_weights;
+        job.plan = rt->mb.plan;
+        job.row_slots = rt->mb.row_slots;
+        job.placement_w = rt->mb.placement_w;
+        job.flags = rt->d_flags;
         pw::launch_moe_layer(mode, bank->table, rt->mb, x, x_f32, rows, max_active, rows, H, I,
                              out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
                              out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr, out_dtype == PW_DTYPE_F32_RAW,
-                             rt->d_flags, s);
+                             rt->d_flags, s, nullptr, mode == PW_MODE_B, &job);
+    } else if (direct && E <= 256) {
+        // one token: the expert set is the direct layer's routes; the routes' order and weights
+        // (the partition) run in extra workgroups of its gate/up launch and give the weights in the
+        // set's order before its down+combine launch
+        PW_HIP(rt->set_w.ensure(8 * 4));
+        pw::launch_route_set(scores, bias, 1, E, (uint32_t *)rt->set_ids.p, s);
+        pw::RouteJob job{};
+        job.scores = scores;
+        job.bias = bias;
+        job.rows = 1;
+        job.E = E;
+        job.set_ids = (const uint32_t *)rt->set_ids.p;
+        job.route_ids = route_ids;
+        job.route_w = route_weights;
+        job.plan = rt->mb.plan;
+        job.row_slots = nullptr;
+        job.placement_w = (float *)rt->set_w.p;
+        job.flags = rt->d_flags;
+        const pw::OneTokenRoutes routes{(const uint32_t *)rt->set_ids.p, (const float *)rt->set_w.p, E};
+        pw::launch_moe_layer(mode, bank->table, rt->mb, x, x_f32, rows, max_active, rows, H, I,
+                             out_dtype != PW_DTYPE_BF16 ? (float *)output : nullptr,
+                             out_dtype == PW_DTYPE_BF16 ? (uint16_t *)output : nullptr, out_dtype == PW_DTYPE_F32_RAW,
+                             rt->d_flags, s, &routes, false, &job);
     } else {
         pw::launch_router_select(scores, bias, rows, E, route_ids, route_weights, nullptr, rt->d_flags, s);
         launch_routed_layer(rt->mb, bank, mode, x, x_f32, rows, route_ids, route_weights, max_active, output,

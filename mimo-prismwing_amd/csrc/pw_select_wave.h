@@ -494,4 +494,67 @@ PW_WAVE int select_route_row(W &w, const float *scores_row, const float *bias, u
     return ROUTE_OK;
 }
 
+// The set of the eight experts select_route_row selects, without the partition, where the set does
+// not depend on the partition order: every score and bias finite, every corrected score finite,
+// and the eighth largest corrected score strictly above the ninth. nth_element then leaves exactly
+// the eight largest corrected scores in positions 0..7 (equal values above the boundary are all
+// among them, whatever their order), so picking the largest value, all of its copies at once,
+// eight times at most, finds the same set. Writes the ids in ascending order to ids[0..7] and
+// returns true; returns false (nothing written) otherwise: the caller runs select_route_row. The
+// order of the eight ids, and so the weights' denominator, still needs the partition.
+template <int NC, class W>
+PW_WAVE bool fast_top8_set(W &w, const float *scores_row, const float *bias, uint32_t E, uint32_t *ids)
+{
+    float v[NC];
+    bool bad = false;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t e = 64 * c + w.lane();
+        v[c] = -__builtin_inff();
+        if (e < E) {
+            const float sc = scores_row[e], b = bias[e];
+            v[c] = sc + b;
+            bad |= !finite_f32_bits(sc) || !finite_f32_bits(b) || !finite_f32_bits(v[c]);
+        }
+    }
+    if (w.ballot(bad))
+        return false;
+    bool sel[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+        sel[c] = false;
+    uint32_t picked = 0;  // wave-uniform
+    for (int it = 0; it < 8 && picked < 8; ++it) {
+        // the largest value not yet taken (positions past E hold -inf and are never taken: every
+        // corrected score is finite and E > 8)
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            m = !sel[c] && v[c] > m ? v[c] : m;
+        m = w.max_all(m);
+        uint32_t cnt = 0;
+        bool hit[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            hit[c] = !sel[c] && 64 * c + w.lane() < E && v[c] == m;
+            cnt += popc64(w.ballot(hit[c]));
+        }
+        if (picked + cnt > 8)
+            return false;  // copies of the eighth largest value also below the boundary: a tie
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            sel[c] = sel[c] || hit[c];
+        picked += cnt;
+    }
+    uint32_t base = 0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint64_t m = w.ballot(sel[c]);
+        if (sel[c])
+            ids[base + w.below(m)] = 64 * c + w.lane();
+        base += popc64(m);
+    }
+    return true;
+}
+
 }  // namespace pw

@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <barrier>
 #include <random>
 #include <thread>
@@ -148,6 +149,36 @@ int route_wave(const std::vector<float> &scores, const std::vector<float> &bias,
     return status;
 }
 
+// fast_top8_set on the emulated wave: whether it decided the set, and the ids it wrote
+template <int NC>
+bool fast_wave(const std::vector<float> &scores, const std::vector<float> &bias, uint32_t ids[8])
+{
+    const uint32_t E = (uint32_t)scores.size();
+    Shared sh;
+    bool decided = false;
+    std::vector<std::thread> threads;
+    for (uint32_t lane = 0; lane < 64; ++lane)
+        threads.emplace_back([&, lane]() {
+            CpuWave w{lane, &sh};
+            const bool d = pw::fast_top8_set<NC>(w, scores.data(), bias.data(), E, ids);
+            if (lane == 0)
+                decided = d;
+        });
+    for (auto &t : threads)
+        t.join();
+    return decided;
+}
+
+bool fast_any(const std::vector<float> &s, const std::vector<float> &b, uint32_t ids[8])
+{
+    const size_t n = s.size();
+    if (n <= 64) return fast_wave<1>(s, b, ids);
+    if (n <= 128) return fast_wave<2>(s, b, ids);
+    if (n <= 256) return fast_wave<4>(s, b, ids);
+    if (n <= 512) return fast_wave<8>(s, b, ids);
+    return fast_wave<16>(s, b, ids);
+}
+
 int route_any(const std::vector<float> &s, const std::vector<float> &b, uint32_t sel[8], float wt[8], bool *tie)
 {
     const size_t n = s.size();
@@ -231,15 +262,33 @@ int main(int argc, char **argv)
     // whole routed rows against the host routing (noaux_route_row): sigmoid-like scores with a
     // bias, tied scores, and a non-finite bias
     std::uniform_real_distribution<float> unit(0.f, 1.f), small(-0.01f, 0.01f);
+    // trials 0..2 (and their repeats): random scores with a bias, five score levels with a bias, random
+    // scores without one (trial 2: a NaN bias); then the rows the fast set must tell apart: five
+    // levels without a bias (a tied boundary), a pair of equal values inside the top eight, the
+    // top eight all equal with a lower ninth, and the eighth and ninth equal
+    const int trials = quick ? 3 : 12;
     for (uint32_t E : {9u, 100u, 256u, 1000u})
-        for (int t = 0; t < (quick ? 3 : 12); ++t) {
+        for (int t = 0; t < trials + 4; ++t) {
             std::vector<float> sc(E), bi(E);
             for (uint32_t e = 0; e < E; ++e) {
-                sc[e] = t % 3 == 1 ? (float)(e % 5) * 0.125f + 0.25f : unit(rng);
-                bi[e] = t % 3 == 2 ? 0.f : small(rng);
+                sc[e] = t % 3 == 1 || t == trials ? (float)(e % 5) * 0.125f + 0.25f : unit(rng);
+                bi[e] = t % 3 == 2 || t >= trials ? 0.f : small(rng);
             }
             if (t == 2)
                 bi[E / 2] = __builtin_nanf("");
+            if (t > trials) {
+                std::vector<uint32_t> order(E);
+                for (uint32_t e = 0; e < E; ++e)
+                    order[e] = e;
+                std::sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return sc[a] > sc[b]; });
+                if (t == trials + 1)
+                    sc[order[5]] = sc[order[2]];
+                else if (t == trials + 2)
+                    for (int k = 1; k < 8; ++k)
+                        sc[order[k]] = sc[order[0]];
+                else
+                    sc[order[8]] = sc[order[7]];
+            }
             uint32_t ws[8] = {}, hs[8] = {};
             float ww[8] = {}, hw[8] = {};
             bool wtie = false, htie = false;
@@ -256,6 +305,28 @@ int main(int argc, char **argv)
             if (!same) {
                 if (mismatches < 5)
                     printf("route mismatch: E %u trial %d status %d vs %d\n", E, t, got, want);
+                ++mismatches;
+            }
+            // the fast set: decided exactly when every value is finite and the boundary is not tied
+            // (a routed row: the host's status is ROUTE_OK), and then the host's eight ids
+            uint32_t fids[8] = {};
+            const bool decided = fast_any(sc, bi, fids);
+            bool fsame = true;
+            if (want == pw::ROUTE_OK) {
+                fsame = decided == !htie;
+                if (decided) {
+                    uint32_t sorted[8];
+                    memcpy(sorted, hs, sizeof sorted);
+                    std::sort(sorted, sorted + 8);
+                    fsame = fsame && memcmp(sorted, fids, sizeof sorted) == 0;
+                }
+            } else if (want == pw::ROUTE_NONFINITE) {
+                fsame = !decided;
+            }
+            ++rows;
+            if (!fsame) {
+                if (mismatches < 5)
+                    printf("fast set mismatch: E %u trial %d decided %d tie %d\n", E, t, decided, htie);
                 ++mismatches;
             }
         }

@@ -305,3 +305,63 @@ def test_routed_layer_rejects_a_failed_row(rt, router_full_bank):
         (fi, fw, fo), _, flags = _routed_vs_two_calls(rt, torch, router_full_bank, x, rw, bias, mode)
         assert flags & P.FLAG_ROUTE and flags & P.FLAG_SCHEDULE
         assert (fi == 256).all() and not np.any(fw) and not np.any(fo.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_routed_layer_tied_and_untied_rows(rt, mode):
+    """The one-launch schedule finds each row's expert set without the partition when the row's
+    top-8 boundary is untied, and partitions the rows whose boundary is tied (one-hot activations
+    over five logit levels); the route order and weights come from the separate weights launch.
+    Six rows, three of each kind, 64 experts, hidden 256, modes A and B: the same routes, weights and
+    output bytes as pw_route_device then pw_moe_layer_device, the oracle's routes and tie count."""
+    import torch
+    hidden, experts, rows = 256, 64, 6
+    bank = WL.synth_bank(rt, n_experts=experts, hidden=hidden, inter=128, seed=WL.SEED_BASE + 95)
+    rng = np.random.default_rng(95)
+    x = WL.activations(rows, WL.SEED_BASE + 96, hidden=hidden)
+    x[:3] = 0.0
+    x[:3, 0] = 1.0
+    rw = (rng.standard_normal((experts, hidden)) * 0.05).astype(np.float32)
+    levels = np.array([0.5, 0.25, 0.125, 0.0625, -0.5], np.float32)
+    rw[:, 0] = levels[rng.integers(0, levels.size, experts)]
+    bias = np.zeros(experts, np.float32)
+    (fi, fw, fo), (ti, tw, to), flags = _routed_vs_two_calls(rt, torch, bank, x, rw, bias, mode,
+                                                             out_dtype=P.DTYPE_BF16, w_f32=True)
+    assert flags == 0
+    _, _, ref_sel, ref_w, ref_ties = O.route(WL.bf16_round_np(x), rw, bias)
+    assert ref_ties == 3
+    assert np.array_equal(fi, ti) and np.array_equal(fi, ref_sel)
+    assert np.array_equal(fw.view(np.uint32), tw.view(np.uint32))
+    assert np.array_equal(fw.view(np.uint32), ref_w.view(np.uint32))
+    assert np.array_equal(fo, to) and np.any(fo)
+    # one-token batches of a tied and an untied row (mode A: the schedule-free one-token layer)
+    for r in (0, 3):
+        (fi, fw, fo), (ti, tw, to), flags = _routed_vs_two_calls(rt, torch, bank, x[r:r + 1], rw, bias, mode,
+                                                                 out_dtype=P.DTYPE_BF16, w_f32=True)
+        assert flags == 0
+        assert np.array_equal(fi, ti) and np.array_equal(fi, ref_sel[r:r + 1])
+        assert np.array_equal(fw.view(np.uint32), tw.view(np.uint32))
+        assert np.array_equal(fo, to) and np.any(fo)
+
+
+def test_routed_layer_rejects_zero_route_weights(rt):
+    """Logits near -256 make every sigmoid score 0 while the biases (distinct) still rank the experts,
+    so the expert sets are found without a tie, but the weights are 0 / 1e-20 = 0 and fail the
+    reference's sum check: the weights launch must reject the batch it did not schedule itself --
+    FLAG_ROUTE and FLAG_SCHEDULE, ids E, zero weights, zero output, as pw_route_device then
+    pw_moe_layer_device give."""
+    import torch
+    hidden, experts, rows = 256, 64, 2
+    bank = WL.synth_bank(rt, n_experts=experts, hidden=hidden, inter=128, seed=WL.SEED_BASE + 97)
+    v = WL.activations(1, WL.SEED_BASE + 98, hidden=hidden)[0]
+    x = np.stack([v, v])
+    vb = (WL.bf16_bits_np(v).astype(np.uint32) << 16).view(np.float32)
+    assert float(np.dot(vb.astype(np.float64), vb)) > 120.0
+    rw = np.tile(-vb, (experts, 1)).astype(np.float32)
+    bias = np.random.default_rng(97).permutation(experts).astype(np.float32) * np.float32(1e-3)
+    for mode, n in ((0, 2), (1, 2), (0, 1), (1, 1)):
+        (fi, fw, fo), (ti, tw, to), flags = _routed_vs_two_calls(rt, torch, bank, x[:n], rw, bias, mode, w_f32=True)
+        assert flags & P.FLAG_ROUTE and flags & P.FLAG_SCHEDULE
+        assert (fi == experts).all() and (ti == experts).all()
+        assert not np.any(fw) and not np.any(tw)
+        assert not np.any(fo.view(np.uint32)) and not np.any(to.view(np.uint32))
