@@ -190,6 +190,156 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
     }
 }
 
+// Two 16-row tiles per workgroup for the staged form of wider batches (up to 8 activation rows):
+// eight waves split K (BPW = 4 blocks each), every wave loads the weights of both tiles for its
+// split and reads each activation unit from LDS once for both, so a copied activation row feeds
+// twice the weight rows of linear_a_kernel's 16-row workgroups (whose eight-row copies cost L2
+// requests equal to the weights' own) and the grid halves. The split partials meet in LDS (over
+// the stage, after every wave is done with it) and are added in split order 0..7.
+template <int NS>
+__global__ __launch_bounds__(512) void linear_a_pair_kernel(
+    const ProjTile *__restrict__ tiles, uint32_t n_tiles, const uint16_t *__restrict__ x, uint32_t W,
+    uint32_t K, float *__restrict__ y_f32, uint16_t *__restrict__ y_bf16, uint32_t N, uint32_t round_f32)
+{
+    constexpr int KSPLIT = 8, BPW = 4, RT = 2;  // the epilogue's tile selects assume RT = 2
+    const size_t plane = (size_t)W * K;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = lane >> 4, r16 = lane & 15;
+    extern __shared__ uint4 lds_xa[];  // per wave [NS][W][ROW] 16-byte units; then [KSPLIT][RT][64] f32x4
+    constexpr uint32_t UNITS = BPW * 16, ROW = UNITS + 1;
+    uint4 *xs = lds_xa + (size_t)wave * NS * W * ROW;
+    const uint32_t blocks = K >> 7;
+
+    for (uint32_t pr = blockIdx.x; pr * RT < n_tiles; pr += gridDim.x) {
+        ProjTile tile[RT];
+        bool live[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            const uint32_t t = pr * RT + r;
+            live[r] = t < n_tiles;
+            tile[r] = tiles[live[r] ? t : n_tiles - 1];
+        }
+        f32x4 total[RT];
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+            total[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (uint32_t round = 0; round < blocks; round += KSPLIT * BPW) {
+            const uint32_t b0 = round + (uint32_t)wave * BPW;
+            const bool whole = b0 + BPW <= blocks;
+            // this wave's columns of every activation row -> its LDS region (as linear_a_kernel)
+            const uint32_t units = (b0 < blocks ? (blocks - b0 < (uint32_t)BPW ? blocks - b0 : BPW) : 0) * 16;
+            for (uint32_t sp = 0; sp < (uint32_t)NS; ++sp)
+                for (uint32_t t = 0; t < W; ++t)
+                    for (uint32_t u0 = 0; u0 < units; u0 += 64)
+                        if (u0 + (uint32_t)lane < units)
+                            lds_load16(x + sp * plane + (size_t)t * K + ((size_t)b0 << 7) + (u0 + lane) * 8,
+                                       xs + (sp * W + t) * ROW + u0);
+            asm volatile("" ::: "memory");  // the copies stay the oldest memory operations
+            uint4 wv[RT][BPW][2];
+            float sc[RT][BPW];
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                const bool row_ok = live[r] && (uint32_t)r16 < tile[r].valid;
+                const uint8_t *wrow = tile[r].w + (size_t)r16 * K + q * 16;
+#pragma unroll
+                for (int j = 0; j < BPW; ++j) {
+                    const uint32_t b = b0 + j;
+                    wv[r][j][0] = make_uint4(0, 0, 0, 0);
+                    wv[r][j][1] = wv[r][j][0];
+                    sc[r][j] = 0.f;
+                    if (b < blocks) {
+                        if (row_ok) {
+                            wv[r][j][0] = load_global16(wrow + ((size_t)b << 7));
+                            wv[r][j][1] = load_global16(wrow + ((size_t)b << 7) + 64);
+                        }
+                        sc[r][j] = tile[r].s[b];
+                    }
+                }
+            }
+            // every load but this wave's youngest 2 RT BPW weight loads: its copies have landed
+            if (whole)
+                wait_vmcnt<2 * RT * BPW>();
+            else
+                wait_vmcnt<0>();
+#pragma unroll
+            for (int j = 0; j < BPW; ++j) {
+                const uint32_t b = b0 + j;
+                if (b >= blocks)
+                    break;
+                f32x4 acc[RT];
+#pragma unroll
+                for (int r = 0; r < RT; ++r)
+                    acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    bf16x8 a[RT][2];
+#pragma unroll
+                    for (int r = 0; r < RT; ++r) {
+                        a[r][0] = fp8x8_to_bf16x8(wv[r][j][half].x, wv[r][j][half].y);
+                        a[r][1] = fp8x8_to_bf16x8(wv[r][j][half].z, wv[r][j][half].w);
+                    }
+#pragma unroll
+                    for (int sp = 0; sp < NS; ++sp) {
+                        uint4 x0 = make_uint4(0, 0, 0, 0), x1 = x0;
+                        if ((uint32_t)r16 < W) {
+                            const uint4 *xp = xs + (sp * W + r16) * ROW + j * 16 + half * 8 + q * 2;
+                            x0 = xp[0];
+                            x1 = xp[1];
+                        }
+#pragma unroll
+                        for (int r = 0; r < RT; ++r) {
+                            acc[r] = mfma_bf16_16x16x32(a[r][0], bf16x8_from_u4(x0), acc[r]);
+                            acc[r] = mfma_bf16_16x16x32(a[r][1], bf16x8_from_u4(x1), acc[r]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < RT; ++r)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        total[r][i] = __builtin_fmaf(sc[r][j], acc[r][i], total[r][i]);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next copies
+        }
+        // split partials in LDS over the stage (every wave is past its reads), summed in split order
+        __syncthreads();
+        f32x4 *red = (f32x4 *)lds_xa;
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+            red[(wave * RT + r) * 64 + lane] = total[r];
+        __syncthreads();
+        const bool mine = wave == 0 ? live[0] : live[1];  // waves 0 and 1 write tiles 0 and 1
+        if (wave < RT && mine) {
+            f32x4 sum = red[wave * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < KSPLIT; ++w) {
+                const f32x4 o = red[(w * RT + wave) * 64 + lane];
+                sum[0] += o[0];
+                sum[1] += o[1];
+                sum[2] += o[2];
+                sum[3] += o[3];
+            }
+            const ProjTile tl = wave == 0 ? tile[0] : tile[1];
+            if ((uint32_t)r16 < W) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t row = q * 4 + i;
+                    if (row >= tl.valid)
+                        continue;
+                    const size_t at = (size_t)r16 * N + tl.out_row + row;
+                    const float v = sum[i];
+                    if (y_f32)
+                        y_f32[at] = round_f32 ? round_bf16(v) : v;
+                    if (y_bf16)
+                        y_bf16[at] = bf16_bits(v);
+                }
+            }
+        }
+        __syncthreads();  // the partials are read before the next pair's copies overwrite them
+    }
+}
+
 // ------------------------------------------------------------------------------------ mode B
 template <int KSPLIT, int NT, int BPW>
 __global__ __launch_bounds__(64 * KSPLIT) void linear_b_kernel(
@@ -401,6 +551,19 @@ template <int NS>
 static void launch_a_planes(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x, uint32_t W, uint32_t K,
                             float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32, hipStream_t stream)
 {
+    // batches of 4..8 rows over many tiles: two tiles per staged workgroup (linear_a_pair_kernel),
+    // when eight splits of four blocks cover K in whole rounds and the stage fits
+    const size_t pair_lds = staged_lds(NS, 8, 4, W);
+    if (W >= 4 && W <= 8 && n_tiles >= 512 && (K >> 7) % 32 == 0 && pair_lds <= LINEAR_STAGE_LDS &&
+        pair_lds >= (size_t)8 * 2 * 64 * 16) {
+        if (pair_lds > 48 * 1024)
+            (void)hipFuncSetAttribute((const void *)linear_a_pair_kernel<NS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)pair_lds);
+        const uint32_t pairs = (n_tiles + 1) / 2;
+        hipLaunchKernelGGL((linear_a_pair_kernel<NS>), dim3(grid_for(pairs, 65535)), dim3(512), pair_lds, stream, tiles,
+                           n_tiles, x, W, K, y32, y16, N, round_f32);
+        return;
+    }
     const LinearSplit sp = pick_split(K >> 7, W, n_tiles);
 #define PW_A(KS, BPW) launch_a_split<NS, KS, BPW>(tiles, n_tiles, x, W, K, y32, y16, N, round_f32, stream)
 #define PW_A_BPW(KS)                                                                                       \

@@ -221,7 +221,9 @@ __device__ __forceinline__ ActiveExpert route_entry(const SplitArgs &args, uint3
     return ae;
 }
 
-template <int NS, int BPW, int RM>
+// JOB: the launch also carries args.job (the route weights, in its first ROUTE_JOB_WGS workgroups);
+// the launches without one are compiled without that code.
+template <int NS, int BPW, int RM, bool JOB>
 __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs args, uint16_t *__restrict__ hidden)
 {
     constexpr int MATS = RM == 16 ? 2 : 1;  // 16-row MFMA operands per block
@@ -236,9 +238,11 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     // up to 7% slower for some physical placements of the bank. A lone expert (the one-expert
     // forward, the dense MLP) keeps the strided order, which measured 1 µs faster there. Which
     // workgroup computes which rows does not change any sum.
-    uint32_t bid;
-    if (route_job_prologue(args.job, lds_x, &bid))
-        return;  // one of the route-weights workgroups
+    uint32_t bid = blockIdx.x;
+    if constexpr (JOB) {
+        if (route_job_prologue(args.job, lds_x, &bid))
+            return;  // one of the route-weights workgroups
+    }
     const uint32_t G = args.R / RM;
     const uint32_t a = bid / G, local = bid % G;
     const uint32_t g = G % 8 == 0 && !args.single ? (local % 8) * (G / 8) + local / 8 : local;
@@ -436,12 +440,17 @@ bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_activ
     // work items: twice the workgroups
     const bool half = args.R % 8 == 0 && (args.single || args.cap == 1);
     const dim3 grid(max_active * (args.R / (half ? 8 : 16)) + (args.job.rows ? ROUTE_JOB_WGS : 0)), block(512);
-#define PW_FUSED(NS, RM)                                                                                     \
+#define PW_FUSED_J(NS, RM, J)                                                                                \
     do {                                                                                                      \
         if (lds > 65536)                                                                                      \
-            (void)hipFuncSetAttribute((const void *)moe_a_gateup_fused_kernel<NS, 4, RM>,                     \
+            (void)hipFuncSetAttribute((const void *)moe_a_gateup_fused_kernel<NS, 4, RM, J>,                  \
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);                  \
-        hipLaunchKernelGGL((moe_a_gateup_fused_kernel<NS, 4, RM>), grid, block, lds, stream, args, hidden_planes); \
+        hipLaunchKernelGGL((moe_a_gateup_fused_kernel<NS, 4, RM, J>), grid, block, lds, stream, args,         \
+                           hidden_planes);                                                                    \
+    } while (0)
+#define PW_FUSED(NS, RM)                                                                                     \
+    do {                                                                                                      \
+        if (args.job.rows) PW_FUSED_J(NS, RM, true); else PW_FUSED_J(NS, RM, false);                          \
     } while (0)
     if (ns == 3) {
         if (half) PW_FUSED(3, 8); else PW_FUSED(3, 16);
@@ -449,6 +458,7 @@ bool launch_moe_a_gateup_fused(int ns, const SplitArgs &args, uint32_t max_activ
         if (half) PW_FUSED(1, 8); else PW_FUSED(1, 16);
     }
 #undef PW_FUSED
+#undef PW_FUSED_J
     return true;
 }
 

@@ -88,7 +88,8 @@ static size_t b_lds(uint32_t cap, uint32_t K, int mats)
     return stage > red ? stage : red;
 }
 
-template <int BPW, int RM>
+// JOB: the launch also carries args.job (the route weights, in its first ROUTE_JOB_WGS workgroups).
+template <int BPW, int RM, bool JOB>
 __global__ __launch_bounds__(512) void moe_b_gateup_fused_kernel(const MoeBArgs args)
 {
     constexpr int MATS = RM == 16 ? 2 : 1;  // 16-row MFMA operands per block
@@ -97,9 +98,11 @@ __global__ __launch_bounds__(512) void moe_b_gateup_fused_kernel(const MoeBArgs 
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // split index, wave-uniform
     const int q = lane >> 4, r16 = lane & 15;
-    uint32_t bid;
-    if (route_job_prologue(args.job, lds_x, &bid))
-        return;  // one of the route-weights workgroups
+    uint32_t bid = blockIdx.x;
+    if constexpr (JOB) {
+        if (route_job_prologue(args.job, lds_x, &bid))
+            return;  // one of the route-weights workgroups
+    }
     const uint32_t G = args.R / RM;
     const uint32_t a = bid / G;
     const uint32_t g = xcd_group(bid % G, G, args.single);
@@ -393,15 +396,20 @@ bool launch_moe_b_gateup_fused(const MoeBArgs &args, uint32_t max_active, hipStr
     const bool half = args.single || args.cap == 1;
     const size_t lds = b_lds(args.cap, args.K, half ? 1 : 2);
     const uint32_t grid = max_active * (args.R / (half ? 8 : 16)) + (args.job.rows ? ROUTE_JOB_WGS : 0);
+#define PW_GU_J(B, J)                                                                                \
+    do {                                                                                             \
+        if (half) launch_b(moe_b_gateup_fused_kernel<B, 8, J>, grid, lds, args, stream);             \
+        else launch_b(moe_b_gateup_fused_kernel<B, 16, J>, grid, lds, args, stream);                 \
+    } while (0)
 #define PW_GU(B)                                                                                     \
     do {                                                                                             \
-        if (half) launch_b(moe_b_gateup_fused_kernel<B, 8>, grid, lds, args, stream);                \
-        else launch_b(moe_b_gateup_fused_kernel<B, 16>, grid, lds, args, stream);                    \
+        if (args.job.rows) PW_GU_J(B, true); else PW_GU_J(B, false);                                 \
     } while (0)
     if (bpw == 4) PW_GU(4);
     else if (bpw == 2) PW_GU(2);
     else PW_GU(1);
 #undef PW_GU
+#undef PW_GU_J
     return true;
 }
 
