@@ -1,6 +1,8 @@
 """Test helpers: seeded data in the reference's formats and the parity metrics the tests use."""
 from __future__ import annotations
 
+import math
+
 import numpy as np
 
 # e4m3fn magnitudes of codes 0..0x7e (0x7f is NaN), exact in f64
@@ -376,3 +378,35 @@ def route_weight_alternatives(scores_sel: np.ndarray, selected) -> dict:
         "id_order": weights(s, fold(s_id)),
         "no_eps": weights(s, fold(s), eps=False),
     }
+
+
+# ------------------------------------------------------------------ staged SwiGLU known answers
+# (gate bits, up bits) -> output bits of round(round(silu(round(g))) * round(u)). The expected
+# outputs come from the exact silu (every case sits more than 64 f32 ulps from a bf16 rounding
+# boundary, so any faithful f32 evaluation gives these bits). `dropped` is the output with the named
+# rounding taken out; each differs from the expected bits.
+STAGED_CASES = [
+    # the reference's case: gate 1.03125, up 0.71484375 (src/staged_metal_expert.rs:2826-2831)
+    dict(g=0x3F840000, u=0x3F370000, out=0x3F0B0000, dropped={}),
+    # silu rounding: 0.9913 * -1.3032
+    dict(g=0x3F7DC693, u=0xBFA6CDDB, out=0xBF710000, dropped={"silu": 0xBF720000}),
+    # up rounding: 1.0937 * 0.2941
+    dict(g=0x3F8BFEED, u=0x3E969889, out=0x3E780000, dropped={"up": 0x3E770000}),
+    # gate rounding: 0.02443 * -0.2756
+    dict(g=0x3CC81A2C, u=0xBE8D1BD3, out=0xBB5F0000, dropped={"gate": 0xBB600000}),
+    # product exactly halfway between two bf16 values (0xbd968000): ties to the even code
+    dict(g=0xC02E0000, u=0x3EE00000, out=0xBD960000, dropped={"product": 0xBD968000}),
+]
+STAGES = ("gate", "up", "silu", "product")
+
+
+def staged_swiglu_independent(g_bits, u_bits, drop=None):
+    """The staged SwiGLU evaluated independently of the oracle, with the stage `drop` left unrounded:
+    bf16 rounding in numpy, silu in f64 (math.exp) rounded once to f32, the product in f32."""
+    def rnd(v, stage):
+        return v if stage == drop else np.float32(bf16_round(np.array([v], np.float32))[0])
+
+    g = rnd(np.float32(np.uint32(g_bits).view(np.float32)), "gate")
+    u = rnd(np.float32(np.uint32(u_bits).view(np.float32)), "up")
+    silu = rnd(np.float32(float(g) / (1.0 + math.exp(-float(g)))), "silu")
+    return int(np.float32(rnd(np.float32(silu * u), "product")).view(np.uint32))

@@ -19,8 +19,8 @@ import pytest
 
 import oracle as O
 import prismwing_amd as P
-from helpers import (_unit_codes, bf16_normal, bf16_round, closed_form_mode_b, decode_table, fp8_weight,
-                     log_uniform_scales, to_bf16_bits)
+from helpers import (STAGED_CASES, STAGES, _unit_codes, bf16_normal, bf16_round, closed_form_mode_b, decode_table,
+                     fp8_weight, log_uniform_scales, staged_swiglu_independent, to_bf16_bits)
 
 pytestmark = pytest.mark.gpu
 
@@ -139,21 +139,23 @@ def test_staged_swiglu_every_bf16_gate(rt):
     assert diff.size == 0, [(float(g[i]), float(inplace[i]), float(want[i])) for i in diff[:8]]
 
 
-# (gate bits, up bits, output bits) of round(round(silu(round(g))) * round(u)); each case flips
-# when one of the four roundings is dropped (the reference's own case first,
-# src/staged_metal_expert.rs:2826-2831)
-STAGED_KNOWN = [(0x3F840000, 0x3F370000, 0x3F0B0000), (0x3F7DC693, 0xBFA6CDDB, 0xBF710000),
-                (0x3F8BFEED, 0x3E969889, 0x3E780000), (0x3CC81A2C, 0xBE8D1BD3, 0xBB5F0000),
-                (0xC02E0000, 0x3EE00000, 0xBD960000)]
-
-
 @pytest.mark.parametrize("form", [0, 1])
 def test_staged_swiglu_known_answers(rt, form):
-    g = _f32_bits([c[0] for c in STAGED_KNOWN])
-    u = _f32_bits([c[1] for c in STAGED_KNOWN])
+    """Both device forms on the staged-SwiGLU known answers (the reference's case first,
+    src/staged_metal_expert.rs:2826-2831): each output equals the independent evaluation
+    (bf16 rounding in numpy, silu in f64, helpers.staged_swiglu_independent) with every rounding in
+    place, and differs from the same evaluation with the case's named rounding taken out, so a
+    device form missing that rounding fails here."""
+    g = _f32_bits([c["g"] for c in STAGED_CASES])
+    u = _f32_bits([c["u"] for c in STAGED_CASES])
     out, flags = _swiglu_device(rt, g, u, form)
     assert flags == 0
-    assert out.view(np.uint32).tolist() == [c[2] for c in STAGED_KNOWN]
+    got = out.view(np.uint32).tolist()
+    for c, bits in zip(STAGED_CASES, got):
+        assert bits == staged_swiglu_independent(c["g"], c["u"]) == c["out"], (hex(c["g"]), hex(bits))
+        for stage in c["dropped"]:
+            assert bits != staged_swiglu_independent(c["g"], c["u"], drop=stage), (hex(c["g"]), stage)
+    assert {st for c in STAGED_CASES for st in c["dropped"]} == set(STAGES)
 
 
 def test_staged_swiglu_flags_nonfinite(rt):

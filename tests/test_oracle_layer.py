@@ -25,7 +25,8 @@ import numpy as np
 import pytest
 
 import oracle as O
-from helpers import bf16_normal, bf16_round, closed_form_mode_b, dequant, fp8_weight, log_uniform_scales
+from helpers import (STAGED_CASES, STAGES, bf16_normal, bf16_round, closed_form_mode_b, dequant, fp8_weight,
+                     log_uniform_scales, staged_swiglu_independent)
 
 
 def _bits(x):
@@ -284,37 +285,6 @@ def test_layer_rejects_non_bijective_routes():
 
 
 # ------------------------------------------------------------------ staged SwiGLU known answers
-# (gate bits, up bits) -> output bits of round(round(silu(round(g))) * round(u)). The expected
-# outputs come from the exact silu (every case sits more than 64 f32 ulps from a bf16 rounding
-# boundary, so any faithful f32 evaluation gives these bits). `dropped` is the output with the named
-# rounding taken out; each differs from the expected bits.
-STAGED_CASES = [
-    # the reference's case: gate 1.03125, up 0.71484375 (src/staged_metal_expert.rs:2826-2831)
-    dict(g=0x3F840000, u=0x3F370000, out=0x3F0B0000, dropped={}),
-    # silu rounding: 0.9913 * -1.3032
-    dict(g=0x3F7DC693, u=0xBFA6CDDB, out=0xBF710000, dropped={"silu": 0xBF720000}),
-    # up rounding: 1.0937 * 0.2941
-    dict(g=0x3F8BFEED, u=0x3E969889, out=0x3E780000, dropped={"up": 0x3E770000}),
-    # gate rounding: 0.02443 * -0.2756
-    dict(g=0x3CC81A2C, u=0xBE8D1BD3, out=0xBB5F0000, dropped={"gate": 0xBB600000}),
-    # product exactly halfway between two bf16 values (0xbd968000): ties to the even code
-    dict(g=0xC02E0000, u=0x3EE00000, out=0xBD960000, dropped={"product": 0xBD968000}),
-]
-STAGES = ("gate", "up", "silu", "product")
-
-
-def _staged_f64_silu(g_bits, u_bits, drop=None):
-    """The staged SwiGLU evaluated independently of the oracle, with the stage `drop` left unrounded:
-    bf16 rounding in numpy, silu in f64 (math.exp) rounded once to f32, the product in f32."""
-    def rnd(v, stage):
-        return v if stage == drop else np.float32(bf16_round(np.array([v], np.float32))[0])
-
-    g = rnd(np.float32(_f32(g_bits)), "gate")
-    u = rnd(np.float32(_f32(u_bits)), "up")
-    silu = rnd(np.float32(float(g) / (1.0 + math.exp(-float(g)))), "silu")
-    return _bits(rnd(np.float32(silu * u), "product"))
-
-
 @pytest.mark.parametrize("case", STAGED_CASES, ids=lambda c: hex(c["g"]))
 def test_staged_swiglu_known_answers(case):
     """The oracle gives the expected bits; the independent evaluation gives them too with every
@@ -324,9 +294,9 @@ def test_staged_swiglu_known_answers(case):
     u = np.array([_f32(case["u"])], np.float32)
     got = _bits(O.swiglu_bf16_staged(g, u)[0])
     assert got == case["out"], hex(got)
-    assert _staged_f64_silu(case["g"], case["u"]) == case["out"]
+    assert staged_swiglu_independent(case["g"], case["u"]) == case["out"]
     for stage in STAGES:
-        alt = _staged_f64_silu(case["g"], case["u"], drop=stage)
+        alt = staged_swiglu_independent(case["g"], case["u"], drop=stage)
         if stage in case["dropped"]:
             assert alt == case["dropped"][stage] and alt != case["out"], (stage, hex(alt))
     # together the cases pin all four roundings
