@@ -298,8 +298,8 @@ int pw_moe_layer_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mod
  * reference's RoutingTrace. For decode batches of up to 8 rows over banks of up to 256 experts the
  * layer's schedule is built from each row's expert set (found without the top-k partition where the
  * row's top-8 boundary is not tied), and the routes' order and weights (the partition) run in extra
- * workgroups of the gate/up launch, beside the expert weight stream. The same routes and the same
- * output bytes as pw_route_device then pw_moe_layer_device. A row whose routing fails raises
+ * workgroups of one of the layer's expert launches, beside the expert weight stream. The same
+ * routes and the same output bytes as pw_route_device then pw_moe_layer_device. A row whose routing fails raises
  * PW_FLAG_ROUTE, and the batch is rejected like invalid routes (PW_FLAG_SCHEDULE, zero output).
  * rows 1..32; hidden a multiple of 8; x and router_weight 16-byte aligned. Asynchronous on stream. */
 int pw_moe_layer_routed_device(pw_runtime *rt, const pw_expert_bank *bank, uint32_t mode, const void *x,

@@ -78,8 +78,9 @@ struct MoeBuffers {
 // The route weights of a batch scheduled from its expert sets alone (launch_route_set_schedule):
 // per row, select_route_row gives the routes in the reference's order and their weights, which go
 // to the route outputs and to the placements (route_weights_row, pw_route_job.h). The decode
-// layer's gate/up launch runs it in eight extra workgroups while its other workgroups stream the
-// experts' weights; rows = 0: no job.
+// layer runs it in eight extra workgroups of a launch whose other workgroups stream the experts'
+// weights (the mode A split-K down, the mode A one-token gate/up, the mode B gate/up); rows = 0:
+// no job.
 struct RouteJob {
     const float *scores, *bias;  // router scores [rows][E], bias [E]
     uint32_t rows, E;
@@ -92,7 +93,7 @@ struct RouteJob {
     float *placement_w;          // the schedule's placement weights, or [rows][8] in set order
     uint32_t *flags;
 };
-constexpr uint32_t ROUTE_JOB_WGS = 8;  // workgroups a gate/up launch adds for a job (one per row)
+constexpr uint32_t ROUTE_JOB_WGS = 8;  // workgroups a launch adds for a job (one per row)
 
 // Arguments of the split-K mode A expert projection (pw_moe_a.hip).
 struct SplitArgs {
@@ -287,8 +288,8 @@ void launch_router_select(const float *scores, const float *bias, uint32_t rows,
 // schedule in one launch, with zero placement weights and the sets in set_ids [rows][8]; with
 // `quant`, the launch also quantises those activation rows. False (nothing launched) outside
 // rows 1..8, 9..256 experts, 64 routed experts. A RouteJob then writes the routes, their weights
-// and the placement weights before the combine: inside the gate/up launch (launch_moe_layer's job)
-// or as launch_route_weights.
+// and the placement weights before the combine: inside one of the layer's expert launches
+// (launch_moe_layer's job) or as launch_route_weights.
 bool launch_route_set_schedule(const float *scores, const float *bias, const ExpertPtrs *bank, uint32_t rows,
                                uint32_t E, uint32_t max_active, uint32_t *set_ids, const MoeBuffers &mb,
                                uint32_t *flags, hipStream_t stream, const QuantJob *quant = nullptr);

@@ -861,7 +861,7 @@ bool launch_route_set_schedule(const float *scores, const float *bias, const Exp
 }
 
 // The route weights of a batch scheduled by route_set_schedule_kernel as a launch of its own (when
-// the gate/up launch cannot carry them): one wave per row (route_weights_row).
+// no expert launch of the layer carries them): one wave per row (route_weights_row).
 template <int NC>
 __global__ __launch_bounds__(64) void route_weights_kernel(const RouteJob job)
 {
@@ -1355,7 +1355,11 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
         gp_args.active = mb.pieces;
         gp_args.cap = PIECE_ROWS;
     }
-    if (job)  // the fused gate/up carries the route weights (in extra workgroups)
+    // the route weights (job) ride in extra workgroups of a launch that runs anyway: the split-K
+    // down's (about 1 us there against about 4 us in the gate/up launch, whose workgroups are
+    // longer), or the fused gate/up's where the down is the one-token down+combine
+    const bool job_in_down = job && !direct;
+    if (job && !job_in_down)
         gp_args.job = *job;
     const bool fused = nt == 1 && launch_moe_a_gateup_fused(x_f32 ? 3 : 1, gp_args, pieces && !x_f32 ? placements
                                                             : max_active, mb.hidden_planes, stream);
@@ -1367,7 +1371,7 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
         launch_moe_a_swiglu(mb.partial, gp.ks, placements, I, mb.hidden_planes, flags, stream);
         timer_end(t, stream);
     }
-    if (job) {
+    if (job && !job_in_down) {
         if (!fused)  // the split gate/up cannot carry the route weights: before the down, on their own
             launch_route_weights(*job, stream);
         *job_done = true;
@@ -1397,7 +1401,15 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     }
     const SplitPlan dp = plan_split(I, 1, 3, pieces ? PIECE_ROWS : cnt);
     da.KS = dp.ks;
+    if (job_in_down && dp.bpw == 8 && (pieces || nt == 1)) {  // the instantiation compiled with a job
+        da.job = *job;
+        *job_done = true;
+    }
     launch_moe_a_split(1, 3, pieces ? 1 : nt, da, dp, pieces ? placements : max_active, stream);
+    if (job_in_down && !*job_done) {  // another down shape: the weights on their own, before the combine
+        launch_route_weights(*job, stream);
+        *job_done = true;
+    }
     timer_end(t, stream);
     return ExpertOut{mb.partial, dp.ks, (size_t)placements * H};
 }
@@ -1512,13 +1524,13 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
 {
     const DirectOut direct{out_f32, out_bf16, raw};
     // the route weights (job) must be in place before a kernel reads them: the mode A experts carry
-    // them in their gate/up launch or launch them right after it (before the down, which may combine
-    // as well), the mode B ones in their whole-K gate/up launch, else they run before the combine
+    // them in their split-K down launch (or, for the one-token down+combine, in the gate/up launch),
+    // the mode B ones in their whole-K gate/up launch, else they run before the combine
     bool job_done = false;
     const ExpertOut eo = launch_experts(mode, bank, mb, x, x_f32, rows, rows * 8, routes ? 8 : max_active,
                                         routes ? 1 : max_count, H, I, flags, stream, rows == 1 ? &direct : nullptr,
                                         routes, x_quantised, job, &job_done);
-    if (job && !job_done)  // the gate/up launch did not carry the route weights
+    if (job && !job_done)  // no expert launch carried the route weights
         launch_route_weights(*job, stream);
     if (!eo.y)
         return;  // the one-token down wrote the combined output

@@ -24,7 +24,9 @@
 
 namespace pw {
 
-template <int MATS, int NS, int NT, int BPW>
+// JOB: the launch also carries args.job in its first ROUTE_JOB_WGS workgroups (the routed decode
+// step's down; only that instantiation is compiled with it).
+template <int MATS, int NS, int NT, int BPW, bool JOB = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4 : 2))) void moe_a_split_kernel(const SplitArgs args)
 {
     extern __shared__ uint4 lds_x[];  // [NS * cnt][KC/8 + 1]
@@ -32,10 +34,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int q = lane >> 4, r16 = lane & 15;
+    uint32_t bid = blockIdx.x;
+    if constexpr (JOB) {
+        if (route_job_prologue(args.job, lds_x, &bid))
+            return;  // one of the route-weights workgroups
+    }
     const uint32_t G = args.R >> 6;
-    const uint32_t s = blockIdx.x % args.KS;
-    const uint32_t g = (blockIdx.x / args.KS) % G;
-    const uint32_t a = blockIdx.x / (args.KS * G);
+    const uint32_t s = bid % args.KS;
+    const uint32_t g = (bid / args.KS) % G;
+    const uint32_t a = bid / (args.KS * G);
     const ActiveExpert ae = args.single ? args.one : args.active[a];
     if (ae.cnt == 0)
         return;
@@ -886,7 +893,11 @@ static void launch_split_nt(const SplitArgs &args, const SplitPlan &sp, uint32_t
     switch (sp.bpw) {
     case 8:
         if constexpr (MATS == 1) {
-            hipLaunchKernelGGL((moe_a_split_kernel<MATS, NS, NT, 8>), dim3(grid), dim3(256), sp.lds, stream, args);
+            if (args.job.rows)
+                hipLaunchKernelGGL((moe_a_split_kernel<MATS, NS, NT, 8, true>), dim3(grid + ROUTE_JOB_WGS), dim3(256),
+                                   sp.lds, stream, args);
+            else
+                hipLaunchKernelGGL((moe_a_split_kernel<MATS, NS, NT, 8>), dim3(grid), dim3(256), sp.lds, stream, args);
             break;
         }
         [[fallthrough]];

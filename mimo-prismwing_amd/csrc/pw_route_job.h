@@ -1,5 +1,5 @@
 // The route weights of one batch row scheduled from its expert set alone (RouteJob): run by the
-// standalone route_weights_kernel and by the extra workgroups of the decode gate/up launches.
+// standalone route_weights_kernel and by the extra workgroups of the decode layer's expert launches.
 #pragma once
 
 #include "pw_device.h"
@@ -63,7 +63,7 @@ __device__ __forceinline__ void route_weights_row(const RouteJob &j, uint32_t p,
     }
 }
 
-// The extra workgroups of a gate/up launch carrying a job (the first ROUTE_JOB_WGS of its grid):
+// The extra workgroups of an expert launch carrying a job (the first ROUTE_JOB_WGS of its grid):
 // wave 0 of workgroup p < rows takes row p. Returns true for those workgroups, which then leave;
 // the others see their own index less ROUTE_JOB_WGS in *bid.
 __device__ __forceinline__ bool route_job_prologue(const RouteJob &j, void *lds, uint32_t *bid)

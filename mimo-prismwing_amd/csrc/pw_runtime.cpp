@@ -1394,8 +1394,8 @@ int pw_moe_layer_routed_device(pw_runtime *rt, const pw_expert_bank *bank, uint3
                                                  (uint32_t *)rt->set_ids.p, rt->mb, rt->d_flags, s,
                                                  mode == PW_MODE_B ? &qj : nullptr)) {
         // the expert sets are scheduled; the routes' order and weights (a serial partition per row)
-        // run in extra workgroups of the gate/up launch while its others stream the experts'
-        // weights (or in a launch of their own before the combine)
+        // run in extra workgroups of an expert launch (mode A: the down, mode B: the gate/up) while
+        // its others stream the experts' weights (or in a launch of their own before the combine)
         pw::RouteJob job{};
         job.scores = scores;
         job.bias = bias;
