@@ -532,24 +532,49 @@ static bool wave_schedule(uint32_t rows, uint32_t E, uint32_t max_active)
 // then filled lane-parallel (lane a: the a-th routed expert). Route rejection follows
 // moe_schedule_kernel: an id >= E, a non-finite weight or a token naming one expert twice raises
 // FLAG_SCHEDULE and leaves the placement tables zeroed.
-__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v, int lane)
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
 {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_up(v, d, 64);
-        if (lane >= d)
-            v += o;
-    }
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Inclusive prefix sum over the wave (lane l: v_0 + ... + v_l) by DPP moves: shifts by 1, 2, 4, 8
+// within each 16-lane row, then the totals of rows 0 and 2 (lanes 15 and 47) into rows 1 and 3 and
+// the total of rows 0-1 (lane 31) into rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v)
+{
+    v += dpp_u32<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_u32<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_u32<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_u32<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_u32<0x142, 0xa>(v);  // row_bcast:15
+    v += dpp_u32<0x143, 0xc>(v);  // row_bcast:31
     return v;
 }
 
+// The wave's maximum, as a scalar: within each 16-lane row by DPP swaps, then the four rows' maxima.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    v = max(v, dpp_u32<0xb1, 0xf>(v));   // quad_perm [1, 0, 3, 2]
+    v = max(v, dpp_u32<0x4e, 0xf>(v));   // quad_perm [2, 3, 0, 1]
+    v = max(v, dpp_u32<0x141, 0xf>(v));  // row_half_mirror
+    v = max(v, dpp_u32<0x140, 0xf>(v));  // row_mirror
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
 // LDS of the one-wave schedule besides the bank's pointer table.
-struct SchedWaveLds {
+struct alignas(16) SchedWaveLds {
     uint32_t bitmap[32];      // routed expert ids (E <= 1024)
     uint32_t expert_of[64];   // by rank
-    uint32_t count_of[64];
+    uint32_t route[64];       // lane p's expert id where its route is valid, else NO_ROUTE
+    uint32_t rows_of[1024];   // bit r: token row r routes to the expert (valid routes only)
     uint16_t tok_of[64 * 16]; // token rows of each expert's first 16 placements
 };
+constexpr uint32_t NO_ROUTE = 0xffffffffu;
 
 // Orders the LDS accesses of one wave's lanes (its LDS operations complete in order; this waits for
 // them and keeps the compiler from moving memory accesses across).
@@ -559,79 +584,73 @@ __device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcn
 // the bank's pointer table already in lds_bank (E x 48 bytes) and visible to this wave. Only this
 // wave touches `lds`, so it needs no workgroup barrier (the routed-layer entry that selects the
 // routes runs it after its other waves have left).
+//
+// Lane p = 8 r + k holds route k of token row r. Its slot (lower expert ids first, then lower token
+// rows) is the placements of the experts ranked below its own plus the earlier token rows routed to
+// its expert: the set bits below r of rows_of[id] (a token row names an expert at most once among
+// its valid routes).
 __device__ __forceinline__ void schedule_wave_body(
     uint32_t id, float w, uint32_t rows, uint32_t E, uint32_t max_active, const u32x4 *lds_bank, SchedWaveLds &lds,
     MoePlan *plan, uint32_t *__restrict__ active_expert, uint32_t *__restrict__ active_offset,
     ActiveExpert *__restrict__ active, uint32_t *__restrict__ placement_pos, float *__restrict__ placement_w,
     uint32_t *__restrict__ row_slots, ActiveExpert *__restrict__ pieces, uint32_t max_pieces, uint32_t *flags)
 {
-    uint32_t *bitmap = lds.bitmap, *expert_of = lds.expert_of, *count_of = lds.count_of;
+    uint32_t *bitmap = lds.bitmap, *expert_of = lds.expert_of, *rows_of = lds.rows_of;
     uint16_t *tok_of = lds.tok_of;
     const int lane = threadIdx.x & 63;
     const uint32_t P = rows * 8;
     const uint32_t nw = (E + 31) >> 5;
+    const uint32_t r = (uint32_t)lane >> 3, k = (uint32_t)lane & 7;
     if ((uint32_t)lane < nw)
         bitmap[lane] = 0u;
-    count_of[lane] = 0u;
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-        tok_of[i * 64 + lane] = 0;
+    u32x4 *tz = (u32x4 *)tok_of + 2 * lane;
+    tz[0] = u32x4{0u, 0u, 0u, 0u};
+    tz[1] = u32x4{0u, 0u, 0u, 0u};
     bool ok = (uint32_t)lane < P && id < E && finite_f32(w);
-    // a token naming one expert twice: the later slot is rejected
-    const int base = lane & ~7, sl = lane & 7;
+    lds.route[lane] = ok ? id : NO_ROUTE;
+    if (id < E)
+        rows_of[id] = 0u;
+    wave_lds_sync();
+    // the token row's eight routes; a token naming one expert twice: the later slot is rejected
+    const u32x4 g0 = ((const u32x4 *)lds.route)[2 * r], g1 = ((const u32x4 *)lds.route)[2 * r + 1];
+    const uint32_t grp[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
     bool dup = false;
+    uint32_t before = 0;  // the token row's valid routes to lower expert ids
 #pragma unroll
-    for (int k = 0; k < 7; ++k) {
-        const uint32_t o = __shfl(id, base + k, 64);
-        const int ov = __shfl((int)ok, base + k, 64);
-        dup |= k < sl && ov && o == id;
+    for (uint32_t m = 0; m < 8; ++m) {
+        dup |= m < k && grp[m] == id;
+        before += grp[m] < id ? 1u : 0u;
     }
     ok &= !dup;
     const bool bad = __ballot((uint32_t)lane < P && !ok) != 0;
-    const uint64_t valid = __ballot(ok);
-    wave_lds_sync();
-    if (ok)
+    if (ok) {
         atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+        atomicOr(&rows_of[id], 1u << r);
+    }
     wave_lds_sync();
     // rank of this lane's expert: routed ids below it
     const uint32_t word = (uint32_t)lane < nw ? bitmap[lane] : 0u;
     const uint32_t wc = __popc(word);
-    const uint32_t wincl = wave_inclusive_scan(wc, lane);
+    const uint32_t wincl = wave_inclusive_scan(wc);
     const uint32_t U = __builtin_amdgcn_readlane(wincl, 63);
     const int src = ok ? (int)(id >> 5) : 0;
     const uint32_t wsel = __shfl(word, src, 64), esel = __shfl(wincl - wc, src, 64);
     const uint32_t rank = ok ? esel + __popc(wsel & ((1u << (id & 31)) - 1u)) : 0u;
-    if (ok) {
+    const uint32_t mine = ok ? rows_of[id] : 0u;
+    if (ok)
         expert_of[rank] = id;
-        atomicAdd(&count_of[rank], 1u);
-    }
-    // slot of this placement (lower expert ids first, then lower token rows) and its position
-    // among the token's routes ordered by expert id
-    uint32_t slot = 0;
-    for (int j = 0; j < 64; ++j) {
-        const uint32_t idj = (uint32_t)__builtin_amdgcn_readlane((int)id, j);
-        const bool vj = (valid >> j) & 1u;
-        slot += (vj && (idj < id || (idj == id && j < lane))) ? 1u : 0u;
-    }
-    uint32_t before = 0;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const uint32_t o = __shfl(id, base + m, 64);
-        before += (((valid >> (base + m)) & 1u) && o < id) ? 1u : 0u;
-    }
     wave_lds_sync();
     // lane a: the a-th routed expert
     const uint32_t a = (uint32_t)lane;
     const uint32_t e_a = a < U ? expert_of[a] : 0u;
-    const uint32_t c_a = a < U ? count_of[a] : 0u;
-    const uint32_t incl = wave_inclusive_scan(c_a, lane);
+    const uint32_t c_a = a < U ? __popc(rows_of[e_a]) : 0u;
+    const uint32_t incl = wave_inclusive_scan(c_a);
     const uint32_t off_a = incl - c_a, total = __builtin_amdgcn_readlane(incl, 63);
-    // this placement's index inside its expert -> token row table
-    if (ok) {
-        const uint32_t t = slot - (uint32_t)__shfl((int)off_a, (int)rank, 64);
-        if (t < 16)
-            tok_of[rank * 16 + t] = (uint16_t)(lane >> 3);
-    }
+    // this placement's index inside its expert -> token row table, and its slot
+    const uint32_t t = __popc(mine & ((1u << r) - 1u));
+    const uint32_t slot = (uint32_t)__shfl((int)off_a, (int)rank, 64) + t;
+    if (ok && t < 16)
+        tok_of[rank * 16 + t] = (uint16_t)r;
     wave_lds_sync();
     u32x4 ep0 = {0u, 0u, 0u, 0u}, ep1 = ep0, ep2 = ep0;
     if (a < U && a < max_active) {
@@ -662,7 +681,7 @@ __device__ __forceinline__ void schedule_wave_body(
     // their LDS stages are sized for that many rows (see launch_a_moe); a piece carries its slots'
     // token rows (slots 0..15 of an expert: PIECE_ROWS * pieces <= 16 here)
     const uint32_t np = (c_a + PIECE_ROWS - 1) / PIECE_ROWS;  // 0 past the routed experts
-    const uint32_t pincl = wave_inclusive_scan(np, lane);
+    const uint32_t pincl = wave_inclusive_scan(np);
     const uint32_t pbase = pincl - np, npieces = __builtin_amdgcn_readlane(pincl, 63);
     for (uint32_t i = 0; i < np; ++i) {
         if (pbase + i < max_pieces) {
@@ -696,10 +715,7 @@ __device__ __forceinline__ void schedule_wave_body(
             row_slots[(size_t)(lane >> 3) * 8 + (before & 7)] = slot;
         }
     }
-    uint32_t mx = c_a;
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1)
-        mx = max(mx, (uint32_t)__shfl_xor(mx, d, 64));
+    const uint32_t mx = wave_max_u32(c_a);
     if (lane == 0) {
         plan->n_active = U;
         plan->n_placements = total;

@@ -393,6 +393,22 @@ PW_WAVE void nth_element_wave_regs(W &w, WaveRow<NC> &a, uint32_t nth, uint32_t 
     }
 }
 
+// The row's scores and bias at positions e = 64 c + lane, read by every lane (positions past E,
+// E >= 1, reread position E - 1, so no load sits behind a branch and the row's loads are all in
+// flight together); the caller masks positions >= E.
+template <int NC, class W>
+PW_WAVE void load_row_scores(W &w, const float *scores_row, const float *bias, uint32_t E, float (&sc)[NC],
+                             float (&b)[NC])
+{
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const uint32_t e = 64 * c + w.lane();
+        const uint32_t ec = e < E ? e : E - 1;
+        sc[c] = scores_row[ec];
+        b[c] = bias[ec];
+    }
+}
+
 // The largest value at positions [from, n) of the row (-inf when none).
 template <int NC, class W>
 PW_WAVE float wave_max_from(W &w, const WaveRow<NC> &a, uint32_t from, uint32_t n)
@@ -421,19 +437,16 @@ PW_WAVE int select_route_row(W &w, const float *scores_row, const float *bias, u
     WaveRow<NC> a;
     uint32_t sb[NC];  // the uncorrected scores' bits, by position as loaded (= expert id)
     bool bad = false;
+    float sc[NC], b[NC];
+    load_row_scores<NC>(w, scores_row, bias, E, sc, b);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const uint32_t e = 64 * c + w.lane();
-        sb[c] = 0u;
-        a.v[c] = -__builtin_inff();
-        a.id[c] = -1;
-        if (e < E) {
-            const float sc = scores_row[e], b = bias[e];
-            bad |= !finite_f32_bits(sc) || !finite_f32_bits(b);
-            sb[c] = f32_bits(sc);
-            a.v[c] = sc + b;
-            a.id[c] = (int32_t)e;
-        }
+        const bool in = e < E;
+        bad |= in && (!finite_f32_bits(sc[c]) || !finite_f32_bits(b[c]));
+        sb[c] = in ? f32_bits(sc[c]) : 0u;
+        a.v[c] = in ? sc[c] + b[c] : -__builtin_inff();
+        a.id[c] = in ? (int32_t)e : -1;
     }
     *tie = false;
     sel_k = 0u;
@@ -507,15 +520,15 @@ PW_WAVE bool fast_top8_set(W &w, const float *scores_row, const float *bias, uin
 {
     float v[NC];
     bool bad = false;
+    float sc[NC], b[NC];
+    load_row_scores<NC>(w, scores_row, bias, E, sc, b);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         const uint32_t e = 64 * c + w.lane();
-        v[c] = -__builtin_inff();
-        if (e < E) {
-            const float sc = scores_row[e], b = bias[e];
-            v[c] = sc + b;
-            bad |= !finite_f32_bits(sc) || !finite_f32_bits(b) || !finite_f32_bits(v[c]);
-        }
+        const bool in = e < E;
+        const float s = sc[c] + b[c];
+        v[c] = in ? s : -__builtin_inff();
+        bad |= in && (!finite_f32_bits(sc[c]) || !finite_f32_bits(b[c]) || !finite_f32_bits(s));
     }
     if (w.ballot(bad))
         return false;
