@@ -642,6 +642,7 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
     const uint32_t row0 = blockIdx.x * 16;
     float *red = (float *)(lds_x + 16 * 3 * STRIDE);  // [16 waves][16 rows]
     uint32_t *rank_slot = (uint32_t *)(red + 16 * 16);  // [8] routes: the slot of each expert rank
+    float *rank_w = (float *)(rank_slot + 8);           // [8] routes: the weight of each expert rank
     // routes without a schedule: lane i < 8 ranks route i by (expert id, route index), so the
     // waves and the combine take the experts in ascending id like the schedule; duplicates, ids
     // past the bank and non-finite weights are rejected
@@ -664,6 +665,7 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
         rejected = __ballot(lane < 8 && bad) != 0;
         if (wave == 0 && lane < 8) {
             rank_slot[rank] = li;
+            rank_w[rank] = rw;
             if (bad)
                 raise_flag(args.flags, FLAG_SCHEDULE);
         }
@@ -736,18 +738,30 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
     __syncthreads();
     if (wave != 0 || lane >= 16)
         return;
-    // 4. the combine for output row row0 + lane
+    // 4. the combine for output row row0 + lane, with every expert's route weight fetched first (from
+    //    LDS with routes; with a schedule, the eight slots and then the eight weights in flight)
+    const uint32_t ne = n_active < 8 ? n_active : 8;
+    float wt[8];
+    if (args.route_ids) {
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e)
+            wt[e] = rank_w[e];
+    } else {
+        uint32_t sl[8];
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e)
+            sl[e] = e < ne ? args.active[e].off : 0u;
+#pragma unroll
+        for (uint32_t e = 0; e < 8; ++e)
+            wt[e] = placement_w[sl[e] < args.P ? sl[e] : 0];
+    }
     float acc = 0.f;
-    for (uint32_t e = 0; e < n_active && e < 8; ++e) {
-        const float y = red[(2 * e) * 16 + lane] + red[(2 * e + 1) * 16 + lane];
-        float w;
-        if (args.route_ids) {
-            w = load_g(args.route_w + rank_slot[e]);
-        } else {
-            const uint32_t slot = args.active[e].off;
-            w = placement_w[slot < args.P ? slot : 0];
+#pragma unroll
+    for (uint32_t e = 0; e < 8; ++e) {
+        if (e < ne) {
+            const float y = red[(2 * e) * 16 + lane] + red[(2 * e + 1) * 16 + lane];
+            acc = __fadd_rn(acc, __fmul_rn(y, wt[e]));
         }
-        acc = __fadd_rn(acc, __fmul_rn(y, w));
     }
     acc = rejected ? 0.f : acc;
     const float r = round_bf16(acc);
@@ -773,7 +787,7 @@ bool launch_moe_a_down_combine1(const SplitArgs &args, const MoePlan *plan, cons
     // token, so its eight placements are the rows
     if (args.P != 8 || args.rows != 8 || args.K != 2048 || args.R % 16 != 0)
         return false;
-    const size_t lds = (size_t)16 * 3 * (1024 / 8 + 1) * 16 + 16 * 16 * 4 + 8 * 4;
+    const size_t lds = (size_t)16 * 3 * (1024 / 8 + 1) * 16 + 16 * 16 * 4 + 8 * 4 + 8 * 4;
     (void)hipFuncSetAttribute((const void *)moe_a_down_combine1_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                               (int)lds);
     hipLaunchKernelGGL(moe_a_down_combine1_kernel, dim3(args.R >> 4), dim3(1024), lds, stream, args, plan,
