@@ -110,6 +110,25 @@ struct ActiveExpert {
 };
 static_assert(sizeof(ActiveExpert) == 96, "ActiveExpert is read as 96 bytes");
 
+// Entry a (wave-uniform) of a schedule table that an earlier launch wrote: read through the
+// constant address space, so the whole entry comes in scalar loads in one round trip, and taken
+// by an empty asm before the caller's early exits, so no part of it is fetched after them (a
+// compiler that sinks the pointer loads below an exit adds a second dependent round trip).
+__device__ __forceinline__ ActiveExpert load_entry(const ActiveExpert *table, uint32_t a)
+{
+    typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+    struct Raw {
+        u32x8 q[3];
+    };
+    const __attribute__((address_space(4))) u32x8 *p = (const __attribute__((address_space(4))) u32x8 *)(table + a);
+    Raw r;
+    r.q[0] = p[0];
+    r.q[1] = p[1];
+    r.q[2] = p[2];
+    asm volatile("" ::"s"(r.q[0]), "s"(r.q[1]), "s"(r.q[2]));
+    return __builtin_bit_cast(ActiveExpert, r);
+}
+
 // Device-side routed schedule (ascending expert id, positions ascending per expert), the
 // layout of the reference's BTreeMap<expert, [(position, weight)]> (src/text_endpoint.rs:4767-4775).
 struct MoePlan {

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4
     const uint32_t s = bid % args.KS;
     const uint32_t g = (bid / args.KS) % G;
     const uint32_t a = bid / (args.KS * G);
-    const ActiveExpert ae = args.single ? args.one : args.active[a];
+    const ActiveExpert ae = args.single ? args.one : load_entry(args.active, a);
     if (ae.cnt == 0)
         return;
     if (ae.cnt > 16u * NT || ae.cnt > args.cap) {
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(512) void moe_a_gateup_fused_kernel(const SplitArgs
     const uint32_t G = args.R / RM;
     const uint32_t a = bid / G, local = bid % G;
     const uint32_t g = G % 8 == 0 && !args.single ? (local % 8) * (G / 8) + local / 8 : local;
-    const ActiveExpert ae = args.single ? args.one : (args.route_ids ? route_entry(args, a) : args.active[a]);
+    const ActiveExpert ae = args.single ? args.one : (args.route_ids ? route_entry(args, a) : load_entry(args.active, a));
     if (ae.cnt == 0)
         return;
     if (ae.cnt > 16u || ae.cnt > args.cap) {
@@ -618,7 +618,8 @@ bool launch_moe_a_down_out(const SplitArgs &args, float *out_f32, uint16_t *out_
 
 // Down and combine of a one-token batch in one launch (the decode layer at width 1: eight routed
 // experts with one slot each). Work item: 16 output rows. Sixteen waves: wave w takes routed
-// expert w / 2 (ascending id, the schedule's order) and K half w % 2, which is exactly the split-K
+// expert w / 2 (the schedule's, in ascending id, or route w / 2 of a batch passed as routes) and K
+// half w % 2, which is exactly the split-K
 // down's work for those rows (KS = 2, eight 128-column blocks per split, the same MFMA sequence and
 // block-scale order), so each split sum is the same f32 value. The sums meet in LDS; lanes 0..15
 // of wave 0 then form each output row as the combine does: per expert in ascending id, the split
@@ -638,17 +639,20 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int q = lane >> 4, r16 = lane & 15;
     const uint32_t a = (uint32_t)wave >> 1, s = (uint32_t)wave & 1;
-    const uint32_t K = args.K, H = args.R;
+    const uint32_t K = args.K;
     const uint32_t row0 = blockIdx.x * 16;
     float *red = (float *)(lds_x + 16 * 3 * STRIDE);  // [16 waves][16 rows]
     uint32_t *rank_slot = (uint32_t *)(red + 16 * 16);  // [8] routes: the slot of each expert rank
     float *rank_w = (float *)(rank_slot + 8);           // [8] routes: the weight of each expert rank
-    // routes without a schedule: lane i < 8 ranks route i by (expert id, route index), so the
-    // waves and the combine take the experts in ascending id like the schedule; duplicates, ids
-    // past the bank and non-finite weights are rejected
-    uint32_t n_active, slot_of_a = a;
+    // routes without a schedule: waves 2a and 2a + 1 take route a itself (its pointer entry is
+    // loaded with the routes, so the weights wait on two round trips); lane i < 8 ranks route i by
+    // (expert id, route index), so the combine takes the experts in ascending id like the
+    // schedule; duplicates, ids past the bank and non-finite weights are rejected
+    uint32_t n_active;
     bool rejected;  // routes that fail the schedule's checks: the combine writes zeros, as the schedule's does
+    ActiveExpert ae{};
     if (args.route_ids) {
+        ae = route_entry(args, a);
         const uint32_t li = (uint32_t)lane & 7;
         const uint32_t id = load_g(args.route_ids + li);
         const float rw = load_g(args.route_w + li);
@@ -660,7 +664,6 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
             rank += idj < id || (idj == id && (uint32_t)j < li);
             dup |= idj == id && (uint32_t)j != li;
         }
-        slot_of_a = __builtin_ctzll(__ballot(lane < 8 && rank == a));
         const bool bad = dup || id >= args.E || !finite_f32(rw);
         rejected = __ballot(lane < 8 && bad) != 0;
         if (wave == 0 && lane < 8) {
@@ -676,7 +679,8 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
     }
     f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
     if (a < n_active) {
-        const ActiveExpert ae = args.route_ids ? route_entry(args, slot_of_a) : args.active[a];
+        if (!args.route_ids)
+            ae = load_entry(args.active, a);
         if (ae.cnt != 1 && lane == 0)
             raise_flag(args.flags, FLAG_SCHEDULE);
         const uint32_t k0 = s * KC;
@@ -759,7 +763,9 @@ __global__ __launch_bounds__(1024) void moe_a_down_combine1_kernel(const SplitAr
 #pragma unroll
     for (uint32_t e = 0; e < 8; ++e) {
         if (e < ne) {
-            const float y = red[(2 * e) * 16 + lane] + red[(2 * e + 1) * 16 + lane];
+            // the waves of the e-th expert in ascending id: those of its route (with routes) or 2e, 2e + 1
+            const uint32_t wa = args.route_ids ? rank_slot[e] : e;
+            const float y = red[(2 * wa) * 16 + lane] + red[(2 * wa + 1) * 16 + lane];
             acc = __fadd_rn(acc, __fmul_rn(y, wt[e]));
         }
     }

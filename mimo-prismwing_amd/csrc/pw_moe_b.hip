@@ -106,7 +106,7 @@ __global__ __launch_bounds__(512) void moe_b_gateup_fused_kernel(const MoeBArgs 
     const uint32_t G = args.R / RM;
     const uint32_t a = bid / G;
     const uint32_t g = xcd_group(bid % G, G, args.single);
-    const ActiveExpert ae = args.single ? args.one : args.active[a];
+    const ActiveExpert ae = args.single ? args.one : load_entry(args.active, a);
     if (ae.cnt == 0)
         return;
     if (ae.cnt > 16u || ae.cnt > args.cap) {
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(512) void moe_b_down_fused_kernel(const MoeBArgs ar
     const uint32_t a = blockIdx.x / (G * KS), rem = blockIdx.x % (G * KS);
     const uint32_t s = rem % KS;
     const uint32_t g = xcd_group(rem / KS, G, args.single);
-    const ActiveExpert ae = args.single ? args.one : args.active[a];
+    const ActiveExpert ae = args.single ? args.one : load_entry(args.active, a);
     if (ae.cnt == 0 || ae.cnt > 16u || ae.cnt > args.cap)
         return;  // the gate/up launch flagged such an entry
     const uint32_t K = args.K, blocks = K >> 7;
