@@ -82,6 +82,25 @@ def test_schedule_matches_btreemap(rt, bank256, rows):
     check_equal(device_schedule(rt, bank256, sel, w), host_schedule(sel, w, 256))
 
 
+@pytest.mark.parametrize("n_experts", [9, 64, 1000, 1024])
+def test_schedule_wave_expert_counts(rt, n_experts):
+    """The one-wave schedule (up to 8 rows) over banks of 9 to 1024 experts (one to 32 words of its
+    routed-id bitmap, token-row masks at every id): routes spread over the whole id range, every
+    row on the eight highest ids (one expert per row rank, eight rows each), and a row naming an
+    expert twice (rejected, then the valid routes again)."""
+    bank = WL.synth_bank(rt, n_experts=n_experts, hidden=128, inter=128, seed=WL.SEED_BASE + 72 + n_experts)
+    for rows in (1, 5, 8):
+        rng = np.random.default_rng(n_experts * 10 + rows)
+        sel, w = distinct_routes(rng, rows, n_experts)
+        check_equal(device_schedule(rt, bank, sel, w), host_schedule(sel, w, n_experts))
+        top = np.tile(np.arange(n_experts - 1, n_experts - 9, -1, dtype=np.uint32), (rows, 1))
+        check_equal(device_schedule(rt, bank, top, w), host_schedule(top, w, n_experts))
+    twice = sel.copy()
+    twice[rows - 1, 7] = twice[rows - 1, 2]
+    assert device_schedule(rt, bank, twice, w)[4] & P.FLAG_SCHEDULE
+    check_equal(device_schedule(rt, bank, sel, w), host_schedule(sel, w, n_experts))
+
+
 @pytest.mark.parametrize("rows", [100, 2048])
 def test_schedule_zipf_routes(rt, bank256, rows):
     rng = np.random.default_rng(900 + rows)
