@@ -317,6 +317,23 @@ __device__ __forceinline__ void load_act8<uint16_t>(const uint16_t *p, float (&v
     }
 }
 
+// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r + 15 of a wave, all active): swaps
+// within quads, then the half-row and row mirrors, each a v_max_f32 with a DPP operand (no LDS
+// permute).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row16_max(float m)
+{
+    m = fmaxf(m, dpp_f32<0xb1>(m));   // quad_perm [1, 0, 3, 2]
+    m = fmaxf(m, dpp_f32<0x4e>(m));   // quad_perm [2, 3, 0, 1]
+    m = fmaxf(m, dpp_f32<0x141>(m));  // row_half_mirror
+    m = fmaxf(m, dpp_f32<0x140>(m));  // row_mirror
+    return m;
+}
+
 // Dynamic FP8 quantisation of one 128-column activation group (dynamic_fp8_quantized_group128,
 // kernels/block_fp8_gemv.metal:84-137; CPU dynamic_fp8_activations, src/text_endpoint.rs:3008-3051)
 // by 16 lanes of one wave (lane16 = 0..15, eight consecutive values each): max |finite x| over
@@ -340,9 +357,7 @@ __device__ __forceinline__ void quant_group128_team(const T *__restrict__ x, uin
     }
     if (!all)
         raise_flag(flags, FLAG_QUANT_NONFINITE);
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1)  // maximum over the group's 16 lanes
-        m = fmaxf(m, __shfl_xor(m, off, 16));
+    m = row16_max(m);  // maximum over the group's 16 lanes (one DPP row: callers run whole teams)
     // bf16 inputs: a bf16 maximum, so the scale needs no division (scale_of_bf16_max), one
     // division per group for the reciprocal and quant_ratio_bf16 per value (the same codes as
     // x / scale over every bf16 input); f32 inputs divide each value

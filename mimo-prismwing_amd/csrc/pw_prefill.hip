@@ -571,22 +571,6 @@ void launch_swiglu_staged(const float *gate, const float *up, uint32_t n, const 
 
 constexpr int SWQ_GPT = 2;  // 128-column groups per 16-lane team of prefill_swiglu_quant_kernel
 
-// Maximum over the 16 lanes of a DPP row (lanes 16r .. 16r + 15 of a wave): swaps within quads,
-// then the half-row and row mirrors, each a v_max_f32 with a DPP operand (no LDS permute).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f32(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float row16_max(float m)
-{
-    m = fmaxf(m, dpp_f32<0xb1>(m));   // quad_perm [1, 0, 3, 2]
-    m = fmaxf(m, dpp_f32<0x4e>(m));   // quad_perm [2, 3, 0, 1]
-    m = fmaxf(m, dpp_f32<0x141>(m));  // row_half_mirror
-    m = fmaxf(m, dpp_f32<0x140>(m));  // row_mirror
-    return m;
-}
-
 // bf16_staged_swiglu (kernels/block_fp8_gemv.metal:139-160; CPU src/text_endpoint.rs:5336-5343)
 // on the bf16 gate/up outputs, h = round(round(g / (1 + e^-g)) * u), fused with the dynamic
 // per-(slot, 128-column group) re-quantisation of h for the down projection
