@@ -228,15 +228,6 @@ __device__ __forceinline__ bool finite_f32(float v) { return (f32_bits(v) & 0x7f
 // table, the elementwise staged SwiGLU), so the in-place and table forms give the same bits.
 __device__ __forceinline__ float silu_bf16_staged(float g) { return round_bf16(g / (1.0f + expf(-g))); }
 
-// Butterfly max over the 64 lanes of a wave.
-__device__ __forceinline__ float wave_max(float v)
-{
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1)
-        v = fmaxf(v, __shfl_xor(v, offset, 64));
-    return v;
-}
-
 // One wave's primitives for code written against a wave policy (pw_select_wave.h): lane id,
 // ballot, a lane's value (the lane index wave-uniform), the value of the lane below, the wave
 // maximum, and LDS ordering between the wave's own lanes (its LDS operations complete in order).
@@ -379,30 +370,52 @@ __device__ __forceinline__ void quant_group128_team(const T *__restrict__ x, uin
     *(uint2 *)(codes + base) = make_uint2(lo, hi);
 }
 
-// Exclusive prefix sum over the workgroup (blockDim.x <= 1024): wave scans with lane shuffles,
-// then a scan of the per-wave totals. `tmp` holds 33 words of LDS. Returns the total in *total.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// Inclusive prefix sum over the wave (lane l: v_0 + ... + v_l) by DPP moves: shifts by 1, 2, 4, 8
+// within each 16-lane row, then the totals of rows 0 and 2 (lanes 15 and 47) into rows 1 and 3 and
+// the total of rows 0-1 (lane 31) into rows 2 and 3.
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v)
+{
+    v += dpp_u32<0x111, 0xf>(v);  // row_shr:1
+    v += dpp_u32<0x112, 0xf>(v);  // row_shr:2
+    v += dpp_u32<0x114, 0xf>(v);  // row_shr:4
+    v += dpp_u32<0x118, 0xf>(v);  // row_shr:8
+    v += dpp_u32<0x142, 0xa>(v);  // row_bcast:15
+    v += dpp_u32<0x143, 0xc>(v);  // row_bcast:31
+    return v;
+}
+
+// The wave's maximum, as a scalar: within each 16-lane row by DPP swaps, then the four rows' maxima.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    v = max(v, dpp_u32<0xb1, 0xf>(v));   // quad_perm [1, 0, 3, 2]
+    v = max(v, dpp_u32<0x4e, 0xf>(v));   // quad_perm [2, 3, 0, 1]
+    v = max(v, dpp_u32<0x141, 0xf>(v));  // row_half_mirror
+    v = max(v, dpp_u32<0x140, 0xf>(v));  // row_mirror
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(r0, r1), max(r2, r3));
+}
+
+// Exclusive prefix sum over the workgroup (blockDim.x <= 1024, whole waves): DPP scans of each
+// wave, then of the per-wave totals. `tmp` holds 33 words of LDS. Returns the total in *total.
 __device__ inline uint32_t block_exclusive_scan(uint32_t v, uint32_t *tmp, uint32_t *total)
 {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-    uint32_t inc = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t o = __shfl_up(inc, d, 64);
-        if (lane >= (uint32_t)d)
-            inc += o;
-    }
+    const uint32_t inc = wave_inclusive_scan(v);
     if (lane == 63)
         tmp[wave] = inc;
     __syncthreads();
     if (threadIdx.x < 64) {
-        uint32_t w = threadIdx.x < nw ? tmp[threadIdx.x] : 0u;
-        uint32_t wi = w;
-#pragma unroll
-        for (int d = 1; d < 16; d <<= 1) {
-            const uint32_t o = __shfl_up(wi, d, 64);
-            if (threadIdx.x >= (uint32_t)d)
-                wi += o;
-        }
+        const uint32_t w = threadIdx.x < nw ? tmp[threadIdx.x] : 0u;
+        const uint32_t wi = wave_inclusive_scan(w);
         if (threadIdx.x < nw)
             tmp[16 + threadIdx.x] = wi - w;  // exclusive wave offsets
         if (threadIdx.x == nw - 1)

@@ -532,40 +532,6 @@ static bool wave_schedule(uint32_t rows, uint32_t E, uint32_t max_active)
 // then filled lane-parallel (lane a: the a-th routed expert). Route rejection follows
 // moe_schedule_kernel: an id >= E, a non-finite weight or a token naming one expert twice raises
 // FLAG_SCHEDULE and leaves the placement tables zeroed.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
-{
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
-}
-
-// Inclusive prefix sum over the wave (lane l: v_0 + ... + v_l) by DPP moves: shifts by 1, 2, 4, 8
-// within each 16-lane row, then the totals of rows 0 and 2 (lanes 15 and 47) into rows 1 and 3 and
-// the total of rows 0-1 (lane 31) into rows 2 and 3.
-__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v)
-{
-    v += dpp_u32<0x111, 0xf>(v);  // row_shr:1
-    v += dpp_u32<0x112, 0xf>(v);  // row_shr:2
-    v += dpp_u32<0x114, 0xf>(v);  // row_shr:4
-    v += dpp_u32<0x118, 0xf>(v);  // row_shr:8
-    v += dpp_u32<0x142, 0xa>(v);  // row_bcast:15
-    v += dpp_u32<0x143, 0xc>(v);  // row_bcast:31
-    return v;
-}
-
-// The wave's maximum, as a scalar: within each 16-lane row by DPP swaps, then the four rows' maxima.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
-{
-    v = max(v, dpp_u32<0xb1, 0xf>(v));   // quad_perm [1, 0, 3, 2]
-    v = max(v, dpp_u32<0x4e, 0xf>(v));   // quad_perm [2, 3, 0, 1]
-    v = max(v, dpp_u32<0x141, 0xf>(v));  // row_half_mirror
-    v = max(v, dpp_u32<0x140, 0xf>(v));  // row_mirror
-    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
-    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
-    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
-    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
-    return max(max(r0, r1), max(r2, r3));
-}
-
 // LDS of the one-wave schedule besides the bank's pointer table.
 struct alignas(16) SchedWaveLds {
     uint32_t bitmap[32];      // routed expert ids (E <= 1024)
