@@ -39,8 +39,11 @@ def _device_route(rt, torch, x, rw, bias, x_f32=False, w_f32=False):
     return (ids.cpu().numpy().astype(np.uint32), wts.cpu().numpy(), scores.cpu().numpy(), int(ties.item()), flags)
 
 
-@pytest.mark.parametrize("rows,zipf", [(1, False), (8, False), (8, True), (32, False), (300, True)])
+@pytest.mark.parametrize("rows,zipf", [(1, False), (2, False), (3, True), (8, False), (8, True), (12, False),
+                                       (32, False), (300, True)])
 def test_device_routes_bit_exact(rt, rows, zipf):
+    """Scores, routes, weights and ties bit-exact with the oracle: 1, 2, 3 (four loaded rows, the
+    last reread) and 8 rows per scores workgroup, and 12 rows (a chunk of eight, then one of four)."""
     import torch
     x = WL.activations(rows, WL.SEED_BASE + 60 + rows)
     rw, bias = WL.router_inputs(WL.SEED_BASE + 3, zipf=zipf)
