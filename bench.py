@@ -300,6 +300,20 @@ def projection_legs(torch, rt, bank, P, WL, calls=200, small_only=False):
             rec[label] = {"us": round(us, 2), "GB/s": round(alg / (us * 1e-6) / 1e9, 1), "spread_us": sp}
         out[f"bf16_o_proj_w{width}"] = rec
     del bprojs, wb
+    # the LM head through the same wide linear (src/text_endpoint.rs:5673-5705): [152576 x 4096]
+    # bf16, 1.25 GB (beyond the MALL, so every call streams it from HBM), widths 1 and 8
+    n, k = 152576, 4096
+    wl = (torch.randn((n, k), device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
+    lproj = rt.bind_bf16_device(wl, n, k)
+    for width in (1, 8):
+        x = torch.randn((width, k), dtype=torch.float32, device="cuda")
+        y = torch.empty((width, n), dtype=torch.float32, device="cuda")
+        alg = n * k * 2 + width * k * 4 + width * n * 4
+        us, sp = _time_calls(torch, rt, lambda i, st: rt.bf16_linear_device(lproj, x, width, y, stream=st),
+                             max(calls // 4, 20))
+        out[f"bf16_lm_head_w{width}"] = {"algorithmic_bytes": alg, "us": round(us, 2),
+                                         "GB/s": round(alg / (us * 1e-6) / 1e9, 1), "spread_us": sp}
+    del lproj, wl
     out.update(dense_mlp_legs(torch, rt, P, WL, (P.MODE_A, P.MODE_B), calls))
     return out
 

@@ -91,6 +91,30 @@ def test_o_proj_shape(rt, rows):
     assert normwise(got32, ref) <= BF16_OUT
 
 
+@pytest.mark.parametrize("rows", [1, 8])
+def test_lm_head_shape(rt, rows):
+    """The LM head the reference runs through the same wide linear (src/text_endpoint.rs:5673-5705):
+    [152576 x 4096] bf16 weights (1.25 GB, generated on the device), every output row computed and
+    2048 of them, spread over the matrix and including its last 64-row group, checked against the
+    f64 sum and the oracle."""
+    import torch
+    vocab, hidden = 152576, 4096
+    gen = torch.Generator(device="cuda").manual_seed(60 + rows)
+    wt = (torch.randn((vocab, hidden), generator=gen, device="cuda") * 0.02).to(torch.bfloat16).view(torch.int16)
+    rng = np.random.default_rng(61 + rows)
+    x = rng.standard_normal((rows, hidden)).astype(np.float32)
+    proj = rt.bind_bf16_device(wt, vocab, hidden)
+    got = _device(torch, rt, proj, x, rows, P.DTYPE_F32_RAW)
+    got32 = _device(torch, rt, proj, x, rows, P.DTYPE_F32)
+    pick = np.unique(np.concatenate([np.linspace(0, vocab - 1, 1984).astype(np.int64), np.arange(vocab - 64, vocab)]))
+    w = wt[torch.from_numpy(pick).cuda()].cpu().numpy().view(np.uint16)
+    exact = x.astype(np.float64) @ (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64).T
+    assert normwise(got[:, pick], exact) <= RAW_TOL
+    ref, _ = O.bf16_linear(w, x, raw=True)
+    assert normwise(got32[:, pick], ref) <= BF16_OUT
+    assert np.all(np.isfinite(got))
+
+
 def test_closed_form_exact_outputs(rt):
     """Weights and inputs that are small powers of two: every sum is exact in any order, so the
     device output equals the oracle's bit for bit."""
