@@ -4,11 +4,11 @@
 // kernels/block_fp8_gemv.metal:358-397, then bf16_round_in_place :219-232) and its CPU twin
 // bf16_linear (src/text_endpoint.rs:3347-3380: decode the bf16 tensor, SGEMM, round).
 //
-// Work item: (64 weight rows, one K split of KC = BPW * 128 columns). Four waves of 16 rows; every
-// lane issues all of its weight loads at once (16 bytes = 8 bf16 per instruction, one row per
-// lane, 64 contiguous bytes of each of 16 rows per instruction), so a wave keeps 16 KB in flight
-// at BPW = 4. The activation rows of the K split go straight into LDS (direct-to-LDS loads) and
-// are shared by the four waves. Activations are bf16 planes (f32 inputs arrive as three exact
+// Work item: (64 or 128 weight rows, one K split of KC = BPW * 128 columns). Four or eight waves
+// of 16 rows; every lane issues all of its weight loads at once (16 bytes = 8 bf16 per
+// instruction, one row per lane, 64 contiguous bytes of each of 16 rows per instruction), so a
+// wave keeps 16 KB in flight at BPW = 4. The activation rows of the K split go straight into LDS
+// (direct-to-LDS loads) and are shared by the workgroup's waves. Activations are bf16 planes (f32 inputs arrive as three exact
 // planes), so v_mfma_f32_16x16x32_bf16 forms exact products and accumulates in f32; only the f32
 // summation order differs from the reference's. Split-K partials go to a buffer and
 // bf16_reduce_kernel adds them in split order 0..KS-1 (deterministic), then rounds to bf16.
@@ -17,8 +17,8 @@
 
 namespace pw {
 
-template <int NS, int NT, int BPW>
-__global__ __launch_bounds__(256) void bf16_split_kernel(const Bf16Args a)
+template <int NS, int NT, int BPW, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void bf16_split_kernel(const Bf16Args a)
 {
     extern __shared__ uint4 lds_x[];  // [NS * W][KC / 8 + 1] 16-byte units
     constexpr uint32_t KC = BPW * 128, UNITS = KC / 8, STRIDE = UNITS + 1;
@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void bf16_split_kernel(const Bf16Args a)
     const uint32_t s = blockIdx.x % a.KS, g = blockIdx.x / a.KS;
     const uint32_t K = a.K, R = a.R, W = a.W;
     const uint32_t k0 = s * KC;
-    const uint32_t row_base = g * 64 + wave * 16;
+    const uint32_t row_base = g * (16 * WAVES) + wave * 16;
     // rows past R (a partial last group) load the last row: in-bounds reads whose outputs are dropped
     const uint32_t row = row_base + r16 < R ? row_base + r16 : R - 1;
 
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void bf16_split_kernel(const Bf16Args a)
             wv[j][c] = load_global16(wrow + j * 128 + c * 32);
 
     // 2. the activation rows of this K split -> LDS [plane][token][KC/8 + 1], fully unrolled and
-    //    dealt round-robin to the four waves
+    //    dealt round-robin to the waves
 #pragma unroll
     for (uint32_t t = 0; t < 16u * NT; ++t) {
         if (t < W) {
@@ -51,7 +51,7 @@ __global__ __launch_bounds__(256) void bf16_split_kernel(const Bf16Args a)
             for (uint32_t p = 0; p < (uint32_t)NS; ++p)
 #pragma unroll
                 for (uint32_t c = 0; c < CPR; ++c)
-                    if (((t * NS + p) * CPR + c) % 4 == (uint32_t)wave && (uint32_t)lane < LANES)
+                    if (((t * NS + p) * CPR + c) % WAVES == (uint32_t)wave && (uint32_t)lane < LANES)
                         lds_load16(a.x + p * a.x_plane + (size_t)t * K + k0 + (c * 64 + lane) * 8,
                                    lds_x + (p * W + t) * STRIDE + c * 64);
         }
@@ -145,17 +145,29 @@ int bf16_blocks_per_wave(uint32_t K, int planes, uint32_t W, size_t lds_cap)
     return 1;
 }
 
+template <int NS, int NT, int WAVES>
+static void launch_bf16_waves(const Bf16Args &a, int bpw, hipStream_t stream)
+{
+    const dim3 grid(((a.R + 16 * WAVES - 1) / (16 * WAVES)) * a.KS), block(64 * WAVES);
+    const size_t lds = (size_t)NS * a.W * (bpw * 16 + 1) * 16;
+    if (bpw == 4)
+        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 4, WAVES>), grid, block, lds, stream, a);
+    else if (bpw == 2)
+        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 2, WAVES>), grid, block, lds, stream, a);
+    else
+        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 1, WAVES>), grid, block, lds, stream, a);
+}
+
+// Projections of many rows (the LM head) take 128 rows per workgroup, so one staged copy of the
+// activations feeds twice the weight rows; smaller ones (o_proj) keep 64 rows and twice the
+// workgroups.
 template <int NS, int NT>
 static void launch_bf16_nt(const Bf16Args &a, int bpw, hipStream_t stream)
 {
-    const dim3 grid(((a.R + 63) / 64) * a.KS), block(256);
-    const size_t lds = (size_t)NS * a.W * (bpw * 16 + 1) * 16;
-    if (bpw == 4)
-        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 4>), grid, block, lds, stream, a);
-    else if (bpw == 2)
-        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 2>), grid, block, lds, stream, a);
+    if (a.R >= 16384)
+        launch_bf16_waves<NS, NT, 8>(a, bpw, stream);
     else
-        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 1>), grid, block, lds, stream, a);
+        launch_bf16_waves<NS, NT, 4>(a, bpw, stream);
 }
 
 void launch_bf16_linear(const Bf16Args &a, int planes, int bpw, float *y32, uint16_t *y16, uint32_t round_f32,
