@@ -376,9 +376,9 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t v)
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
 }
 
-// Inclusive prefix sum over the wave (lane l: v_0 + ... + v_l) by DPP moves: shifts by 1, 2, 4, 8
-// within each 16-lane row, then the totals of rows 0 and 2 (lanes 15 and 47) into rows 1 and 3 and
-// the total of rows 0-1 (lane 31) into rows 2 and 3.
+// Inclusive prefix sum over the wave (every lane active; lane l: v_0 + ... + v_l) by DPP moves:
+// shifts by 1, 2, 4, 8 within each 16-lane row, then the totals of rows 0 and 2 (lanes 15 and 47)
+// into rows 1 and 3 and the total of rows 0-1 (lane 31) into rows 2 and 3.
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v)
 {
     v += dpp_u32<0x111, 0xf>(v);  // row_shr:1
@@ -390,7 +390,8 @@ __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v)
     return v;
 }
 
-// The wave's maximum, as a scalar: within each 16-lane row by DPP swaps, then the four rows' maxima.
+// The wave's maximum (every lane active), as a scalar: within each 16-lane row by DPP swaps, then
+// the four rows' maxima.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
     v = max(v, dpp_u32<0xb1, 0xf>(v));   // quad_perm [1, 0, 3, 2]
