@@ -17,7 +17,10 @@
 
 namespace pw {
 
-template <int NS, int NT, int BPW, int WAVES>
+// XF32: the activations arrive as f32 rows (a.xf, W <= 16): each thread loads its share of the
+// K split's columns before the weights, and once those older loads are in, splits them into the
+// three planes in LDS while the weights are still on their way (no separate split launch).
+template <int NS, int NT, int BPW, int WAVES, bool XF32 = false>
 __global__ __launch_bounds__(64 * WAVES) void bf16_split_kernel(const Bf16Args a)
 {
     extern __shared__ uint4 lds_x[];  // [NS * W][KC / 8 + 1] 16-byte units
@@ -33,6 +36,21 @@ __global__ __launch_bounds__(64 * WAVES) void bf16_split_kernel(const Bf16Args a
     // rows past R (a partial last group) load the last row: in-bounds reads whose outputs are dropped
     const uint32_t row = row_base + r16 < R ? row_base + r16 : R - 1;
 
+    // 0. (XF32) this thread's f32 activation units (8 columns each) of the K split, rows past W
+    //    rereading row W - 1
+    constexpr uint32_t XU = XF32 ? (16 * UNITS + 64 * WAVES - 1) / (64 * WAVES) : 1;
+    float4 xr[XU][2];
+    if constexpr (XF32) {
+        static_assert(NS == 3 && NT == 1, "f32 rows split into three planes, at most 16 rows");
+#pragma unroll
+        for (uint32_t i = 0; i < XU; ++i) {
+            const uint32_t u = (uint32_t)tid + i * 64 * WAVES, t = u / UNITS, c = u % UNITS;
+            const float *src = a.xf + (size_t)(t < W ? t : W - 1) * K + k0 + c * 8;
+            xr[i][0] = *(const float4 *)src;
+            xr[i][1] = *(const float4 *)(src + 4);
+        }
+    }
+
     // 1. every weight byte of this wave's 16 rows and K split, in flight at once
     const uint16_t *wrow = a.w + (size_t)row * K + k0 + q * 8;
     uint4 wv[BPW][4];
@@ -42,18 +60,44 @@ __global__ __launch_bounds__(64 * WAVES) void bf16_split_kernel(const Bf16Args a
         for (int c = 0; c < 4; ++c)
             wv[j][c] = load_global16(wrow + j * 128 + c * 32);
 
-    // 2. the activation rows of this K split -> LDS [plane][token][KC/8 + 1], fully unrolled and
-    //    dealt round-robin to the waves
+    // 2. the activation rows of this K split -> LDS [plane][token][KC/8 + 1]: the f32 units split
+    //    into their planes (their loads were issued before the weights', so the split waits only
+    //    for them), or the bf16 planes copied straight into LDS, fully unrolled and dealt
+    //    round-robin to the waves
+    if constexpr (XF32) {
 #pragma unroll
-    for (uint32_t t = 0; t < 16u * NT; ++t) {
-        if (t < W) {
+        for (uint32_t i = 0; i < XU; ++i) {
+            const uint32_t u = (uint32_t)tid + i * 64 * WAVES, t = u / UNITS, c = u % UNITS;
+            if (t < W) {
+                const float v[8] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w,
+                                    xr[i][1].x, xr[i][1].y, xr[i][1].z, xr[i][1].w};
+                uint32_t pk[3][4];
 #pragma unroll
-            for (uint32_t p = 0; p < (uint32_t)NS; ++p)
+                for (int e = 0; e < 4; ++e) {
+                    uint16_t h0, m0, l0, h1, m1, l1;
+                    split3_bf16(v[2 * e], h0, m0, l0);
+                    split3_bf16(v[2 * e + 1], h1, m1, l1);
+                    pk[0][e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    pk[1][e] = (uint32_t)m0 | ((uint32_t)m1 << 16);
+                    pk[2][e] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+                }
 #pragma unroll
-                for (uint32_t c = 0; c < CPR; ++c)
-                    if (((t * NS + p) * CPR + c) % WAVES == (uint32_t)wave && (uint32_t)lane < LANES)
-                        lds_load16(a.x + p * a.x_plane + (size_t)t * K + k0 + (c * 64 + lane) * 8,
-                                   lds_x + (p * W + t) * STRIDE + c * 64);
+                for (uint32_t p = 0; p < 3; ++p)
+                    lds_x[(p * W + t) * STRIDE + c] = make_uint4(pk[p][0], pk[p][1], pk[p][2], pk[p][3]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t t = 0; t < 16u * NT; ++t) {
+            if (t < W) {
+#pragma unroll
+                for (uint32_t p = 0; p < (uint32_t)NS; ++p)
+#pragma unroll
+                    for (uint32_t c = 0; c < CPR; ++c)
+                        if (((t * NS + p) * CPR + c) % WAVES == (uint32_t)wave && (uint32_t)lane < LANES)
+                            lds_load16(a.x + p * a.x_plane + (size_t)t * K + k0 + (c * 64 + lane) * 8,
+                                       lds_x + (p * W + t) * STRIDE + c * 64);
+            }
         }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -145,36 +189,38 @@ int bf16_blocks_per_wave(uint32_t K, int planes, uint32_t W, size_t lds_cap)
     return 1;
 }
 
-template <int NS, int NT, int WAVES>
+template <int NS, int NT, int WAVES, bool XF32 = false>
 static void launch_bf16_waves(const Bf16Args &a, int bpw, hipStream_t stream)
 {
     const dim3 grid(((a.R + 16 * WAVES - 1) / (16 * WAVES)) * a.KS), block(64 * WAVES);
     const size_t lds = (size_t)NS * a.W * (bpw * 16 + 1) * 16;
     if (bpw == 4)
-        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 4, WAVES>), grid, block, lds, stream, a);
+        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 4, WAVES, XF32>), grid, block, lds, stream, a);
     else if (bpw == 2)
-        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 2, WAVES>), grid, block, lds, stream, a);
+        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 2, WAVES, XF32>), grid, block, lds, stream, a);
     else
-        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 1, WAVES>), grid, block, lds, stream, a);
+        hipLaunchKernelGGL((bf16_split_kernel<NS, NT, 1, WAVES, XF32>), grid, block, lds, stream, a);
 }
 
 // Projections of many rows (the LM head) take 128 rows per workgroup, so one staged copy of the
 // activations feeds twice the weight rows; smaller ones (o_proj) keep 64 rows and twice the
 // workgroups.
-template <int NS, int NT>
+template <int NS, int NT, bool XF32 = false>
 static void launch_bf16_nt(const Bf16Args &a, int bpw, hipStream_t stream)
 {
     if (a.R >= 16384)
-        launch_bf16_waves<NS, NT, 8>(a, bpw, stream);
+        launch_bf16_waves<NS, NT, 8, XF32>(a, bpw, stream);
     else
-        launch_bf16_waves<NS, NT, 4>(a, bpw, stream);
+        launch_bf16_waves<NS, NT, 4, XF32>(a, bpw, stream);
 }
 
 void launch_bf16_linear(const Bf16Args &a, int planes, int bpw, float *y32, uint16_t *y16, uint32_t round_f32,
                         uint32_t *flags, hipStream_t stream)
 {
     const int t = timer_begin(K_BF16_LINEAR, stream);
-    if (planes == 3) {
+    if (a.xf) {
+        launch_bf16_nt<3, 1, true>(a, bpw, stream);  // the caller keeps a.xf to W <= 16
+    } else if (planes == 3) {
         if (a.W > 16) launch_bf16_nt<3, 2>(a, bpw, stream); else launch_bf16_nt<3, 1>(a, bpw, stream);
     } else {
         if (a.W > 16) launch_bf16_nt<1, 2>(a, bpw, stream); else launch_bf16_nt<1, 1>(a, bpw, stream);

@@ -140,6 +140,7 @@ void launch_moe_a_split(int mats, int ns, int nt, const SplitArgs &args, const S
 struct Bf16Args {
     const uint16_t *w;
     const uint16_t *x;
+    const float *xf;  // f32 activations [W][K], W <= 16, split into the three planes while staging (x unused)
     size_t x_plane;
     uint32_t K, R, W, KS;
     float *partial;

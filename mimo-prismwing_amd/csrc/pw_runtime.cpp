@@ -973,7 +973,10 @@ static int enqueue_bf16_linear(pw_runtime *rt, const void *x, bool x_f32, uint32
 {
     const int planes = x_f32 ? 3 : 1;
     const uint16_t *xp = (const uint16_t *)x;
-    if (x_f32) {
+    // f32 rows: up to 16 are split into their planes inside the projection's staging; more go
+    // through a split launch first
+    const bool split_inside = x_f32 && rows <= 16;
+    if (x_f32 && !split_inside) {
         const size_t n = (size_t)rows * p->columns;
         PW_HIP(rt->lin_planes.ensure(3 * n * 2));
         pw::launch_split_planes((const float *)x, (uint32_t)n, (uint16_t *)rt->lin_planes.p, stream);
@@ -983,6 +986,7 @@ static int enqueue_bf16_linear(pw_runtime *rt, const void *x, bool x_f32, uint32
     pw::Bf16Args a{};
     a.w = (const uint16_t *)p->w;
     a.x = xp;
+    a.xf = split_inside ? (const float *)x : nullptr;
     a.x_plane = (size_t)rows * p->columns;
     a.K = p->columns;
     a.R = p->rows;
