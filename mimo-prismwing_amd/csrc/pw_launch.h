@@ -215,6 +215,12 @@ void launch_linear_a(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x,
                      uint32_t W, uint32_t K, float *y32, uint16_t *y16, uint32_t N,
                      uint32_t round_f32, hipStream_t stream);
 void launch_split_planes(const float *x, uint32_t n, uint16_t *planes, hipStream_t stream);
+// Mode A on f32 activation rows [W][K]: one row is split into its planes inside the projection's
+// staging; more rows (or a split whose stage would not fit) go through launch_split_planes into
+// `scratch` ([3][W][K] bf16) first.
+void launch_linear_a_f32(const ProjTile *tiles, uint32_t n_tiles, const float *xf, uint16_t *scratch, uint32_t W,
+                         uint32_t K, float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32,
+                         hipStream_t stream);
 void launch_linear_b(const ProjTile *tiles, uint32_t n_tiles, const uint8_t *codes,
                      const float *scales, uint32_t W, uint32_t K, float *y32, uint16_t *y16,
                      uint32_t N, uint32_t round_f32, hipStream_t stream);

@@ -36,12 +36,16 @@ struct Acc {
 // loads in the in-order memory counter, so block j's MFMAs start when block j's weights arrive. The
 // unstaged form reads the activations from global memory inside the MFMA loop, after every weight
 // load of the round, so each round's first MFMA also waits for those reads.
-template <int NS, int KSPLIT, int NT, int BPW, bool STAGE>
+// XF32 (staged, NS = 3, one row): the row arrives as f32 (xf) instead of planes; each lane loads
+// its 8-column units of the wave's columns before the weights and, once the weights are issued,
+// splits them into the three planes in the wave's LDS region (no separate split launch).
+template <int NS, int KSPLIT, int NT, int BPW, bool STAGE, bool XF32 = false>
 __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
     const ProjTile *__restrict__ tiles, uint32_t n_tiles, const uint16_t *__restrict__ x, uint32_t W,
     uint32_t K, float *__restrict__ y_f32, uint16_t *__restrict__ y_bf16, uint32_t N,
-    uint32_t round_f32)
+    uint32_t round_f32, const float *__restrict__ xf)
 {
+    static_assert(!XF32 || (STAGE && NS == 3 && NT == 1), "f32 rows are split while staging");
     const size_t plane = (size_t)W * K;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -67,10 +71,22 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
             const uint32_t b0 = round + (uint32_t)wave * BPW;
             // whole rounds: this wave issues exactly 2 BPW weight loads after its copies
             const bool whole = b0 + BPW <= blocks;
-            if constexpr (STAGE) {
-                // the wave's columns [128 b0, 128 (b0 + BPW)) of every activation row (whole blocks
-                // only; a partial round copies the blocks it has)
-                const uint32_t units = (b0 < blocks ? (blocks - b0 < (uint32_t)BPW ? blocks - b0 : BPW) : 0) * 16;
+            // the wave's columns [128 b0, 128 (b0 + BPW)) of every activation row (whole blocks
+            // only; a partial round copies the blocks it has)
+            const uint32_t units = (b0 < blocks ? (blocks - b0 < (uint32_t)BPW ? blocks - b0 : BPW) : 0) * 16;
+            constexpr uint32_t XU = XF32 ? (UNITS + 63) / 64 : 1;  // XF32: f32 units per lane
+            float4 xr[XU][2];
+            if constexpr (XF32) {
+                if (units) {
+#pragma unroll
+                    for (uint32_t i = 0; i < XU; ++i) {
+                        const uint32_t u = (uint32_t)lane + 64 * i, uc = u < units ? u : units - 1;
+                        const float *src = xf + ((size_t)b0 << 7) + uc * 8;
+                        xr[i][0] = *(const float4 *)src;
+                        xr[i][1] = *(const float4 *)(src + 4);
+                    }
+                }
+            } else if constexpr (STAGE) {
                 for (uint32_t s = 0; s < (uint32_t)NS; ++s)
                     for (uint32_t t = 0; t < W; ++t)
                         for (uint32_t u0 = 0; u0 < units; u0 += 64)
@@ -95,7 +111,32 @@ __global__ __launch_bounds__(64 * KSPLIT) void linear_a_kernel(
                     sc[j] = tile.s[b];
                 }
             }
-            if constexpr (STAGE) {
+            if constexpr (XF32) {
+                // the row's units split into the planes of the wave's region (plane p at p * ROW)
+                if (units) {
+#pragma unroll
+                    for (uint32_t i = 0; i < XU; ++i) {
+                        const uint32_t u = (uint32_t)lane + 64 * i;
+                        if (u < units) {
+                            const float v[8] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w,
+                                                xr[i][1].x, xr[i][1].y, xr[i][1].z, xr[i][1].w};
+                            uint32_t pk[3][4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                uint16_t h0, m0, l0, h1, m1, l1;
+                                split3_bf16(v[2 * e], h0, m0, l0);
+                                split3_bf16(v[2 * e + 1], h1, m1, l1);
+                                pk[0][e] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                                pk[1][e] = (uint32_t)m0 | ((uint32_t)m1 << 16);
+                                pk[2][e] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+                            }
+#pragma unroll
+                            for (uint32_t pl = 0; pl < 3; ++pl)
+                                xs[pl * ROW + u] = make_uint4(pk[pl][0], pk[pl][1], pk[pl][2], pk[pl][3]);
+                        }
+                    }
+                }
+            } else if constexpr (STAGE) {
                 // every load but this wave's youngest 2 BPW weight loads: its copies have landed
                 if (whole)
                     wait_vmcnt<2 * BPW>();
@@ -537,14 +578,14 @@ static void launch_a_split(const ProjTile *tiles, uint32_t n_tiles, const uint16
             (void)hipFuncSetAttribute((const void *)linear_a_kernel<NS, KSPLIT, 1, BPW, true>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW, true>), dim3(grid), dim3(64 * KSPLIT), lds, stream,
-                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32, nullptr);
     }
     else if (KSPLIT == 16 || W <= 16)
         hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 1, BPW, false>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
-                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32, nullptr);
     else if constexpr (KSPLIT < 16)
         hipLaunchKernelGGL((linear_a_kernel<NS, KSPLIT, 2, BPW, false>), dim3(grid), dim3(64 * KSPLIT), 0, stream,
-                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32);
+                           tiles, n_tiles, x, W, K, y32, y16, N, round_f32, nullptr);
 }
 
 template <int NS>
@@ -587,6 +628,49 @@ void launch_linear_a(const ProjTile *tiles, uint32_t n_tiles, const uint16_t *x,
     else
         launch_a_planes<1>(tiles, n_tiles, x, W, K, y32, y16, N, round_f32, stream);
     timer_end(t, stream);
+}
+
+template <int KSPLIT, int BPW>
+static void launch_a_xf32(const ProjTile *tiles, uint32_t n_tiles, const float *xf, uint32_t K, float *y32,
+                          uint16_t *y16, uint32_t N, uint32_t round_f32, hipStream_t stream)
+{
+    const size_t lds = staged_lds(3, KSPLIT, BPW, 1);
+    if (lds > 48 * 1024)
+        (void)hipFuncSetAttribute((const void *)linear_a_kernel<3, KSPLIT, 1, BPW, true, true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((linear_a_kernel<3, KSPLIT, 1, BPW, true, true>), dim3(grid_for(n_tiles, 65535)),
+                       dim3(64 * KSPLIT), lds, stream, tiles, n_tiles, nullptr, 1u, K, y32, y16, N, round_f32, xf);
+}
+
+void launch_linear_a_f32(const ProjTile *tiles, uint32_t n_tiles, const float *xf, uint16_t *scratch, uint32_t W,
+                         uint32_t K, float *y32, uint16_t *y16, uint32_t N, uint32_t round_f32,
+                         hipStream_t stream)
+{
+    if (W == 1) {
+        // the split the planes would take (one row: never the paired form), staged if it fits
+        const LinearSplit sp = pick_split(K >> 7, 1, n_tiles);
+        // (sixteen waves of eight blocks never fit the stage, and are not instantiated)
+        if (!(sp.ks == 16 && sp.bpw == 8) &&
+            staged_lds(3, sp.ks, sp.bpw, 1) + sizeof(f32x4) * sp.ks * 64 <= LINEAR_STAGE_LDS) {
+            const int t = timer_begin(K_LINEAR_A, stream);
+#define PW_X(KS, BPW) launch_a_xf32<KS, BPW>(tiles, n_tiles, xf, K, y32, y16, N, round_f32, stream)
+#define PW_X_BPW(KS)                                                                                       \
+    do {                                                                                                   \
+        if (sp.bpw == 8) PW_X(KS, 8); else if (sp.bpw == 4) PW_X(KS, 4); else if (sp.bpw == 2) PW_X(KS, 2); \
+        else PW_X(KS, 1);                                                                                  \
+    } while (0)
+            if (sp.ks == 16) {
+                if (sp.bpw == 4) PW_X(16, 4); else if (sp.bpw == 2) PW_X(16, 2); else PW_X(16, 1);
+            } else if (sp.ks == 8) PW_X_BPW(8); else if (sp.ks == 4) PW_X_BPW(4);
+            else if (sp.ks == 2) PW_X_BPW(2); else PW_X_BPW(1);
+#undef PW_X_BPW
+#undef PW_X
+            timer_end(t, stream);
+            return;
+        }
+    }
+    launch_split_planes(xf, W * K, scratch, stream);
+    launch_linear_a(tiles, n_tiles, scratch, 3, W, K, y32, y16, N, round_f32, stream);
 }
 
 template <int KSPLIT, int BPW>

@@ -825,15 +825,15 @@ static int enqueue_linear(pw_runtime *rt, uint32_t mode, const void *x, bool x_f
                           hipStream_t stream)
 {
     if (mode == PW_MODE_A) {
-        const uint16_t *planes = (const uint16_t *)x;
         if (x_f32) {
             const size_t n = (size_t)rows * p->columns;
             PW_HIP(rt->lin_planes.ensure(3 * n * 2));
-            pw::launch_split_planes((const float *)x, (uint32_t)n, (uint16_t *)rt->lin_planes.p, stream);
-            planes = (const uint16_t *)rt->lin_planes.p;
+            pw::launch_linear_a_f32(p->tiles, p->n_tiles, (const float *)x, (uint16_t *)rt->lin_planes.p, rows,
+                                    p->columns, y32, y16, p->rows, round_f32, stream);
+        } else {
+            pw::launch_linear_a(p->tiles, p->n_tiles, (const uint16_t *)x, 1, rows, p->columns, y32, y16,
+                                p->rows, round_f32, stream);
         }
-        pw::launch_linear_a(p->tiles, p->n_tiles, planes, x_f32 ? 3 : 1, rows, p->columns, y32, y16,
-                            p->rows, round_f32, stream);
     } else if (mode == PW_MODE_B) {
         PW_HIP(rt->codes.ensure((size_t)rows * p->columns));
         PW_HIP(rt->scales.ensure((size_t)rows * (p->columns / 128) * 4));

@@ -100,6 +100,24 @@ def test_mode_a_matches_oracle(rt, rows, x_kind):
     assert within_bf16_cond(host, bf16_round(ref), condition(w, s, x))
 
 
+@pytest.mark.parametrize("n,k", [(200, 512), (2048, 4096)])
+def test_mode_a_f32_row_split_in_staging(rt, n, k):
+    """One f32 row is split into its bf16 planes inside the projection's staging; two rows go
+    through the separate split launch. The same row alone and as both rows of a pair gives the same
+    raw f32 bits."""
+    rng = np.random.default_rng(n + k)
+    s = log_uniform_scales(rng, n, k)
+    w = fp8_weight(rng, n, k, s)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    proj = rt.bind_projection(w, s)
+    one = run_device(rt, proj, x, x_dtype=P.DTYPE_F32)
+    two = run_device(rt, proj, np.concatenate([x, x]), x_dtype=P.DTYPE_F32)
+    assert np.array_equal(one[0].view(np.uint32), two[0].view(np.uint32))
+    assert np.array_equal(one[0].view(np.uint32), two[1].view(np.uint32))
+    # the f32 summation order against the oracle's: 2e-6 at K = 512, more room at K = 4096
+    assert normwise(one, O.gemm_mode_a(w, s, x)) <= (2e-6 if k <= 512 else 1e-5)
+
+
 def test_real_checkpoint_gemv_fixture(rt, golden_dir):
     with open(os.path.join(golden_dir, "mtp-gate-fp8-gemv.json")) as f:
         fx = json.load(f)
