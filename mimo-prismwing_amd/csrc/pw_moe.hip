@@ -1517,9 +1517,12 @@ void launch_moe_layer(uint32_t mode, const ExpertPtrs *bank, const MoeBuffers &m
     if (!eo.y)
         return;  // the one-token down wrote the combined output
     const uint32_t n4 = rows * (H >> 2);
+    // a short batch (up to 256 workgroups of 256) spreads its gather over twice the CUs with
+    // 128-thread workgroups: 8 tokens of 4096 columns take 64 of them
+    const uint32_t cb = n4 <= 65536u ? 128u : 256u;
     const int t = timer_begin(K_MOE_COMBINE, stream);
 #define PW_COMBINE(KS)                                                                                         \
-    hipLaunchKernelGGL((moe_combine_kernel<KS>), dim3((n4 + 255) / 256), dim3(256), 0, stream, eo.y, eo.ks, \
+    hipLaunchKernelGGL((moe_combine_kernel<KS>), dim3((n4 + cb - 1) / cb), dim3(cb), 0, stream, eo.y, eo.ks, \
                        eo.stride, mb.placement_w, mb.row_slots, rows, H, mb.plan, out_f32, out_bf16, raw ? 1u : 0u, \
                        flags)
     switch (eo.ks) {
