@@ -1366,8 +1366,9 @@ static ExpertOut launch_a_moe(const MoeBuffers &mb, const void *x, bool x_f32, u
     da.K = I;
     da.R = H;
     da.rows = placements;
-    // down in pieces: a four-row LDS stage (25 KB at hidden 4096) fits five workgroups per CU
-    // instead of three at eight rows
+    // down in pieces: a four-row LDS stage (25 KB at hidden 4096) leaves the kernel's 98 VGPRs
+    // (four waves per SIMD) to set its occupancy, four workgroups per CU instead of three at eight
+    // rows
     if (pieces) {
         da.active = mb.pieces;
         da.cap = PIECE_ROWS;
